@@ -1,0 +1,166 @@
+// One MoE block on the device: workspace layout and the stage sequence
+//   rmsnorm -> router logits -> router top-k -> dispatch -> expert gate/up -> expert down
+//   -> combine,
+// i.e. GLM4MoeExecutor._moe_mlp_block (offload_runtime/executors/glm4_moe.py:176-240) and
+// Qwen3NextExecutor._moe_mlp_block (offload_runtime/executors/qwen3_next.py:273-333).
+// Everything runs on the caller's stream out of the caller's workspace; nothing is
+// allocated here.
+#include "mx_common.h"
+#include "mx_internal.h"
+
+namespace {
+
+struct Carve {
+  char* base;
+  size_t off = 0;
+  void* take(size_t n) {
+    off = mx_align_up(off, 256);
+    void* p = base ? base + off : nullptr;
+    off += n;
+    return p;
+  }
+};
+
+int check_desc(const MxMoeDesc* d) {
+  if (!d) return MX_ERR_INVALID;
+  if (d->hidden <= 0 || d->inter <= 0 || d->shared_inter < 0 || d->n_experts <= 0)
+    return MX_ERR_INVALID;
+  if (d->top_k < 1 || d->top_k > d->n_experts || d->top_k > 32) return MX_ERR_INVALID;
+  if (d->router_mode < 0 || d->router_mode > 2) return MX_ERR_INVALID;
+  if (d->param_dtype != MX_DT_F32 && d->param_dtype != MX_DT_F16) return MX_ERR_INVALID;
+  if (d->weight_dtype != MX_DT_F32 && d->weight_dtype != MX_DT_F16 && d->weight_dtype != MX_DT_I8)
+    return MX_ERR_INVALID;
+  if (d->has_shared_gate && d->shared_inter == 0) return MX_ERR_INVALID;
+  if (d->n_experts > 1024) return MX_ERR_UNSUPPORTED;
+  if (d->hidden % 4) return MX_ERR_UNSUPPORTED;
+  return MX_OK;
+}
+
+int layout(const MxMoeDesc* d, int T, void* ws, MxMoeViews* v, size_t* total) {
+  MX_TRY(check_desc(d));
+  if (T < 0) return MX_ERR_INVALID;
+  const int Tn = T > 0 ? T : 1;
+  const size_t H = d->hidden, E = d->n_experts, k = d->top_k;
+  const int e1 = d->n_experts + (d->has_shared_gate ? 1 : 0);
+  const int has_sh = d->shared_inter > 0;
+  const int S = mx_router_splits_for(Tn, d->hidden, e1);
+  const int m_blk = mx_m_blk_for(Tn, d->weight_dtype);
+  const size_t P = (size_t)Tn * k;
+  const size_t R = P + (has_sh ? Tn : 0);
+  const size_t imax = d->inter > d->shared_inter ? d->inter : d->shared_inter;
+  const size_t mtmax = mx_max_mtiles(Tn, d->top_k, d->n_experts, has_sh, m_blk);
+  const size_t aesz = d->weight_dtype == MX_DT_F32 ? 4 : 2;
+  Carve c{(char*)ws};
+  MxMoeViews t;
+  t.h32 = (float*)c.take((size_t)Tn * H * 4);
+  t.h16 = d->weight_dtype == MX_DT_F32 ? nullptr : c.take((size_t)Tn * H * 2);
+  t.logits = (float*)c.take((size_t)S * Tn * e1 * 4);
+  t.router_splits = S;
+  t.topk_ids = (int32_t*)c.take(P * 4);
+  t.topk_w = (float*)c.take(P * 4);
+  t.shared_w = (float*)c.take((size_t)Tn * 4);
+  t.counts = (int32_t*)c.take(E * 4);
+  t.offsets = (int32_t*)c.take((E + 1) * 4);
+  t.sorted_tok = (int32_t*)c.take(R * 4);
+  t.sorted_w = (float*)c.take(R * 4);
+  t.pair_pos = (int32_t*)c.take(P * 4);
+  t.g_expert = (int32_t*)c.take((E + 1) * 4);
+  t.g_start = (int32_t*)c.take((E + 1) * 4);
+  t.g_count = (int32_t*)c.take((E + 1) * 4);
+  t.n_groups = (int32_t*)c.take(4);
+  t.mt_group = (int32_t*)c.take(mtmax * 4);
+  t.mt_row0 = (int32_t*)c.take(mtmax * 4);
+  t.n_mtiles = (int32_t*)c.take(4);
+  t.m_blk = m_blk;
+  t.act = c.take(R * imax * aesz);
+  t.y = (float*)c.take(R * H * 4);
+  if (v) *v = t;
+  if (total) *total = mx_align_up(c.off, 256);
+  return MX_OK;
+}
+
+int run_stage(int stage, const MxMoeDesc* d, const MxMoeWeights* w, const float* x, float* out,
+              int T, const MxMoeViews& v, hipStream_t s) {
+  const int has_sh = d->shared_inter > 0;
+  switch (stage) {
+    case 0:
+      return mx_rmsnorm(x, w->norm_w, d->param_dtype, d->eps, T, d->hidden, v.h32, v.h16, s);
+    case 1:
+      return mx_router_logits(v.h32, w->router_w, d->has_shared_gate ? w->shared_gate_w : nullptr,
+                              d->param_dtype, T, d->hidden, d->n_experts, v.router_splits,
+                              v.logits, s);
+    case 2:
+      return mx_router_topk(v.logits, v.router_splits, d->has_bias ? w->bias : nullptr,
+                            d->param_dtype, T, d->n_experts, d->top_k, d->router_mode,
+                            d->norm_topk_prob, d->routed_scaling, d->has_shared_gate, v.topk_ids,
+                            v.topk_w, v.shared_w, s);
+    case 3:
+      return mx_dispatch(v.topk_ids, v.topk_w, v.shared_w, T, d->top_k, d->n_experts, has_sh,
+                         v.m_blk, v.counts, v.offsets, v.sorted_tok, v.sorted_w, v.pair_pos,
+                         v.g_expert, v.g_start, v.g_count, v.n_groups, v.mt_group, v.mt_row0,
+                         v.n_mtiles, s);
+    case 4:
+      return mx_expert_gate_up(d, w->experts, T,
+                               d->weight_dtype == MX_DT_F32 ? (const void*)v.h32 : v.h16,
+                               v.sorted_tok, v.g_expert, v.g_start, v.g_count, v.mt_group,
+                               v.mt_row0, v.n_mtiles, v.m_blk, v.act, s);
+    case 5:
+      return mx_expert_down(d, w->experts, T, v.act, v.sorted_w, v.g_expert, v.g_start, v.g_count,
+                            v.mt_group, v.mt_row0, v.n_mtiles, v.m_blk, v.y, s);
+    case 6:
+      return mx_combine(x, v.y, v.pair_pos, T, d->hidden, d->top_k, has_sh, out, s);
+    default:
+      return MX_ERR_INVALID;
+  }
+}
+
+int forward(const MxMoeDesc* d, const MxMoeWeights* w, const float* x, float* out, int T, void* ws,
+            size_t ws_bytes, hipStream_t s, void* const* events) {
+  MX_TRY(check_desc(d));
+  if (!w || !x || !out || !ws || T < 0) return MX_ERR_INVALID;
+  if (!w->norm_w || !w->router_w || !w->experts) return MX_ERR_INVALID;
+  if (d->has_bias && !w->bias) return MX_ERR_INVALID;
+  if (d->has_shared_gate && !w->shared_gate_w) return MX_ERR_INVALID;
+  if (T == 0) return MX_OK;
+  MxMoeViews v;
+  size_t need = 0;
+  MX_TRY(layout(d, T, ws, &v, &need));
+  if (ws_bytes < need) return MX_ERR_WORKSPACE;
+  for (int st = 0; st < MX_N_STAGES; ++st) {
+    if (events) MX_TRY(mx_status(hipEventRecord((hipEvent_t)events[st], s)));
+    MX_TRY(run_stage(st, d, w, x, out, T, v, s));
+  }
+  if (events) MX_TRY(mx_status(hipEventRecord((hipEvent_t)events[MX_N_STAGES], s)));
+  return MX_OK;
+}
+
+}  // namespace
+
+extern "C" int mx_moe_workspace_size(const MxMoeDesc* desc, int32_t tokens, size_t* nbytes) {
+  if (!nbytes) return MX_ERR_INVALID;
+  return layout(desc, tokens, nullptr, nullptr, nbytes);
+}
+
+extern "C" int mx_moe_views(const MxMoeDesc* desc, int32_t tokens, void* workspace,
+                            MxMoeViews* views) {
+  if (!workspace || !views) return MX_ERR_INVALID;
+  return layout(desc, tokens, workspace, views, nullptr);
+}
+
+extern "C" int mx_moe_forward(const MxMoeDesc* desc, const MxMoeWeights* weights, const float* x,
+                              float* out, int32_t tokens, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  return forward(desc, weights, x, out, tokens, workspace, workspace_bytes, (hipStream_t)stream,
+                 nullptr);
+}
+
+extern "C" int mx_moe_forward_profiled(const MxMoeDesc* desc, const MxMoeWeights* weights,
+                                       const float* x, float* out, int32_t tokens, void* workspace,
+                                       size_t workspace_bytes, void* stream, void* const* events,
+                                       int32_t n_events) {
+  if (!events || n_events != MX_N_STAGES + 1) return MX_ERR_INVALID;
+  for (int i = 0; i < n_events; ++i)
+    if (!events[i]) return MX_ERR_INVALID;
+  return forward(desc, weights, x, out, tokens, workspace, workspace_bytes, (hipStream_t)stream,
+                 events);
+}

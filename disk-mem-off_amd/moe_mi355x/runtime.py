@@ -1,0 +1,318 @@
+"""Layer-offload runtime with host->device transfers issued ahead of compute.
+
+API and metrics of offload_runtime/runtime.py:15-198 (``LayerExecutor``, ``LayerMetrics``,
+``RuntimeMetrics``, ``OffloadRuntime.run_inference``): storage wait -> optional host
+dequantisation -> pinned staging -> device buffer (pool) -> H2D on the transfer stream ->
+event -> ``run_layer`` on the compute stream -> release -> next storage prefetch.
+
+Difference in scheduling: the reference enqueues the copy of layer i immediately before
+computing layer i, so copies never overlap compute.  Here the copies of layers
+i+1 .. i+transfer_lookahead are enqueued on the transfer stream *before* layer i runs on
+the compute stream (``transfer_lookahead`` defaults to the scheduler's ``lookahead``;
+0 restores the reference order).  Buffer hazards are fenced with events: a device buffer
+goes back to the pool together with the event that marks the end of its compute, and the
+next copy into it waits on that event on the transfer stream; a pinned staging buffer is
+reused only after the event of its copy has completed.
+"""
+from __future__ import annotations
+
+import time
+from collections import deque
+from dataclasses import dataclass, field
+from typing import Any, Protocol
+
+from .backends import DeviceBackend
+from .buffer_pool import DeviceBufferPool, PinnedHostBufferPool
+from .scheduler import PrefetchScheduler
+from .storage import LayerStorage
+from .types import DeviceBuffer, HostBuffer, LayerSpec
+
+
+class LayerExecutor(Protocol):
+    """Executes one layer using device weights already copied to the device."""
+
+    def run_layer(self, layer: LayerSpec, activations: Any, device_weights: DeviceBuffer,
+                  backend: DeviceBackend, stream: Any) -> Any: ...
+
+
+@dataclass
+class LayerMetrics:
+    layer_id: int
+    h2d_ms: float = 0.0          # host time to enqueue the copy (reference meaning)
+    compute_ms: float = 0.0      # host wall time of run_layer
+    stall_ms: float = 0.0
+    disk_read_ms: float = 0.0
+    nbytes: int = 0
+    compressed_nbytes: int = 0
+    h2d_gpu_ms: float = 0.0      # event-timed copy on the transfer stream (GPU backends)
+    compute_gpu_ms: float = 0.0  # event-timed run_layer work on the compute stream
+
+
+@dataclass
+class RuntimeMetrics:
+    transferred_bytes: int = 0
+    compressed_bytes: int = 0
+    transfer_seconds: float = 0.0
+    compute_seconds: float = 0.0
+    layer_count: int = 0
+    end_to_end_seconds: float = 0.0
+    layer_metrics: list[LayerMetrics] = field(default_factory=list)
+    transfer_gpu_seconds: float = 0.0
+    compute_gpu_seconds: float = 0.0
+    device_seconds: float = 0.0  # event-timed first copy start -> last compute end
+
+    @property
+    def effective_bandwidth_gbps(self) -> float:
+        if self.transfer_seconds <= 0:
+            return 0.0
+        return (self.transferred_bytes / 1e9) / self.transfer_seconds
+
+    @property
+    def overlap_ratio(self) -> float:
+        """1 - e2e / (transfer + compute), the reference formula (runtime.py:56-61)."""
+        total = self.transfer_seconds + self.compute_seconds
+        if total <= 0 or self.end_to_end_seconds <= 0:
+            return 0.0
+        return 1.0 - (self.end_to_end_seconds / total)
+
+    @property
+    def gpu_transfer_bandwidth_gbps(self) -> float:
+        if self.transfer_gpu_seconds <= 0:
+            return 0.0
+        return (self.transferred_bytes / 1e9) / self.transfer_gpu_seconds
+
+    @property
+    def gpu_overlap_ratio(self) -> float:
+        """Same formula on event-timed device intervals."""
+        total = self.transfer_gpu_seconds + self.compute_gpu_seconds
+        if total <= 0 or self.device_seconds <= 0:
+            return 0.0
+        return 1.0 - (self.device_seconds / total)
+
+
+@dataclass
+class _Inflight:
+    index: int
+    layer: LayerSpec
+    lm: LayerMetrics
+    host: HostBuffer
+    staged: HostBuffer
+    device: DeviceBuffer
+    copied: Any  # event recorded after the copy on the transfer stream
+    t_start: Any = None  # timing events (GPU backends)
+    t_end: Any = None
+
+
+class OffloadRuntime:
+    def __init__(
+        self,
+        layers: list[LayerSpec],
+        backend: DeviceBackend,
+        storage: LayerStorage,
+        scheduler: PrefetchScheduler,
+        executor: LayerExecutor,
+        use_buffer_pool: bool = False,
+        use_pinned_staging: bool = False,
+        dequantizer: Any | None = None,
+        transfer_lookahead: int | None = None,
+    ) -> None:
+        self.layers = {layer.layer_id: layer for layer in layers}
+        self.backend = backend
+        self.storage = storage
+        self.scheduler = scheduler
+        self.executor = executor
+        self.transfer_stream = backend.create_stream("transfer")
+        self.compute_stream = backend.create_stream("compute")
+        self._pool = DeviceBufferPool(backend) if use_buffer_pool else None
+        self._pinned_pool: PinnedHostBufferPool | None = None
+        if use_pinned_staging and backend.supports_pinned_host:
+            self._pinned_pool = PinnedHostBufferPool(backend)
+        self.dequantizer = dequantizer
+        if transfer_lookahead is None:
+            transfer_lookahead = int(getattr(scheduler, "lookahead", 0))
+        if transfer_lookahead < 0:
+            raise ValueError("transfer_lookahead must be >= 0")
+        self.transfer_lookahead = transfer_lookahead
+        self._timing = hasattr(backend, "create_timing_event")
+        self._deferred_free: list[tuple[DeviceBuffer, Any]] = []
+
+    def __enter__(self) -> "OffloadRuntime":
+        return self
+
+    def __exit__(self, exc_type: Any, exc_val: Any, exc_tb: Any) -> None:
+        self.close()
+
+    def close(self) -> None:
+        self.backend.synchronize_stream(self.transfer_stream)
+        self.backend.synchronize_stream(self.compute_stream)
+        self._flush_deferred(force=True)
+        if self._pinned_pool is not None:
+            self._pinned_pool.drain()
+        if self._pool is not None:
+            self._pool.drain()
+        self.backend.destroy_stream(self.transfer_stream)
+        self.backend.destroy_stream(self.compute_stream)
+
+    # -- buffers --
+    def _alloc_device(self, nbytes: int) -> DeviceBuffer:
+        if self._pool is not None:
+            buf = self._pool.acquire(nbytes)
+            ev = self._pool.last_event
+            if ev is not None:
+                # The previous user of this buffer must finish before the copy lands.
+                self.backend.wait_event(self.transfer_stream, ev)
+                self.backend.destroy_event(ev)
+            return buf
+        return self.backend.alloc_device(nbytes)
+
+    def _free_device(self, buf: DeviceBuffer, done_event: Any) -> None:
+        if self._pool is not None:
+            self._pool.release(buf, done_event)
+        elif done_event is None:
+            self.backend.free_device(buf)
+        else:
+            self._deferred_free.append((buf, done_event))
+
+    def _flush_deferred(self, force: bool = False) -> None:
+        keep = []
+        for buf, ev in self._deferred_free:
+            if force or self._event_done(ev):
+                self.backend.destroy_event(ev)
+                self.backend.free_device(buf)
+            else:
+                keep.append((buf, ev))
+        self._deferred_free = keep
+
+    def _event_done(self, ev: Any) -> bool:
+        query = getattr(self.backend, "event_done", None)
+        return True if query is None else bool(query(ev))
+
+    def _stage_pinned(self, host_weights: HostBuffer) -> HostBuffer:
+        if self._pinned_pool is None or host_weights.pinned:
+            return host_weights
+        pinned = self._pinned_pool.acquire(host_weights.nbytes)
+        pinned.view[: host_weights.nbytes] = host_weights.view[: host_weights.nbytes]
+        return pinned
+
+    def _wait_copy(self, rec: _Inflight) -> None:
+        sync = getattr(self.backend, "event_synchronize", None)
+        if sync is not None:
+            sync(rec.copied)
+
+    # -- one layer's transfer --
+    def _issue(self, index: int, layer_id: int, metrics: RuntimeMetrics) -> _Inflight:
+        layer = self.layers[layer_id]
+        lm = LayerMetrics(layer_id=layer_id)
+        t_stall = time.perf_counter()
+        self.storage.wait(layer_id)
+        host = self.storage.get(layer_id)
+        lm.stall_ms = (time.perf_counter() - t_stall) * 1000
+        if hasattr(self.storage, "get_disk_read_ms"):
+            lm.disk_read_ms = self.storage.get_disk_read_ms(layer_id)
+        if self.dequantizer is not None and self.dequantizer.needs_dequantize(layer):
+            compressed = host.nbytes
+            host = self.dequantizer.dequantize(layer, host)
+            lm.compressed_nbytes = compressed
+            metrics.compressed_bytes += compressed
+        nbytes = host.nbytes
+        staged = self._stage_pinned(host)
+        device = self._alloc_device(nbytes)
+        t0 = time.perf_counter()
+        t_start = t_end = None
+        if self._timing:
+            t_start = self.backend.create_timing_event()
+            self.backend.record(t_start, self.transfer_stream)
+        self.backend.copy_h2d_async(device, staged, self.transfer_stream)
+        if self._timing:
+            t_end = self.backend.create_timing_event()
+            self.backend.record(t_end, self.transfer_stream)
+        copied = self.backend.record_event(self.transfer_stream)
+        elapsed = time.perf_counter() - t0
+        lm.h2d_ms = elapsed * 1000
+        lm.nbytes = nbytes
+        metrics.transfer_seconds += elapsed
+        metrics.transferred_bytes += nbytes
+        return _Inflight(index, layer, lm, host, staged, device, copied, t_start, t_end)
+
+    def run_inference(self, ordered_layer_ids: list[int], inputs: Any) -> tuple[Any, RuntimeMetrics]:
+        unknown = [lid for lid in ordered_layer_ids if lid not in self.layers]
+        if unknown:
+            raise ValueError(f"Unknown layer IDs: {unknown}")
+        metrics = RuntimeMetrics(layer_count=len(ordered_layer_ids))
+        activations = inputs
+        wall_start = time.perf_counter()
+        for layer_id in self.scheduler.warmup_prefetch_ids(ordered_layer_ids):
+            self.storage.request(layer_id)
+
+        inflight: deque[_Inflight] = deque()
+        timings: list[tuple[LayerMetrics, Any, Any, Any, Any]] = []
+        n = len(ordered_layer_ids)
+        next_issue = 0
+        try:
+            for index, layer_id in enumerate(ordered_layer_ids):
+                last = min(n - 1, index + self.transfer_lookahead)
+                while next_issue <= last:
+                    inflight.append(self._issue(next_issue, ordered_layer_ids[next_issue], metrics))
+                    next_issue += 1
+                rec = inflight.popleft()
+                self.backend.wait_event(self.compute_stream, rec.copied)
+
+                c_start = c_end = None
+                if self._timing:
+                    c_start = self.backend.create_timing_event()
+                    self.backend.record(c_start, self.compute_stream)
+                t1 = time.perf_counter()
+                activations = self.executor.run_layer(
+                    layer=rec.layer,
+                    activations=activations,
+                    device_weights=rec.device,
+                    backend=self.backend,
+                    stream=self.compute_stream,
+                )
+                compute_elapsed = time.perf_counter() - t1
+                if self._timing:
+                    c_end = self.backend.create_timing_event()
+                    self.backend.record(c_end, self.compute_stream)
+                rec.lm.compute_ms = compute_elapsed * 1000
+                metrics.compute_seconds += compute_elapsed
+
+                done = self.backend.record_event(self.compute_stream) if self._timing else None
+                self._free_device(rec.device, done)
+                self.storage.release(layer_id)
+                if rec.staged is not rec.host and self._pinned_pool is not None:
+                    self._wait_copy(rec)
+                    self._pinned_pool.release(rec.staged)
+                self.backend.destroy_event(rec.copied)
+                timings.append((rec.lm, rec.t_start, rec.t_end, c_start, c_end))
+                metrics.layer_metrics.append(rec.lm)
+                self._flush_deferred()
+
+                next_layer_id = self.scheduler.next_prefetch_id(ordered_layer_ids, index)
+                if next_layer_id is not None:
+                    self.storage.request(next_layer_id)
+        finally:
+            while inflight:
+                rec = inflight.popleft()
+                self.backend.synchronize_stream(self.transfer_stream)
+                self._free_device(rec.device, None)
+                if rec.staged is not rec.host and self._pinned_pool is not None:
+                    self._pinned_pool.release(rec.staged)
+                self.backend.destroy_event(rec.copied)
+            self.backend.synchronize_stream(self.transfer_stream)
+            self.backend.synchronize_stream(self.compute_stream)
+            self._flush_deferred(force=True)
+
+        metrics.end_to_end_seconds = time.perf_counter() - wall_start
+        if self._timing and timings:
+            first = None
+            for lm, hs, he, cs, ce in timings:
+                lm.h2d_gpu_ms = self.backend.elapsed_ms(hs, he)
+                lm.compute_gpu_ms = self.backend.elapsed_ms(cs, ce)
+                metrics.transfer_gpu_seconds += lm.h2d_gpu_ms / 1000
+                metrics.compute_gpu_seconds += lm.compute_gpu_ms / 1000
+                first = hs if first is None else first
+            metrics.device_seconds = self.backend.elapsed_ms(first, timings[-1][4]) / 1000
+            for _, hs, he, cs, ce in timings:
+                for ev in (hs, he, cs, ce):
+                    self.backend.destroy_event(ev)
+        return activations, metrics

@@ -1,0 +1,101 @@
+"""Synthetic MoE layers and activations (seeded, reproducible, shape-faithful).
+
+Every tensor draws from its own counter-based stream (``gen.normal``) keyed by
+``(seed, crc32(name))``, so a layer can be produced on the host (NumPy) or directly on
+the device (``mx_fill_normal``) with the same values.  Distributions follow the
+benchmark workloads: activations ~ N(0, 1), weights ~ N(0, 0.02), correction bias
+~ N(0, 0.01), RMSNorm weight 1 (or 1 + N(0, 0.1) with ``norm_noise``).
+"""
+from __future__ import annotations
+
+import zlib
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import gen
+
+GLM = "glm4_moe"
+QWEN = "qwen3_next"
+
+
+def stream_of(name: str) -> int:
+    return zlib.crc32(name.encode())
+
+
+@dataclass(frozen=True)
+class MoeShape:
+    arch: str
+    hidden: int
+    n_experts: int
+    top_k: int
+    inter: int
+    shared_inter: int
+    routed_scaling: float
+    eps: float
+    has_bias: bool = True
+    has_shared_gate: bool = False
+
+    def config(self) -> dict:
+        """HF-style config dict with the keys the executors read."""
+        cfg = {"hidden_size": self.hidden, "num_experts_per_tok": self.top_k,
+               "moe_intermediate_size": self.inter, "norm_topk_prob": True,
+               "rms_norm_eps": self.eps, "num_attention_heads": 1}
+        if self.arch == GLM:
+            cfg.update({"architectures": ["Glm4MoeForCausalLM"], "n_routed_experts": self.n_experts,
+                        "routed_scaling_factor": self.routed_scaling, "n_shared_experts": 1,
+                        "intermediate_size": self.inter})
+        else:
+            cfg.update({"architectures": ["Qwen3NextForCausalLM"], "num_experts": self.n_experts,
+                        "shared_expert_intermediate_size": self.shared_inter})
+        return cfg
+
+
+# Workload shapes (hidden, experts, top-k, moe_intermediate, shared intermediate).
+C1 = MoeShape(GLM, 1024, 16, 4, 256, 256, 2.5, 1e-5)
+GLM47 = MoeShape(GLM, 5120, 160, 8, 1536, 1536, 2.5, 1e-5)
+QWEN3_NEXT = MoeShape(QWEN, 2048, 512, 10, 512, 512, 1.0, 1e-6, has_bias=False,
+                      has_shared_gate=True)
+
+
+def tensor_specs(shape: MoeShape) -> list[tuple[str, tuple[int, ...], str, float]]:
+    """(name, shape, kind, std) for every MoE tensor; kind is 'norm', 'normal' or 'bias'."""
+    H, E, I, Is = shape.hidden, shape.n_experts, shape.inter, shape.shared_inter
+    specs = [("post_attention_layernorm.weight", (H,), "norm", 0.0),
+             ("mlp.gate.weight", (E, H), "normal", 0.02)]
+    if shape.has_bias:
+        specs.append(("mlp.gate.e_score_correction_bias", (E,), "bias", 0.01))
+    for e in range(E):
+        specs += [(f"mlp.experts.{e}.gate_proj.weight", (I, H), "normal", 0.02),
+                  (f"mlp.experts.{e}.up_proj.weight", (I, H), "normal", 0.02),
+                  (f"mlp.experts.{e}.down_proj.weight", (H, I), "normal", 0.02)]
+    if Is:
+        pre = "mlp.shared_experts." if shape.arch == GLM else "mlp.shared_expert."
+        specs += [(pre + "gate_proj.weight", (Is, H), "normal", 0.02),
+                  (pre + "up_proj.weight", (Is, H), "normal", 0.02),
+                  (pre + "down_proj.weight", (H, Is), "normal", 0.02)]
+        if shape.has_shared_gate:
+            specs.append(("mlp.shared_expert_gate.weight", (1, H), "normal", 0.02))
+    return specs
+
+
+def make_tensors(shape: MoeShape, seed: int, weight_dtype=np.float32, param_dtype=np.float32,
+                 norm_noise: float = 0.0) -> dict[str, np.ndarray]:
+    """All MoE tensors of one layer on the host.  Expert weights in ``weight_dtype``
+    (float32 / float16), router, bias, norm and shared gate in ``param_dtype``."""
+    out = {}
+    for name, shp, kind, std in tensor_specs(shape):
+        if kind == "norm":
+            v = np.ones(shp, dtype=np.float32)
+            if norm_noise:
+                v = v + gen.normal(seed, stream_of(name), shp, std=norm_noise)
+        else:
+            v = gen.normal(seed, stream_of(name), shp, std=std)
+        is_expert = name.startswith(("mlp.experts.", "mlp.shared_experts.", "mlp.shared_expert."))
+        dt = weight_dtype if is_expert else param_dtype
+        out[name] = v.astype(dt)
+    return out
+
+
+def make_inputs(seed: int, tokens: int, hidden: int) -> np.ndarray:
+    return gen.normal(seed, stream_of("x"), (tokens, hidden), std=1.0)

@@ -1,0 +1,252 @@
+/*
+ * moe_mi355x.h — C ABI of libmoe_mi355x.so, the MI355X (gfx950) MoE-layer hot path.
+ *
+ * Every entry point returns int: 0 on success, a positive hipError_t code when a HIP
+ * runtime call failed, or a negative MX_ERR_* code for argument errors detected on the
+ * host.  No entry point throws across the ABI and no hot-path entry point allocates
+ * device memory: the caller owns every buffer, including the workspace.
+ *
+ * Pointers are plain addresses.  "Device" pointers are hipMalloc'd (or offsets into a
+ * hipMalloc'd layer buffer); streams and events are hipStream_t / hipEvent_t passed as
+ * void*.  A NULL stream is the legacy default stream.
+ *
+ * Reference interfaces replaced (haesookimDev/disk-mem-off):
+ *   backend shim  -> offload_runtime/backends/rocm_backend.py:33-119 (ROCmBackend over hip-python)
+ *   MoE layer     -> offload_runtime/executors/glm4_moe.py:176-240 (GLM4MoeExecutor._moe_mlp_block)
+ *                    offload_runtime/executors/qwen3_next.py:273-333 (Qwen3NextExecutor._moe_mlp_block)
+ */
+#ifndef MOE_MI355X_H
+#define MOE_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------------------ */
+#define MX_OK 0
+#define MX_ERR_INVALID (-1)      /* bad argument: null pointer, bad shape, bad enum        */
+#define MX_ERR_UNSUPPORTED (-2)  /* valid request this build does not implement           */
+#define MX_ERR_WORKSPACE (-3)    /* workspace smaller than mx_moe_workspace_size() says    */
+#define MX_ERR_ALIGNMENT (-4)    /* a weight pointer is not 16-byte aligned                */
+
+/* ---- element types ------------------------------------------------------------------ */
+#define MX_DT_F32 0
+#define MX_DT_F16 1
+#define MX_DT_I8 2 /* expert weights only: int8 values + one fp16 scale per output row */
+
+/* ---- router modes -------------------------------------------------------------------
+ * MX_ROUTER_REF_SOFTMAX_BIAS : p = softmax(h.Wr^T + b); top-k on p; weights = p at the
+ *                              selected ids; optional renorm; x routed_scaling.
+ *                              (glm4_moe.py:181-200, what the reference executes)
+ * MX_ROUTER_SIGMOID_SELECT_BIAS : s = sigmoid(h.Wr^T); top-k on s + b; weights = s at the
+ *                              selected ids (bias for selection only); optional renorm;
+ *                              x routed_scaling.  (GLM-4.5/4.7 checkpoint semantics)
+ * MX_ROUTER_SOFTMAX          : p = softmax(h.Wr^T); top-k on p; optional renorm; no bias.
+ *                              (qwen3_next.py:278-293; pass routed_scaling = 1)
+ * Selected ids come out ordered by descending selection key, ties to the lower id.    */
+#define MX_ROUTER_REF_SOFTMAX_BIAS 0
+#define MX_ROUTER_SIGMOID_SELECT_BIAS 1
+#define MX_ROUTER_SOFTMAX 2
+
+/* Per-expert weight pointers (device addresses).  gate/up are [inter, hidden] and down is
+ * [hidden, inter], nn.Linear row-major ([out, in]) exactly as packed in the layer buffer
+ * (loader/huggingface.py:458-591).  For MX_DT_I8 the *_scale pointers give one fp16 scale
+ * per output row; dequantised W[o, i] = q[o, i] * scale[o] (quantize.py:44 with zero
+ * point 0 and a per-row scale).  For other dtypes the scale pointers are ignored.    */
+typedef struct MxExpertPtrs {
+  const void* gate;
+  const void* up;
+  const void* down;
+  const void* gate_scale;
+  const void* up_scale;
+  const void* down_scale;
+} MxExpertPtrs;
+
+/* Static description of one MoE block.  Field meanings follow the executor config keys
+ * (glm4_moe.py:70-84, qwen3_next.py:105-133).                                         */
+typedef struct MxMoeDesc {
+  int32_t hidden;          /* H                                                        */
+  int32_t inter;           /* I, moe_intermediate_size                                 */
+  int32_t shared_inter;    /* I_s of the shared expert; 0 = no shared expert           */
+  int32_t n_experts;       /* E, routed experts                                        */
+  int32_t top_k;           /* k, num_experts_per_tok (1 <= k <= min(E, 32))             */
+  int32_t router_mode;     /* MX_ROUTER_*                                              */
+  int32_t norm_topk_prob;  /* 1: w /= (sum(w) + 1e-20)                                 */
+  int32_t weight_dtype;    /* expert weights: MX_DT_F32 / MX_DT_F16 / MX_DT_I8         */
+  int32_t param_dtype;     /* norm weight, router weight, bias, shared gate: F32 / F16 */
+  int32_t has_bias;        /* e_score_correction_bias present                          */
+  int32_t has_shared_gate; /* Qwen3-Next shared_expert_gate present                    */
+  float routed_scaling;    /* routed_scaling_factor (1.0 for Qwen3-Next)               */
+  float eps;               /* rms_norm_eps                                             */
+} MxMoeDesc;
+
+/* Device pointers of one layer's MoE tensors. */
+typedef struct MxMoeWeights {
+  const void* norm_w;           /* post_attention_layernorm.weight [H]                 */
+  const void* router_w;         /* mlp.gate.weight [E, H]                              */
+  const void* bias;             /* mlp.gate.e_score_correction_bias [E] or NULL        */
+  const void* shared_gate_w;    /* mlp.shared_expert_gate.weight [1, H] or NULL        */
+  const MxExpertPtrs* experts;  /* device array of E + 1 entries; entry E = shared     */
+} MxMoeWeights;
+
+/* Views into a forward workspace (all device pointers), for inspection after a call. */
+typedef struct MxMoeViews {
+  float* h32;          /* [T, H] rms-normalised activations                             */
+  void* h16;           /* [T, H] fp16 copy (NULL for MX_DT_F32 weights)                 */
+  float* logits;       /* [S, T, E(+1)] router logit partials (S = router_splits)        */
+  int32_t router_splits;
+  int32_t* topk_ids;   /* [T, k]                                                        */
+  float* topk_w;       /* [T, k] routing weights after renorm and scaling              */
+  float* shared_w;     /* [T] shared-expert weight (1, or sigmoid gate)                 */
+  int32_t* counts;     /* [E] tokens per routed expert                                  */
+  int32_t* offsets;    /* [E + 1] exclusive prefix of counts                            */
+  int32_t* sorted_tok; /* [T k + T] token of each expert-sorted row (shared rows last)   */
+  float* sorted_w;     /* [T k + T] routing weight of each row                          */
+  int32_t* pair_pos;   /* [T, k] row of pair (t, j) in the sorted order                 */
+  int32_t* g_expert;   /* [E + 1] expert of group g (group 0 = shared when present)     */
+  int32_t* g_start;    /* [E + 1] first sorted row of group g                           */
+  int32_t* g_count;    /* [E + 1] rows of group g                                       */
+  int32_t* n_groups;   /* [1]                                                           */
+  int32_t* mt_group;   /* [max m-tiles] group of each m-tile                            */
+  int32_t* mt_row0;    /* [max m-tiles] first row of the m-tile within its group        */
+  int32_t* n_mtiles;   /* [1]                                                           */
+  int32_t m_blk;       /* rows per m-tile                                               */
+  void* act;           /* [T k + T, max(I, I_s)] silu(gate) * up                        */
+  float* y;            /* [T k + T, H] weighted expert outputs                          */
+} MxMoeViews;
+
+/* Static description of the device. */
+typedef struct MxDeviceInfo {
+  char name[256];
+  char arch[64];
+  int32_t cu_count;
+  int32_t clock_khz;
+  int32_t mem_clock_khz;
+  int32_t mem_bus_width;
+  int64_t total_mem;
+  int32_t l2_bytes;
+  int32_t lds_per_block;
+} MxDeviceInfo;
+
+/* =================================================================================== *
+ * Backend shim.  Replaces the hip-python calls of ROCmBackend                          *
+ * (offload_runtime/backends/rocm_backend.py:46-119).                                   *
+ * =================================================================================== */
+const char* mx_error_string(int status);                       /* no counterpart: diagnostics */
+int mx_get_device_count(int32_t* count);                       /* no counterpart: probe       */
+int mx_device_info(int32_t device, MxDeviceInfo* info);        /* no counterpart: bench peaks */
+int mx_set_device(int32_t device);                             /* rocm_backend.py:49  hipSetDevice */
+int mx_device_sync(void);                                      /* no counterpart: teardown    */
+int mx_malloc(void** ptr, size_t nbytes);                      /* rocm_backend.py:81-83 hipMalloc */
+int mx_free(void* ptr);                                        /* rocm_backend.py:85-86 hipFree */
+int mx_host_malloc(void** ptr, size_t nbytes);                 /* rocm_backend.py:63-66 hipHostMalloc(n, 0) */
+int mx_host_free(void* ptr);                                   /* rocm_backend.py:68-70 hipHostFree */
+int mx_memcpy_h2d_async(void* dst, const void* src, size_t nbytes, void* stream); /* rocm_backend.py:88-95 */
+int mx_memcpy_d2h_async(void* dst, const void* src, size_t nbytes, void* stream); /* rocm_backend.py:97-104 */
+int mx_memcpy_d2d_async(void* dst, const void* src, size_t nbytes, void* stream); /* no counterpart: device copies */
+int mx_stream_create(void** stream, int32_t nonblocking);      /* rocm_backend.py:72-76 hipStreamCreateWithFlags */
+int mx_stream_destroy(void* stream);                           /* rocm_backend.py:78-79 */
+int mx_stream_sync(void* stream);                              /* rocm_backend.py:118-119 */
+int mx_event_create(void** event, int32_t timing);             /* rocm_backend.py:108 hipEventCreateWithFlags */
+int mx_event_record(void* event, void* stream);                /* rocm_backend.py:109 hipEventRecord */
+int mx_event_wait(void* stream, void* event);                  /* rocm_backend.py:115-116 hipStreamWaitEvent */
+int mx_event_sync(void* event);                                /* no counterpart: host wait   */
+int mx_event_query(void* event, int32_t* done);                /* no counterpart: poll        */
+int mx_event_destroy(void* event);                             /* rocm_backend.py:112-113 */
+int mx_event_elapsed_ms(float* ms, void* start, void* end);    /* no counterpart: timing      */
+
+/* =================================================================================== *
+ * MoE layer.  One call = GLM4MoeExecutor._moe_mlp_block (glm4_moe.py:176-240) or       *
+ * Qwen3NextExecutor._moe_mlp_block (qwen3_next.py:273-333) on device-resident data:    *
+ *   out = x + sum_j w[t,j] * SwiGLU_{id[t,j]}(h[t]) + shared_w[t] * SwiGLU_shared(h[t]) *
+ *   with h = rms_norm(x).  x and out are fp32 [T, H] device buffers (may not alias).    *
+ * =================================================================================== */
+int mx_moe_workspace_size(const MxMoeDesc* desc, int32_t tokens, size_t* nbytes);
+int mx_moe_views(const MxMoeDesc* desc, int32_t tokens, void* workspace, MxMoeViews* views);
+int mx_moe_forward(const MxMoeDesc* desc, const MxMoeWeights* weights, const float* x,
+                   float* out, int32_t tokens, void* workspace, size_t workspace_bytes,
+                   void* stream);
+/* Same as mx_moe_forward, and records events[i] on the stream before stage i and
+ * events[MX_N_STAGES] after the last stage (n_events must be MX_N_STAGES + 1).
+ * Stages: 0 rmsnorm, 1 router logits, 2 router top-k, 3 dispatch, 4 expert gate/up,
+ * 5 expert down, 6 combine.                                                           */
+#define MX_N_STAGES 7
+int mx_moe_forward_profiled(const MxMoeDesc* desc, const MxMoeWeights* weights,
+                            const float* x, float* out, int32_t tokens, void* workspace,
+                            size_t workspace_bytes, void* stream, void* const* events,
+                            int32_t n_events);
+
+/* ---- individual stages (each replaces the reference lines cited) -------------------- */
+
+/* h32 = w * (x / sqrt(mean(x^2) + eps)), optional fp16 copy h16.  _common.py:73-75. */
+int mx_rmsnorm(const float* x, const void* norm_w, int32_t param_dtype, float eps,
+               int32_t tokens, int32_t hidden, float* h32, void* h16, void* stream);
+
+/* Router logit partials: logits[s, t, e] = sum over the s-th slice of H of
+ * h32[t, :] * Wr[e, :], for e < E; e == E (if shared_gate_w) uses the shared gate row.
+ * glm4_moe.py:181, qwen3_next.py:278 and :328.                                        */
+int mx_router_logits(const float* h32, const void* router_w, const void* shared_gate_w,
+                     int32_t param_dtype, int32_t tokens, int32_t hidden, int32_t n_experts,
+                     int32_t splits, float* logits, void* stream);
+
+/* Bias, softmax/sigmoid, top-k, renorm, scaling.  glm4_moe.py:182-200,
+ * qwen3_next.py:279-293; shared_w[t] = sigmoid(gate logit) (qwen3_next.py:327-329) or 1. */
+int mx_router_topk(const float* logits, int32_t splits, const void* bias, int32_t param_dtype,
+                   int32_t tokens, int32_t n_experts, int32_t top_k, int32_t router_mode,
+                   int32_t norm_topk_prob, float routed_scaling, int32_t has_shared_gate,
+                   int32_t* topk_ids, float* topk_w, float* shared_w, void* stream);
+
+/* Histogram / prefix-sum dispatch: per-expert counts and offsets, the expert-sorted row
+ * order (ascending token inside each expert, as h[token_mask] gathers at
+ * glm4_moe.py:206-215), its inverse pair_pos, the active-group table (shared group first
+ * when has_shared) and the m-tile list with m_blk rows per tile.                      */
+int mx_dispatch(const int32_t* topk_ids, const float* topk_w, const float* shared_w,
+                int32_t tokens, int32_t top_k, int32_t n_experts, int32_t has_shared,
+                int32_t m_blk, int32_t* counts, int32_t* offsets, int32_t* sorted_tok,
+                float* sorted_w, int32_t* pair_pos, int32_t* g_expert, int32_t* g_start,
+                int32_t* g_count, int32_t* n_groups, int32_t* mt_group, int32_t* mt_row0,
+                int32_t* n_mtiles, void* stream);
+
+/* Grouped expert products over the dispatch tables (glm4_moe.py:218-224, :234-237):
+ * gate/up: act[row] = silu(A[tok(row)] . Wg^T) * (A[tok(row)] . Wu^T)
+ * down:    y[row]   = sorted_w[row] * (act[row] . Wd^T)
+ * A is h16 (fp16/int8 weights) or h32 (fp32 weights).                                 */
+int mx_expert_gate_up(const MxMoeDesc* desc, const MxExpertPtrs* experts, int32_t tokens,
+                      const void* a, const int32_t* sorted_tok, const int32_t* g_expert,
+                      const int32_t* g_start, const int32_t* g_count, const int32_t* mt_group,
+                      const int32_t* mt_row0, const int32_t* n_mtiles, int32_t m_blk,
+                      void* act, void* stream);
+int mx_expert_down(const MxMoeDesc* desc, const MxExpertPtrs* experts, int32_t tokens,
+                   const void* act, const float* sorted_w, const int32_t* g_expert,
+                   const int32_t* g_start, const int32_t* g_count, const int32_t* mt_group,
+                   const int32_t* mt_row0, const int32_t* n_mtiles, int32_t m_blk, float* y,
+                   void* stream);
+
+/* out[t] = x[t] + sum_j y[pair_pos[t, j]] + (has_shared ? y[T k + t] : 0).
+ * glm4_moe.py:227-231, :238, :240.                                                    */
+int mx_combine(const float* x, const float* y, const int32_t* pair_pos, int32_t tokens,
+               int32_t hidden, int32_t top_k, int32_t has_shared, float* out, void* stream);
+
+/* ---- synthetic data and offline quantisation (bench / loader plumbing) -------------- */
+
+/* dst[i] = std * N_i, i in [0, n), where N_i is normal number (offset + i) of the
+ * counter-based stream (seed, stream_id): SplitMix64 of two counters -> Box-Muller.
+ * dtype MX_DT_F32 or MX_DT_F16.  Matches moe_mi355x/gen.py element for element (up to
+ * one ulp of the libm used for log/cos).                                             */
+int mx_fill_normal(void* dst, int32_t dtype, size_t n, uint64_t seed, uint64_t stream_id,
+                   uint64_t offset, float std, void* stream);
+
+/* Per-row symmetric int8: scale[r] = fp16(max|W[r,:]| / 127) (1 for an all-zero row),
+ * q[r, c] = clamp(rint(W[r, c] / float(scale[r])), -127, 127).  W is fp32 or fp16
+ * [rows, cols] on the device; q int8 [rows, cols]; scale fp16 [rows].                */
+int mx_quantize_rows_i8(const void* w, int32_t w_dtype, int32_t rows, int32_t cols, int8_t* q,
+                        void* scale, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOE_MI355X_H */
