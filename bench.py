@@ -1,0 +1,366 @@
+#!/usr/bin/env python3
+"""MoE-layer benchmark on one MI355X.
+
+Headline: one GLM-4.7-shape MoE block (hidden 5120, 160 routed experts, top-8,
+moe_intermediate 1536, one shared expert of 1536, sigmoid routing with correction bias,
+routed scaling 2.5, renormalised top-k, fp16 expert weights with fp32 accumulation) on a
+decode batch of T tokens (default 32), activations and weights already resident in HBM.
+A "step" is one full block call: rmsnorm -> router -> top-k -> dispatch -> expert gate/up
+-> expert down -> combine.  value = T * steps / (timed seconds), tokens/s.
+
+The timed region is bracketed by HIP events on the stream the kernels run on; each step
+also records events between its stages, which gives the per-kernel averages used for the
+roofline entry (dominant kernel: expert gate/up).  The CPU baseline is the NumPy oracle
+in the reference's loop structure on the same full-size layer (routed experts copied to
+the host), timed on the host cores.  Other BASELINE workloads (decode T=1/8, Zipf
+prefill T=2048, Qwen3-Next T=1/4096, per-row int8 decode T=1/16) are reported under
+"sweep".  Prints ONE JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "disk-mem-off_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+from moe_mi355x import _lib, synthetic as syn  # noqa: E402
+from moe_mi355x.backends import MI355XBackend  # noqa: E402
+from moe_mi355x.device_layer import DeviceMoeLayer  # noqa: E402
+from moe_mi355x.moe import read_device  # noqa: E402
+from moe_mi355x.workloads import (HBM_PEAK, MFMA_F16_PEAK, MFMA_F32_PEAK, call_traffic,  # noqa: E402
+                                  host_router_logits, synthetic_host_params, zipf_bias)
+
+METRIC = "MoE-layer tokens/s at decode (HBM GB/s %peak) and prefill (MFMA %peak), 1 GPU"
+SEED = 2026
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class Case:
+    """One timed workload on a device layer."""
+
+    def __init__(self, backend, stream, layer: DeviceMoeLayer, shape: syn.MoeShape, wdt: str,
+                 tokens: int, mode: int, x: np.ndarray):
+        self.backend, self.stream, self.layer = backend, stream, layer
+        self.shape, self.wdt, self.T = shape, wdt, tokens
+        self.cfg = layer.config(top_k=shape.top_k, router_mode=mode,
+                                routed_scaling=shape.routed_scaling, eps=shape.eps)
+        self.desc = self.cfg.desc()
+        self.weights = layer.prepare(self.cfg, tokens)
+        r = layer.runner
+        self.x_dev = r._io["x"].handle
+        self.out_dev = r._io["out"].handle
+        xh = np.ascontiguousarray(x, dtype=np.float32)
+        backend.copy_h2d_ptr_async(self.x_dev, xh.ctypes.data, xh.nbytes, stream)
+        backend.synchronize_stream(stream)
+
+    def step(self, events=None):
+        self.layer.runner.forward_device(self.desc, self.weights, self.x_dev, self.out_dev,
+                                         self.T, self.stream, events)
+
+    def run(self, steps: int, warmup: int) -> dict:
+        b = self.backend
+        for _ in range(warmup):
+            self.step()
+        b.synchronize_stream(self.stream)
+        ev = [[b.create_timing_event() for _ in range(_lib.MX_N_STAGES + 1)] for _ in range(steps)]
+        start, end = b.create_timing_event(), b.create_timing_event()
+        b.record(start, self.stream)
+        for i in range(steps):
+            self.step(ev[i])
+        b.record(end, self.stream)
+        b.event_synchronize(end)
+        total_ms = b.elapsed_ms(start, end)
+        stage = np.array([[b.elapsed_ms(e[s], e[s + 1]) for s in range(_lib.MX_N_STAGES)]
+                          for e in ev])
+        for e in ev:
+            for x in e:
+                b.destroy_event(x)
+        b.destroy_event(start)
+        b.destroy_event(end)
+        v = self.layer.runner.views(self.desc, self.T)
+        n_groups = int(read_device(b, v.n_groups, np.int32, 1, self.stream)[0])
+        counts = read_device(b, v.counts, np.int32, self.shape.n_experts, self.stream)
+        n_active = n_groups - (1 if self.shape.shared_inter else 0)
+        tr = call_traffic(self.shape, self.wdt, self.T, n_active)
+        ms = total_ms / steps
+        st = stage.mean(axis=0)
+        return {"ms_per_step": ms, "tokens_per_s": self.T / (ms / 1e3), "stage_ms": st,
+                "n_active": n_active, "counts": counts, "traffic": tr,
+                "layer_hbm_frac": tr["layer_bytes"] / (ms / 1e3) / HBM_PEAK,
+                "layer_mfma_frac": tr["layer_flops"] / (ms / 1e3) / MFMA_F16_PEAK}
+
+    def output(self) -> np.ndarray:
+        return read_device(self.backend, self.out_dev, np.float32, self.T * self.shape.hidden,
+                           self.stream).reshape(self.T, -1)
+
+
+def summarize(res: dict, name: str, wdt: str) -> dict:
+    st = res["stage_ms"]
+    tr = res["traffic"]
+    gu_s, dn_s = st[4] / 1e3, st[5] / 1e3
+    peak_flops = MFMA_F32_PEAK if wdt == "float32" else MFMA_F16_PEAK
+    return {
+        "workload": name, "tokens_per_s": round(res["tokens_per_s"], 1),
+        "ms_per_step": round(res["ms_per_step"], 4), "active_experts": res["n_active"],
+        "layer_GBps": round(tr["layer_bytes"] / (res["ms_per_step"] / 1e3) / 1e9, 1),
+        "layer_hbm_frac": round(res["layer_hbm_frac"], 4),
+        "layer_mfma_frac": round(tr["layer_flops"] / (res["ms_per_step"] / 1e3) / peak_flops, 4),
+        "roofline_frac": round(max(tr["layer_bytes"] / HBM_PEAK, tr["layer_flops"] / peak_flops)
+                               / (res["ms_per_step"] / 1e3), 4),
+        "gate_up_ms": round(st[4], 4), "down_ms": round(st[5], 4),
+        "gate_up_hbm_frac": round(tr["gate_up_bytes"] / gu_s / HBM_PEAK, 4),
+        "down_hbm_frac": round(tr["down_bytes"] / dn_s / HBM_PEAK, 4),
+        "gate_up_mfma_frac": round(tr["gate_up_flops"] / gu_s / peak_flops, 4),
+        "stage_ms": {n: round(float(v), 4) for n, v in zip(_lib.STAGE_NAMES, st)},
+    }
+
+
+def cpu_baseline(layer: DeviceMoeLayer, shape: syn.MoeShape, x: np.ndarray, budget_s: float):
+    """Oracle in the reference's loop structure on the host cores (routed experts only are
+    copied to the host; the copy is not timed).  Returns (baseline dict, oracle output)."""
+    from oracle import moe_oracle as orc
+
+    spec = orc.MoeSpec(top_k=shape.top_k, router_mode=orc.SIGMOID_SELECT_BIAS,
+                       norm_topk_prob=True, routed_scaling=shape.routed_scaling, eps=shape.eps)
+    names = ["post_attention_layernorm.weight", "mlp.gate.weight",
+             "mlp.gate.e_score_correction_bias"]
+    t = layer.read_tensors(names)
+    h = orc.rms_norm(x, t[names[0]], spec.eps)
+    ids, _ = orc.route(orc.router_logits(h, t), t[names[2]], spec)
+    experts = sorted(set(ids.ravel().tolist()))
+    wn = [f"mlp.experts.{e}.{p}.weight" for e in experts for p in ("gate_proj", "up_proj", "down_proj")]
+    wn += [f"mlp.shared_experts.{p}.weight" for p in ("gate_proj", "up_proj", "down_proj")]
+    t.update(layer.read_tensors(wn))
+    try:
+        from threadpoolctl import threadpool_info
+        blas = [i for i in threadpool_info() if i.get("user_api") == "blas"]
+        threads = int(blas[0]["num_threads"]) if blas else len(os.sched_getaffinity(0))
+        blas_name = f"{blas[0]['internal_api']} {blas[0].get('version')}" if blas else "unknown"
+    except Exception:  # pragma: no cover - threadpoolctl missing
+        threads, blas_name = len(os.sched_getaffinity(0)), "unknown"
+    out = orc.moe_block_faithful(x, t, spec)  # warm-up, and the full-size parity reference
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 10):
+        t0 = time.perf_counter()
+        orc.moe_block_faithful(x, t, spec)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() > t_end and len(times) >= 1:
+            break
+    med = float(np.median(times))
+    cpu_model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    base = {"value": round(x.shape[0] / med, 3), "unit": "tokens/s", "cores": threads,
+            "kind": "port",
+            "sample": (f"full GLM-4.7-shape layer, {x.shape[0]} tokens, NumPy oracle in the "
+                       f"reference loop structure (per-expert BLAS, per-token scatter), fp16 "
+                       f"weights promoted to fp32; median of {len(times)} runs "
+                       f"({med * 1e3:.1f} ms each) after 1 warm-up; {blas_name}, "
+                       f"{len(os.sched_getaffinity(0))} host cores visible, {cpu_model}, "
+                       f"numpy {np.__version__}")}
+    return base, out, ids
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--tokens", type=int, default=32, help="decode batch of the headline")
+    ap.add_argument("--no-sweep", action="store_true", help="headline only")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", default=None, help="run one sweep workload (profiling)")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run a 1 GiB device copy (HBM counter calibration)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
+              "(the MoE path is single-device; expert-parallel sharding is design-only).",
+              file=sys.stderr)
+        return 2
+
+    backend = MI355XBackend(0)
+    stream = backend.create_stream("bench")
+    info = _lib.MxDeviceInfo()
+    _lib.check(_lib.load().mx_device_info(0, ctypes.byref(info)))
+    log(f"device {info.name.decode()} {info.arch.decode()} CUs={info.cu_count}")
+    G = syn.GLM47
+    sweep: dict[str, dict] = {}
+    result: dict = {}
+    only = args.only
+
+    def want(name: str) -> bool:
+        return only is None or only == name
+
+    # ---- GLM-4.7 fp16 layer -------------------------------------------------------------
+    need_glm = only is None or only.startswith("glm47_fp16")
+    if need_glm:
+        t0 = time.perf_counter()
+        layer = DeviceMoeLayer.synthetic(backend, G, SEED, stream, weight_dtype="float16",
+                                         param_dtype="float32")
+        log(f"GLM-4.7 fp16 layer: {layer.layer.nbytes / 1e9:.2f} GB built on device in "
+            f"{time.perf_counter() - t0:.1f}s")
+        mode = _lib.MX_ROUTER_SIGMOID_SELECT_BIAS
+        if only is None:
+            T = args.tokens
+            x = syn.make_inputs(SEED, T, G.hidden)
+            case = Case(backend, stream, layer, G, "float16", T, mode, x)
+            res = case.run(args.steps, args.warmup)
+            head = summarize(res, f"glm47_fp16_decode_t{T}", "float16")
+            log(f"headline {head['workload']}: {head['tokens_per_s']:.0f} tok/s, "
+                f"{head['ms_per_step']:.3f} ms, layer {head['layer_GBps']} GB/s")
+            gpu_out = case.output()
+            result.update({"head": head, "res": res})
+            if not args.no_cpu:
+                base, ref_out, ref_ids = cpu_baseline(layer, G, x, budget_s=20.0)
+                v = layer.runner.views(case.desc, T)
+                gpu_ids = read_device(backend, v.topk_ids, np.int32, T * G.top_k, stream)
+                result["cpu_baseline"] = base
+                result["parity"] = {
+                    "max_abs_err_vs_oracle": float(np.max(np.abs(gpu_out - ref_out))),
+                    "ids_match": bool(np.array_equal(gpu_ids.reshape(T, -1), ref_ids)),
+                    "tolerance_abs": 2e-2}
+                log(f"cpu baseline {base['value']} tok/s; parity {result['parity']}")
+        if not args.no_sweep:
+            for T in (1, 8, 32):
+                name = f"glm47_fp16_decode_t{T}"
+                if not want(name) or (only is None and T == args.tokens):
+                    continue
+                x = syn.make_inputs(SEED + T, T, G.hidden)
+                r = Case(backend, stream, layer, G, "float16", T, mode, x).run(
+                    min(args.steps, 30), 5)
+                sweep[name] = summarize(r, name, "float16")
+                log(f"{name}: {sweep[name]['tokens_per_s']} tok/s")
+            name = "glm47_fp16_prefill_t2048_zipf"
+            if want(name):
+                T = 2048
+                x = syn.make_inputs(SEED + 1, T, G.hidden)
+                hp = synthetic_host_params(G, SEED)
+                logits = host_router_logits(x, np.ones(G.hidden, np.float32),
+                                            hp["mlp.gate.weight"], G.eps)
+                bias, loads, c = zipf_bias(logits, G.top_k, 1.1, seed=SEED,
+                                           base_bias=hp["mlp.gate.e_score_correction_bias"])
+                off = layer.layout.offset("mlp.gate.e_score_correction_bias")
+                bb = np.ascontiguousarray(bias, np.float32)
+                backend.copy_h2d_ptr_async(layer.buf.handle + off, bb.ctypes.data, bb.nbytes, stream)
+                backend.synchronize_stream(stream)
+                r = Case(backend, stream, layer, G, "float16", T, mode, x).run(
+                    min(args.steps, 20), 3)
+                s = summarize(r, name, "float16")
+                cnt = np.sort(r["counts"])[::-1]
+                s["zipf"] = {"c": c, "max_load": int(cnt[0]), "min_load": int(cnt[-1]),
+                             "median_load": int(np.median(cnt)), "top5": cnt[:5].tolist()}
+                sweep[name] = s
+                log(f"{name}: {s['tokens_per_s']} tok/s, mfma {s['layer_mfma_frac']}")
+        layer.close()
+
+    # ---- GLM-4.7 per-row int8 layer ----------------------------------------------------------
+    if not args.no_sweep and (only is None or only.startswith("glm47_int8")):
+        layer = DeviceMoeLayer.synthetic(backend, G, SEED, stream, weight_dtype="int8",
+                                         param_dtype="float32")
+        for T in (1, 16):
+            name = f"glm47_int8_decode_t{T}"
+            if not want(name):
+                continue
+            x = syn.make_inputs(SEED + T, T, G.hidden)
+            r = Case(backend, stream, layer, G, "int8", T, _lib.MX_ROUTER_SIGMOID_SELECT_BIAS,
+                     x).run(min(args.steps, 30), 5)
+            sweep[name] = summarize(r, name, "int8")
+            log(f"{name}: {sweep[name]['tokens_per_s']} tok/s")
+        layer.close()
+
+    # ---- Qwen3-Next fp16 layer ---------------------------------------------------------------
+    if not args.no_sweep and (only is None or only.startswith("qwen3next")):
+        Q = syn.QWEN3_NEXT
+        layer = DeviceMoeLayer.synthetic(backend, Q, SEED, stream, weight_dtype="float16",
+                                         param_dtype="float32")
+        for T in (1, 4096):
+            name = f"qwen3next_fp16_t{T}"
+            if not want(name):
+                continue
+            x = syn.make_inputs(SEED + T, T, Q.hidden)
+            r = Case(backend, stream, layer, Q, "float16", T, _lib.MX_ROUTER_SOFTMAX, x).run(
+                min(args.steps, 20 if T > 64 else 30), 3)
+            sweep[name] = summarize(r, name, "float16")
+            log(f"{name}: {sweep[name]['tokens_per_s']} tok/s")
+        layer.close()
+
+    if args.calib_copy:
+        n = 1 << 30
+        a, b = backend.alloc_device(n), backend.alloc_device(n)
+        lib = _lib.load()
+        for _ in range(3):
+            _lib.check(lib.mx_memcpy_d2d_async(b.handle, a.handle, n, stream))
+        backend.synchronize_stream(stream)
+        backend.free_device(a)
+        backend.free_device(b)
+        log("calibration copy: 3 x 1 GiB device-to-device")
+
+    backend.destroy_stream(stream)
+    if "head" not in result:
+        print(json.dumps({"metric": METRIC, "partial": True, "sweep": sweep}))
+        return 0
+
+    head, res = result["head"], result["res"]
+    st = res["stage_ms"]
+    gu_bytes = res["traffic"]["gate_up_bytes"]
+    gu_s = st[4] / 1e3
+    line = {
+        "metric": METRIC,
+        "value": head["tokens_per_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (seeded counter-based normals generated on device; "
+                "x~N(0,1), W~N(0,0.02), bias~N(0,0.01))",
+        "config": {"workload": head["workload"], "hidden": G.hidden, "n_experts": G.n_experts,
+                   "top_k": G.top_k, "moe_intermediate": G.inter,
+                   "shared_intermediate": G.shared_inter, "routing": "sigmoid_select_bias",
+                   "routed_scaling": G.routed_scaling, "weights": "fp16",
+                   "tokens": args.tokens, "active_experts": head["active_experts"],
+                   "parallelism": "single-gpu"},
+        "roofline": {"kernel": "k_expert gate/up (fp16 MFMA, fused SiLU*up)", "bound": "hbm",
+                     "achieved": round(gu_bytes / gu_s / 1e9, 1), "peak": HBM_PEAK / 1e9,
+                     "unit": "GB/s", "frac": round(gu_bytes / gu_s / HBM_PEAK, 4),
+                     "traffic": None, "avg_launch_ms": round(st[4], 4),
+                     "bytes_per_launch": int(gu_bytes)},
+        "layer": {k: head[k] for k in ("layer_GBps", "layer_hbm_frac", "layer_mfma_frac",
+                                       "roofline_frac", "stage_ms", "down_hbm_frac")},
+        "cpu_baseline": result.get("cpu_baseline"),
+        "parity": result.get("parity"),
+        "sweep": sweep,
+        "device": {"name": info.name.decode(), "arch": info.arch.decode(), "cus": info.cu_count},
+        "host": platform.node(),
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
