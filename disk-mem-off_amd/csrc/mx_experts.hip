@@ -279,13 +279,260 @@ __global__ __launch_bounds__(256) void k_expert(const ExpertParams p) {
 }
 
 // ------------------------------------------------------------------------------------
+// Prefill regime (m-tiles of 128 rows, fp16 / int8 weights).
+//
+// With many rows per expert the activation tile is reused by every column slab, so it is
+// staged once per block in LDS (double-buffered, rows padded by 16 bytes so the 16-byte
+// fragment reads of 8 consecutive lanes hit distinct banks) and shared by the 4 waves.
+// Weights still go straight from HBM into MFMA B registers; each wave holds 4 B
+// fragments per k-chunk (gate/up: 2 gate + 2 up column blocks; down: 4 column blocks),
+// so every A fragment read from LDS feeds 4 MFMAs.  A stage covers 64 reduction columns.
+//
+// Blocks are numbered so that consecutive logical ids run on the same XCD: hardware
+// block b goes to XCD b % 8, logical id = (b % 8) * (grid / 8) + b / 8.  Logical ids walk
+// the m-tiles of one column slab before moving to the next slab, so the m-tiles of one
+// expert (which read the same weight rows) are co-resident on one XCD and share its L2.
+// ------------------------------------------------------------------------------------
+// Tunables (compile-time; the defaults are the measured best on MI355X).
+//   MX_LDS_ORDER 0: XCD-grouped, column slab major; 1: hardware order; 2: XCD-grouped,
+//                   m-tile major.
+//   MX_LDS_RB:      weight stages in flight per wave (even).
+//   MX_LDS_OCC_F16: blocks per CU the fp16 variant is register-limited to.
+#ifndef MX_LDS_ORDER
+#define MX_LDS_ORDER 0
+#endif
+#ifndef MX_LDS_RB
+#define MX_LDS_RB 4
+#endif
+#ifndef MX_LDS_OCC_F16
+#define MX_LDS_OCC_F16 2
+#endif
+#ifndef MX_LDS_RA
+#define MX_LDS_RA 4
+#endif
+
+// fp16 fits two blocks per CU; the int8 variant (conversion temporaries, 64-column
+// stages) needs the full register file of one block per CU to avoid spills.
+template <int WF, bool GU>
+__global__ __launch_bounds__(256, WF == MX_DT_F16 ? MX_LDS_OCC_F16 : 1) void k_expert_lds(
+    const ExpertParams p, int mt_max, int nblk) {
+  using Tr = WTr<WF>;
+  constexpr int EPL = Tr::EPL, ESZ = Tr::ESZ;
+  constexpr int KS = 4 * EPL;                // reduction columns per stage: 32 fp16, 64 int8
+  constexpr int MT = 8, MB = 128;
+  constexpr int NBI = GU ? 2 : 4;
+  constexpr int NF = GU ? 2 * NBI : NBI;
+  constexpr int AROW = KS * 2 + 16;          // LDS bytes per staged activation row
+  constexpr int ATILE = MB * AROW;
+  constexpr int CPR = KS * 2 / 16;           // 16-byte chunks per row and stage
+  constexpr int ACH = MB * CPR / 256;        // chunks each thread stages
+  constexpr int RB = MX_LDS_RB;              // weight stages in flight per wave
+  constexpr int RA = (WF == MX_DT_F16 && GU) ? MX_LDS_RA : 2;  // activation stages in flight
+  static_assert(RB % RA == 0 && RA % 2 == 0, "ring sizes must divide the unroll");
+  __shared__ __align__(16) char lds[2 * ATILE];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // provably wave-uniform
+  const int b = blockIdx.x;
+#if MX_LDS_ORDER == 1
+  const int logical = b;
+#else
+  const int logical = (b & 7) * (gridDim.x >> 3) + (b >> 3);
+#endif
+#if MX_LDS_ORDER == 2
+  const int mt = logical / nblk;
+  const int nb = logical - mt * nblk;
+#else
+  const int nb = logical / mt_max;
+  const int mt = logical - nb * mt_max;
+#endif
+  if (nb >= nblk || mt >= mt_max || mt >= *p.n_mtiles) return;
+  const int g = p.mt_group[mt];
+  const int row0 = p.mt_row0[mt];
+  const int eid = p.g_expert[g];
+  const int gstart = p.g_start[g];
+  const int gcount = p.g_count[g];
+  const bool sh = eid == p.E;
+  const int N = sh ? p.N_s : p.N_r;
+  const int K = sh ? p.K_s : p.K_r;
+  if (nb * 4 * 16 * NBI >= N) return;  // whole block past this expert's columns
+  const int n0 = (nb * 4 + wave) * 16 * NBI;
+  const bool wact = n0 < N;
+  const int mrows = min(MB, gcount - row0);
+  const int j = lane & 15, q = lane >> 4;
+  const MxExpertPtrs ep = p.experts[eid];
+
+  const uint32_t rowb = (uint32_t)K * ESZ;
+  const uint32_t matb = (uint32_t)N * rowb;
+  const mx_rsrc_t rb0 = mx_rsrc(GU ? ep.gate : ep.down, matb);
+  const mx_rsrc_t rb1 = mx_rsrc(GU ? ep.up : ep.down, matb);
+  uint32_t boff[NBI];
+#pragma unroll
+  for (int f = 0; f < NBI; ++f) {
+    const int n = n0 + 16 * f + j;
+    boff[f] = (wact && n < N) ? (uint32_t)n * rowb + q * EPL * ESZ : MX_OOB;
+  }
+
+  // Activation chunks this thread stages: fixed rows, advancing columns.
+  const mx_rsrc_t ra = mx_rsrc(p.a, p.a_bytes);
+  uint32_t agoff[ACH];
+  int alds[ACH], acol[ACH];
+#pragma unroll
+  for (int i = 0; i < ACH; ++i) {
+    const int c = tid + 256 * i;
+    const int row = c / CPR, cc = c % CPR;
+    acol[i] = cc * 8;
+    alds[i] = row * AROW + cc * 16;
+    if (row < mrows) {
+      const int r = gstart + row0 + row;
+      const int arow = GU ? p.sorted_tok[r] : r;
+      agoff[i] = (uint32_t)arow * (uint32_t)p.lda * 2 + cc * 16;
+    } else {
+      agoff[i] = MX_OOB;
+    }
+  }
+
+  float4_t acc[MT][NF];
+#pragma unroll
+  for (int mi = 0; mi < MT; ++mi)
+#pragma unroll
+    for (int f = 0; f < NF; ++f) acc[mi][f] = (float4_t){0.f, 0.f, 0.f, 0.f};
+
+  auto load_a = [&](int st, int4_t (&ar)[ACH]) {
+    const int k0 = st * KS;
+#pragma unroll
+    for (int i = 0; i < ACH; ++i)
+      ar[i] = mx_ld16(ra, (k0 + acol[i] < K) ? agoff[i] + (uint32_t)k0 * 2 : MX_OOB);
+  };
+  auto load_b = [&](int st, int4_t (&br)[NF]) {
+    const bool kin = st * KS + q * EPL < K;
+    const uint32_t kb = (uint32_t)st * KS * ESZ;
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      const int fi = GU ? (f % NBI) : f;
+      br[f] = mx_ld16((GU && f >= NBI) ? rb1 : rb0, kin ? boff[fi] + kb : MX_OOB);
+    }
+  };
+  auto store_a = [&](int buf, const int4_t (&ar)[ACH]) {
+    char* base = lds + buf * ATILE;
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) *(int4_t*)(base + alds[i]) = ar[i];
+  };
+  auto compute = [&](int buf, const int4_t (&br)[NF]) {
+    const char* base = lds + buf * ATILE;
+    if constexpr (WF == MX_DT_F16) {
+#pragma unroll
+      for (int mi = 0; mi < MT; ++mi) {
+        const int4_t a = *(const int4_t*)(base + (16 * mi + j) * AROW + q * 16);
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+          acc[mi][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              __builtin_bit_cast(half8_t, a), __builtin_bit_cast(half8_t, br[f]), acc[mi][f],
+              0, 0, 0);
+      }
+    } else {
+      half8_t blo[NF], bhi[NF];
+#pragma unroll
+      for (int f = 0; f < NF; ++f) mx_i8_to_f16(br[f], blo[f], bhi[f]);
+#pragma unroll
+      for (int mi = 0; mi < MT; ++mi) {
+        const char* ap = base + (16 * mi + j) * AROW + q * 32;
+        const int4_t a0 = *(const int4_t*)ap;
+        const int4_t a1 = *(const int4_t*)(ap + 16);
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+          acc[mi][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a0),
+                                                              blo[f], acc[mi][f], 0, 0, 0);
+          acc[mi][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a1),
+                                                              bhi[f], acc[mi][f], 0, 0, 0);
+        }
+      }
+    }
+  };
+
+  // Software pipeline: stage s computes from LDS buffer s % 2 and weight set s % RB while
+  // the activations of stages s + 1 .. s + RA and the weights of stages s + 1 .. s + RB - 1
+  // are in flight; the activations of stage s + 1 go to LDS at the end of stage s.  The
+  // global latency is hidden by the ring depths, not by the LDS double buffer.  The loop
+  // body is branch-free so the in-order load counter is never drained: stages past the
+  // end of K read zeros through the descriptors' bounds check and the stage count is
+  // padded to a multiple of RB (a multiple of RA), which also makes every register-set
+  // index static.  A wave without columns (edge of a narrower shared expert) has
+  // out-of-range weight offsets, computes zeros and skips the epilogue.
+  const int nst = (K + KS - 1) / KS;
+  const int nst_pad = (nst + RB - 1) / RB * RB;
+  int4_t aring[RA][ACH];
+  int4_t bring[RB][NF];
+#pragma unroll
+  for (int u = 0; u < RA; ++u) load_a(u, aring[u]);
+#pragma unroll
+  for (int u = 0; u < RB - 1; ++u) load_b(u, bring[u]);
+  store_a(0, aring[0]);
+  __syncthreads();
+  for (int s0 = 0; s0 < nst_pad; s0 += RB) {
+#pragma unroll
+    for (int u = 0; u < RB; ++u) {
+      const int s = s0 + u;
+      load_b(s + RB - 1, bring[(u + RB - 1) % RB]);
+      compute(u % 2, bring[u]);
+      store_a((u + 1) % 2, aring[(u + 1) % RA]);
+      load_a(s + RA, aring[u % RA]);
+      __syncthreads();
+    }
+  }
+  if (!wact) return;
+
+  if constexpr (GU) {
+#pragma unroll
+    for (int f = 0; f < NBI; ++f) {
+      const int n = n0 + 16 * f + j;
+      if (n >= N) continue;
+      float sg = 1.f, su = 1.f;
+      if constexpr (WF == MX_DT_I8) {
+        sg = (float)((const half_t*)ep.gate_scale)[n];
+        su = (float)((const half_t*)ep.up_scale)[n];
+      }
+#pragma unroll
+      for (int mi = 0; mi < MT; ++mi)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = 16 * mi + 4 * q + r;
+          if (m < mrows) {
+            const float gv = acc[mi][f][r] * sg;
+            const float uv = acc[mi][NBI + f][r] * su;
+            ((half_t*)p.out)[(size_t)(gstart + row0 + m) * p.ldo + n] = (half_t)(mx_silu(gv) * uv);
+          }
+        }
+    }
+  } else {
+#pragma unroll
+    for (int f = 0; f < NBI; ++f) {
+      const int n = n0 + 16 * f + j;
+      if (n >= N) continue;
+      float sd = 1.f;
+      if constexpr (WF == MX_DT_I8) sd = (float)((const half_t*)ep.down_scale)[n];
+#pragma unroll
+      for (int mi = 0; mi < MT; ++mi)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = 16 * mi + 4 * q + r;
+          if (m < mrows) {
+            const int row = gstart + row0 + m;
+            ((float*)p.out)[(size_t)row * p.ldo + n] = p.sorted_w[row] * (acc[mi][f][r] * sd);
+          }
+        }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------
 // Host side.
 // ------------------------------------------------------------------------------------
 int mx_m_blk_for(int tokens, int weight_dtype) {
-  (void)weight_dtype;
   if (tokens <= 16) return 16;
   if (tokens <= 32) return 32;
-  return 64;
+  if (tokens <= 64 || weight_dtype == MX_DT_F32) return 64;
+  return 128;
 }
 
 static int expert_check(const MxMoeDesc* d) {
@@ -334,8 +581,30 @@ static int dispatch_expert(int wdt, int mt, const ExpertParams& p, dim3 grid, hi
   return MX_ERR_INVALID;
 }
 
-static int mt_from_mblk(int m_blk) {
-  return (m_blk == 16 || m_blk == 32 || m_blk == 64) ? m_blk / 16 : 0;
+// Direct-load kernel for m_blk 16/32/64; LDS-staged kernel for m_blk 128 (fp16/int8).
+template <bool GU>
+static int launch_grouped(const MxMoeDesc* d, const ExpertParams& p, int tokens, int m_blk,
+                          int nmax, hipStream_t s) {
+  const int has_shared = d->shared_inter > 0;
+  const int mt_max = mx_max_mtiles(tokens, d->top_k, d->n_experts, has_shared, m_blk);
+  if (m_blk == 128) {
+    if (d->weight_dtype == MX_DT_F32) return MX_ERR_INVALID;
+    const int cols = 4 * 16 * (GU ? 2 : 4);
+    const int nblk = mx_ceil_div(nmax, cols);
+    const long blocks = ((long)mt_max * nblk + 7) / 8 * 8;
+    if (blocks > (1l << 31) - 1) return MX_ERR_UNSUPPORTED;
+    mx_clear_error();
+    if (d->weight_dtype == MX_DT_F16)
+      hipLaunchKernelGGL((k_expert_lds<MX_DT_F16, GU>), dim3((unsigned)blocks), dim3(256), 0, s,
+                         p, mt_max, nblk);
+    else
+      hipLaunchKernelGGL((k_expert_lds<MX_DT_I8, GU>), dim3((unsigned)blocks), dim3(256), 0, s,
+                         p, mt_max, nblk);
+    return mx_launch_status();
+  }
+  if (m_blk != 16 && m_blk != 32 && m_blk != 64) return MX_ERR_INVALID;
+  dim3 grid(mt_max, mx_ceil_div(nmax, 4 * 16 * (GU ? 1 : 2)));
+  return dispatch_expert<GU>(d->weight_dtype, m_blk / 16, p, grid, s);
 }
 
 extern "C" int mx_expert_gate_up(const MxMoeDesc* desc, const MxExpertPtrs* experts,
@@ -348,14 +617,12 @@ extern "C" int mx_expert_gate_up(const MxMoeDesc* desc, const MxExpertPtrs* expe
   if (!experts || !a || !sorted_tok || !g_expert || !g_start || !g_count || !mt_group ||
       !mt_row0 || !n_mtiles || !act || tokens < 0)
     return MX_ERR_INVALID;
-  const int mt = mt_from_mblk(m_blk);
-  if (!mt) return MX_ERR_INVALID;
+  if (m_blk != 16 && m_blk != 32 && m_blk != 64 && m_blk != 128) return MX_ERR_INVALID;
   if (tokens == 0) return MX_OK;
   const int aesz = desc->weight_dtype == MX_DT_F32 ? 4 : 2;
   const long abytes = (long)tokens * desc->hidden * aesz;
   if (abytes >= (1l << 31)) return MX_ERR_UNSUPPORTED;
   if (!mx_aligned16(a) || !mx_aligned16(act)) return MX_ERR_ALIGNMENT;
-  const int has_shared = desc->shared_inter > 0;
   ExpertParams p;
   p.experts = experts;
   p.g_expert = g_expert;
@@ -376,10 +643,7 @@ extern "C" int mx_expert_gate_up(const MxMoeDesc* desc, const MxExpertPtrs* expe
   p.K_r = desc->hidden;
   p.N_s = desc->shared_inter;
   p.K_s = desc->hidden;
-  const int nmax = p.ldo;
-  dim3 grid(mx_max_mtiles(tokens, desc->top_k, desc->n_experts, has_shared, m_blk),
-            mx_ceil_div(nmax, 4 * 16 * 1));
-  return dispatch_expert<true>(desc->weight_dtype, mt, p, grid, (hipStream_t)stream);
+  return launch_grouped<true>(desc, p, tokens, m_blk, p.ldo, (hipStream_t)stream);
 }
 
 extern "C" int mx_expert_down(const MxMoeDesc* desc, const MxExpertPtrs* experts, int32_t tokens,
@@ -391,8 +655,7 @@ extern "C" int mx_expert_down(const MxMoeDesc* desc, const MxExpertPtrs* experts
   if (!experts || !act || !sorted_w || !g_expert || !g_start || !g_count || !mt_group ||
       !mt_row0 || !n_mtiles || !y || tokens < 0)
     return MX_ERR_INVALID;
-  const int mt = mt_from_mblk(m_blk);
-  if (!mt) return MX_ERR_INVALID;
+  if (m_blk != 16 && m_blk != 32 && m_blk != 64 && m_blk != 128) return MX_ERR_INVALID;
   if (tokens == 0) return MX_OK;
   const int has_shared = desc->shared_inter > 0;
   const int aesz = desc->weight_dtype == MX_DT_F32 ? 4 : 2;
@@ -421,7 +684,5 @@ extern "C" int mx_expert_down(const MxMoeDesc* desc, const MxExpertPtrs* experts
   p.K_r = desc->inter;
   p.N_s = desc->hidden;
   p.K_s = desc->shared_inter;
-  dim3 grid(mx_max_mtiles(tokens, desc->top_k, desc->n_experts, has_shared, m_blk),
-            mx_ceil_div(desc->hidden, 4 * 16 * 2));
-  return dispatch_expert<false>(desc->weight_dtype, mt, p, grid, (hipStream_t)stream);
+  return launch_grouped<false>(desc, p, tokens, m_blk, desc->hidden, (hipStream_t)stream);
 }

@@ -144,7 +144,7 @@ def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
     with _lock:
         if _lib is not None:
             return _lib
-        lib_path = Path(path) if path else LIB_PATH
+        lib_path = Path(path or os.environ.get("MX_LIB_PATH") or LIB_PATH)
         if not lib_path.exists():
             raise RuntimeError(
                 f"{lib_path.name} is not built ({lib_path}); run __graft_entry__.build() "

@@ -150,6 +150,32 @@ def test_token_sweep(mi355x, stream, wdt, T):
         assert err <= LOWP_ABS
 
 
+@pytest.mark.parametrize("wdt", ["float16", "int8"])
+@pytest.mark.parametrize("T", [600, 1500])
+def test_skewed_prefill(mi355x, stream, wdt, T):
+    """Hot experts far above 128 rows (several m-tiles per group) next to cold ones."""
+    say(f"[gpu] skewed prefill wdt={wdt} T={T}")
+    shape = syn.MoeShape(syn.GLM, 512, 24, 4, 256, 128, 2.5, 1e-5)
+    base = syn.make_tensors(shape, 99 + T)
+    bias = np.zeros(shape.n_experts, np.float32)
+    bias[:3] = [0.9, 0.5, 0.3]  # experts 0..2 take most tokens in sigmoid-select routing
+    base["mlp.gate.e_score_correction_bias"] = bias
+    if wdt == "float16":
+        t = {n: (v.astype(np.float16) if n.startswith(("mlp.experts.", "mlp.shared_experts."))
+                 else v) for n, v in base.items()}
+    else:
+        t = quantize_moe_tensors(base)
+    x = syn.make_inputs(99 + T, T, shape.hidden)
+    spec = spec_for(shape, orc.SIGMOID_SELECT_BIAS)
+    out, views = run_device(mi355x, stream, t, shape, spec, x)
+    ref = orc.moe_block(x, t, spec)
+    assert ref["counts"][:3].min() > 256
+    check_routing(views, ref, ref["logits"], bias, spec, f"skew/{wdt}/T={T}")
+    err = float(np.max(np.abs(out - ref["out"])))
+    say(f"    max abs err {err:.3e}, counts[:3]={ref['counts'][:3].tolist()}")
+    assert err <= LOWP_ABS
+
+
 # ---- Qwen3-Next structure: softmax router, no bias, gated shared expert --------------------
 
 @pytest.mark.parametrize("wdt", ["float32", "float16"])
