@@ -1,0 +1,98 @@
+"""Packed layer layout (loader contract, loader/huggingface.py:458-591 of the reference),
+metadata parsing and the device pointer table."""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from moe_mi355x import _lib
+from moe_mi355x import synthetic as syn
+from moe_mi355x.layout import MoeLayerLayout, pack_tensors, unpack_host
+from moe_mi355x.quantize import quantize_moe_tensors
+
+
+def test_pack_is_lexicographic_and_contiguous():
+    t = {"b": np.arange(3, dtype=np.float32), "a": np.ones((2, 2), np.float16),
+         "mlp.experts.10.x": np.zeros(1, np.int8), "mlp.experts.2.x": np.zeros(1, np.int8)}
+    raw, meta = pack_tensors(t)
+    assert [m["name"] for m in meta] == ["a", "b", "mlp.experts.10.x", "mlp.experts.2.x"]
+    assert [m["offset"] for m in meta] == [0, 8, 20, 21]
+    back = unpack_host(raw, meta)
+    for k, v in t.items():
+        assert np.array_equal(back[k], v) and back[k].dtype == v.dtype
+
+
+def test_pack_alignment():
+    t = {"a": np.zeros(3, np.int8), "b": np.zeros(5, np.float32)}
+    _, meta = pack_tensors(t, align=256)
+    assert meta[1]["offset"] == 256
+
+
+@pytest.mark.parametrize("shape", [syn.C1, syn.MoeShape(syn.QWEN, 64, 6, 2, 32, 16, 1.0, 1e-6,
+                                                        has_bias=False, has_shared_gate=True)])
+def test_layout_parses_both_architectures(shape):
+    t = syn.make_tensors(shape, 1) if shape.hidden < 1024 else \
+        {n: np.zeros(s, np.float32) for n, s, _, _ in syn.tensor_specs(shape)}
+    _, meta = pack_tensors(t, align=16)
+    lay = MoeLayerLayout.from_meta(meta)
+    assert (lay.hidden, lay.inter, lay.shared_inter, lay.n_experts) == \
+        (shape.hidden, shape.inter, shape.shared_inter, shape.n_experts)
+    assert lay.has_bias == shape.has_bias and lay.has_shared_gate == shape.has_shared_gate
+    assert lay.weight_dtype == _lib.MX_DT_F32 and lay.param_dtype == _lib.MX_DT_F32
+    base = 1 << 40
+    table = lay.expert_table(base)
+    assert len(table) == shape.n_experts + 1
+    e1 = [m for m in meta if m["name"] == "mlp.experts.1.down_proj.weight"][0]
+    assert table[1].down == base + e1["offset"]
+    assert table[shape.n_experts].gate is not None  # shared expert in the last slot
+    w = lay.weights(base, 1234)
+    assert w.experts == 1234 and w.norm_w == base + lay.offset("post_attention_layernorm.weight")
+    assert (w.bias is not None) == shape.has_bias
+
+
+def test_int8_layout_carries_scales():
+    shape = syn.MoeShape(syn.GLM, 32, 4, 2, 16, 16, 2.5, 1e-5)
+    t = quantize_moe_tensors(syn.make_tensors(shape, 2))
+    _, meta = pack_tensors(t, align=16)
+    lay = MoeLayerLayout.from_meta(meta)
+    assert lay.weight_dtype == _lib.MX_DT_I8
+    table = lay.expert_table(4096)
+    assert table[0].gate_scale == 4096 + lay.offset("mlp.experts.0.gate_proj.weight_scale")
+
+
+def test_layout_errors():
+    shape = syn.MoeShape(syn.GLM, 32, 4, 2, 16, 16, 2.5, 1e-5)
+    t = syn.make_tensors(shape, 3)
+    bad = dict(t)
+    del bad["mlp.experts.2.up_proj.weight"]
+    with pytest.raises(ValueError, match="expert 2"):
+        MoeLayerLayout.from_meta(pack_tensors(bad)[1])
+    bad = dict(t)
+    bad["mlp.experts.1.gate_proj.weight"] = bad["mlp.experts.1.gate_proj.weight"].astype(np.float16)
+    with pytest.raises(ValueError, match="one dtype"):
+        MoeLayerLayout.from_meta(pack_tensors(bad)[1])
+    bad = dict(t)
+    del bad["mlp.gate.weight"]
+    with pytest.raises(ValueError, match="missing"):
+        MoeLayerLayout.from_meta(pack_tensors(bad)[1])
+    q = quantize_moe_tensors(t)
+    del q["mlp.experts.0.down_proj.weight_scale"]
+    with pytest.raises(ValueError, match="scale"):
+        MoeLayerLayout.from_meta(pack_tensors(q)[1])
+
+
+def test_misaligned_expert_is_reported():
+    shape = syn.MoeShape(syn.GLM, 32, 4, 2, 16, 16, 2.5, 1e-5)
+    t = syn.make_tensors(shape, 4)
+    t["mlp.a_odd"] = np.zeros(3, np.int8)  # sorts before the experts and shifts them by 3 bytes
+    _, meta = pack_tensors(t)
+    lay = MoeLayerLayout.from_meta(meta)
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        lay.expert_table(0)
+
+
+def test_expert_ptrs_struct_matches_header():
+    assert ctypes.sizeof(_lib.MxExpertPtrs) == 48
+    assert ctypes.sizeof(_lib.MxMoeDesc) == 13 * 4
