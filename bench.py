@@ -129,6 +129,20 @@ def summarize(res: dict, name: str, wdt: str) -> dict:
     }
 
 
+def profiled_traffic(workload: str, kernel: str) -> float | None:
+    """HBM bytes per launch measured by rocprofv3 FETCH_SIZE/WRITE_SIZE runs of this same
+    workload, as recorded in profiles/ (None when no such profile exists)."""
+    import re
+    key = f"traffic_bytes_per_launch[{workload}/{kernel}]:"
+    for f in sorted((ROOT / "profiles").glob("pmc_*.md")):
+        for line in f.read_text().splitlines():
+            if line.startswith(key):
+                m = re.search(r"([0-9.eE+]+)\s*$", line)
+                if m:
+                    return float(m.group(1))
+    return None
+
+
 def cpu_baseline(layer: DeviceMoeLayer, shape: syn.MoeShape, x: np.ndarray, budget_s: float):
     """Oracle in the reference's loop structure on the host cores (routed experts only are
     copied to the host; the copy is not timed).  Returns (baseline dict, oracle output)."""
@@ -348,7 +362,8 @@ def main() -> int:
         "roofline": {"kernel": "k_expert gate/up (fp16 MFMA, fused SiLU*up)", "bound": "hbm",
                      "achieved": round(gu_bytes / gu_s / 1e9, 1), "peak": HBM_PEAK / 1e9,
                      "unit": "GB/s", "frac": round(gu_bytes / gu_s / HBM_PEAK, 4),
-                     "traffic": None, "avg_launch_ms": round(st[4], 4),
+                     "traffic": profiled_traffic(head["workload"], "gate_up"),
+                     "avg_launch_ms": round(st[4], 4),
                      "bytes_per_launch": int(gu_bytes)},
         "layer": {k: head[k] for k in ("layer_GBps", "layer_hbm_frac", "layer_mfma_frac",
                                        "roofline_frac", "stage_ms", "down_hbm_frac")},
