@@ -20,14 +20,21 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ x,
   const int* pp = pair_pos + (size_t)t * k;
   if constexpr (VEC4) {
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int j = 0; j < k; ++j) {
-      const int p = pp[j];
-      if (p < 0) continue;
-      const float4 v = *(const float4*)(y + (size_t)p * H + c);
-      o.x += v.x;
-      o.y += v.y;
-      o.z += v.z;
-      o.w += v.w;
+    // Slots in groups of 8: all loads of a group are issued before the ordered adds.
+    for (int j0 = 0; j0 < k; j0 += 8) {
+      float4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int p = (j0 + u < k) ? pp[j0 + u] : -1;
+        v[u] = p >= 0 ? *(const float4*)(y + (size_t)p * H + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        o.x += v[u].x;
+        o.y += v[u].y;
+        o.z += v[u].z;
+        o.w += v[u].w;
+      }
     }
     if (shared_row0 >= 0) {
       const float4 v = *(const float4*)(y + (size_t)(shared_row0 + t) * H + c);

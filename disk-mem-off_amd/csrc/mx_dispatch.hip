@@ -16,10 +16,7 @@
 #include "mx_common.h"
 #include "mx_internal.h"
 
-__device__ __forceinline__ void mx_lds_fence() {
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-  __builtin_amdgcn_wave_barrier();
-}
+#include "mx_dispatch_dev.h"
 
 __global__ __launch_bounds__(512) void k_dispatch(
     const int* __restrict__ ids, const float* __restrict__ tw, const float* __restrict__ shw,
@@ -29,161 +26,11 @@ __global__ __launch_bounds__(512) void k_dispatch(
     int* __restrict__ g_count, int* __restrict__ n_groups, int* __restrict__ mt_group,
     int* __restrict__ mt_row0, int* __restrict__ n_mtiles) {
   extern __shared__ __align__(16) unsigned char smem[];
-  const int NW = blockDim.x >> 6;
-  unsigned long long* mask = (unsigned long long*)smem;  // [NW][E]
-  int* cnt = (int*)(mask + (size_t)NW * E);             // [NW][E]
-  int* tot = cnt + NW * E;                               // [E]
-  int* off = tot + E;                                    // [E]
-  int* gid = off + E;                                    // [E]
-  int* mtb = gid + E;                                    // [E]
-  __shared__ int s_tot[3];
-
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int P = T * k;
-  const int tpw = (T + NW - 1) / NW;
-  const int tb = min(T, w * tpw), te = min(T, tb + tpw);
-
-  for (int i = tid; i < NW * E; i += blockDim.x) cnt[i] = 0;
-  __syncthreads();
-  for (int p = tb * k + lane; p < te * k; p += 64) {
-    const int e = ids[p];
-    if ((unsigned)e < (unsigned)E) atomicAdd(&cnt[w * E + e], 1);
-  }
-  __syncthreads();
-  // Per expert: exclusive base of every wave's range, and the total.
-  for (int e = tid; e < E; e += blockDim.x) {
-    int run = 0;
-    for (int ww = 0; ww < NW; ++ww) {
-      const int c = cnt[ww * E + e];
-      cnt[ww * E + e] = run;
-      run += c;
-    }
-    tot[e] = run;
-    counts[e] = run;
-  }
-  __syncthreads();
-  // Three exclusive scans over experts by wave 0: rows, active flags, m-tiles.
-  if (w == 0) {
-    const int per = (E + 63) / 64;
-    const int beg = min(E, lane * per), end = min(E, beg + per);
-    int a = 0, b = 0, c = 0;
-    for (int e = beg; e < end; ++e) {
-      const int n = tot[e];
-      a += n;
-      b += n > 0;
-      c += (n + m_blk - 1) / m_blk;
-    }
-    int ia = a, ib = b, ic = c;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const int xa = __shfl_up(ia, d, 64), xb = __shfl_up(ib, d, 64), xc = __shfl_up(ic, d, 64);
-      if (lane >= d) {
-        ia += xa;
-        ib += xb;
-        ic += xc;
-      }
-    }
-    int ea = ia - a, eb = ib - b, ec = ic - c;
-    for (int e = beg; e < end; ++e) {
-      const int n = tot[e];
-      off[e] = ea;
-      gid[e] = eb;
-      mtb[e] = ec;
-      ea += n;
-      eb += n > 0;
-      ec += (n + m_blk - 1) / m_blk;
-    }
-    if (lane == 63) {
-      s_tot[0] = ia;
-      s_tot[1] = ib;
-      s_tot[2] = ic;
-    }
-  }
-  __syncthreads();
-  for (int e = tid; e < E; e += blockDim.x) offsets[e] = off[e];
-  if (tid == 0) offsets[E] = s_tot[0];
-
-  // Stable positions: rounds of 64 tokens per wave, lane = token.
-  unsigned long long* wm = mask + (size_t)w * E;
-  int* wc = cnt + w * E;
-  const unsigned long long below = (1ull << lane) - 1ull;
-  for (int r0 = tb; r0 < te; r0 += 64) {
-    const int t = r0 + lane;
-    const bool v = t < te;
-    for (int j = 0; j < k; ++j) {
-      const int e = v ? ids[t * k + j] : -1;
-      if ((unsigned)e < (unsigned)E) wm[e] = 0ull;
-    }
-    mx_lds_fence();
-    for (int j = 0; j < k; ++j) {
-      const int e = v ? ids[t * k + j] : -1;
-      if ((unsigned)e < (unsigned)E) atomicOr(&wm[e], 1ull << lane);
-    }
-    mx_lds_fence();
-    for (int j = 0; j < k; ++j) {
-      const int e = v ? ids[t * k + j] : -1;
-      if (!v) continue;
-      if ((unsigned)e < (unsigned)E) {
-        const unsigned long long m = ((volatile unsigned long long*)wm)[e];
-        const int pos = off[e] + wc[e] + __popcll(m & below);
-        sorted_tok[pos] = t;
-        sorted_w[pos] = tw[t * k + j];
-        pair_pos[t * k + j] = pos;
-      } else {
-        pair_pos[t * k + j] = -1;
-      }
-    }
-    mx_lds_fence();
-    for (int j = 0; j < k; ++j) {
-      const int e = v ? ids[t * k + j] : -1;
-      if ((unsigned)e < (unsigned)E) {
-        const unsigned long long m = ((volatile unsigned long long*)wm)[e];
-        if ((m & below) == 0ull) wc[e] += __popcll(m);
-      }
-    }
-    mx_lds_fence();
-  }
-  __syncthreads();
-
-  // Group table and m-tile list.
-  const int G0 = has_shared ? 1 : 0;
-  const int S0 = has_shared ? (T + m_blk - 1) / m_blk : 0;
-  for (int e = tid; e < E; e += blockDim.x) {
-    const int n = tot[e];
-    if (n > 0) {
-      const int g = G0 + gid[e];
-      g_expert[g] = e;
-      g_start[g] = off[e];
-      g_count[g] = n;
-      const int nt = (n + m_blk - 1) / m_blk;
-      for (int i = 0; i < nt; ++i) {
-        mt_group[S0 + mtb[e] + i] = g;
-        mt_row0[S0 + mtb[e] + i] = i * m_blk;
-      }
-    }
-  }
-  if (has_shared) {
-    if (tid == 0) {
-      g_expert[0] = E;
-      g_start[0] = P;
-      g_count[0] = T;
-    }
-    for (int i = tid; i < S0; i += blockDim.x) {
-      mt_group[i] = 0;
-      mt_row0[i] = i * m_blk;
-    }
-    for (int t = tid; t < T; t += blockDim.x) {
-      sorted_tok[P + t] = t;
-      sorted_w[P + t] = shw ? shw[t] : 1.f;
-    }
-  }
-  if (tid == 0) {
-    *n_groups = G0 + s_tot[1];
-    *n_mtiles = S0 + s_tot[2];
-  }
+  mx_dispatch_block(smem, ids, tw, shw, T, k, E, has_shared, m_blk, counts, offsets, sorted_tok,
+                    sorted_w, pair_pos, g_expert, g_start, g_count, n_groups, mt_group, mt_row0,
+                    n_mtiles);
 }
 
-static size_t dispatch_lds_bytes(int nw, int E) { return (size_t)nw * E * 12 + (size_t)E * 16; }
 
 int mx_max_mtiles(int tokens, int top_k, int n_experts, int has_shared, int m_blk) {
   const long pairs = (long)tokens * top_k;
@@ -206,8 +53,8 @@ extern "C" int mx_dispatch(const int32_t* topk_ids, const float* topk_w, const f
   if (n_experts > 2048) return MX_ERR_UNSUPPORTED;
   if ((long)tokens * top_k > (1l << 30)) return MX_ERR_UNSUPPORTED;
   int nw = 8;
-  while (nw > 1 && dispatch_lds_bytes(nw, n_experts) > 60 * 1024) nw >>= 1;
-  const size_t lds = dispatch_lds_bytes(nw, n_experts);
+  while (nw > 1 && mx_dispatch_lds_bytes(nw, n_experts) > 60 * 1024) nw >>= 1;
+  const size_t lds = mx_dispatch_lds_bytes(nw, n_experts);
   if (lds > 60 * 1024) return MX_ERR_UNSUPPORTED;
   mx_clear_error();
   hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(nw * 64), lds, (hipStream_t)stream, topk_ids,

@@ -1,0 +1,177 @@
+// Device body of the token -> expert dispatch, shared by k_dispatch and the fused router.
+#pragma once
+
+#include "mx_common.h"
+
+__host__ __device__ static inline size_t mx_dispatch_lds_bytes(int nw, int E) {
+  return (size_t)nw * E * 12 + (size_t)E * 16;
+}
+
+__device__ __forceinline__ void mx_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// Whole-workgroup dispatch (every thread of the block must call it).  `smem` holds
+// mx_dispatch_lds_bytes(blockDim.x / 64, E) bytes.
+__device__ __forceinline__ void mx_dispatch_block(
+    unsigned char* smem, const int* __restrict__ ids, const float* __restrict__ tw,
+    const float* __restrict__ shw, int T, int k, int E, int has_shared, int m_blk,
+    int* __restrict__ counts, int* __restrict__ offsets, int* __restrict__ sorted_tok,
+    float* __restrict__ sorted_w, int* __restrict__ pair_pos, int* __restrict__ g_expert,
+    int* __restrict__ g_start, int* __restrict__ g_count, int* __restrict__ n_groups,
+    int* __restrict__ mt_group, int* __restrict__ mt_row0, int* __restrict__ n_mtiles) {
+  const int NW = blockDim.x >> 6;
+  unsigned long long* mask = (unsigned long long*)smem;  // [NW][E]
+  int* cnt = (int*)(mask + (size_t)NW * E);             // [NW][E]
+  int* tot = cnt + NW * E;                               // [E]
+  int* off = tot + E;                                    // [E]
+  int* gid = off + E;                                    // [E]
+  int* mtb = gid + E;                                    // [E]
+  __shared__ int s_tot[3];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int P = T * k;
+  const int tpw = (T + NW - 1) / NW;
+  const int tb = min(T, w * tpw), te = min(T, tb + tpw);
+
+  for (int i = tid; i < NW * E; i += blockDim.x) cnt[i] = 0;
+  __syncthreads();
+  for (int p = tb * k + lane; p < te * k; p += 64) {
+    const int e = ids[p];
+    if ((unsigned)e < (unsigned)E) atomicAdd(&cnt[w * E + e], 1);
+  }
+  __syncthreads();
+  // Per expert: exclusive base of every wave's range, and the total.
+  for (int e = tid; e < E; e += blockDim.x) {
+    int run = 0;
+    for (int ww = 0; ww < NW; ++ww) {
+      const int c = cnt[ww * E + e];
+      cnt[ww * E + e] = run;
+      run += c;
+    }
+    tot[e] = run;
+    counts[e] = run;
+  }
+  __syncthreads();
+  // Three exclusive scans over experts by wave 0: rows, active flags, m-tiles.
+  if (w == 0) {
+    const int per = (E + 63) / 64;
+    const int beg = min(E, lane * per), end = min(E, beg + per);
+    int a = 0, b = 0, c = 0;
+    for (int e = beg; e < end; ++e) {
+      const int n = tot[e];
+      a += n;
+      b += n > 0;
+      c += (n + m_blk - 1) / m_blk;
+    }
+    int ia = a, ib = b, ic = c;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int xa = __shfl_up(ia, d, 64), xb = __shfl_up(ib, d, 64), xc = __shfl_up(ic, d, 64);
+      if (lane >= d) {
+        ia += xa;
+        ib += xb;
+        ic += xc;
+      }
+    }
+    int ea = ia - a, eb = ib - b, ec = ic - c;
+    for (int e = beg; e < end; ++e) {
+      const int n = tot[e];
+      off[e] = ea;
+      gid[e] = eb;
+      mtb[e] = ec;
+      ea += n;
+      eb += n > 0;
+      ec += (n + m_blk - 1) / m_blk;
+    }
+    if (lane == 63) {
+      s_tot[0] = ia;
+      s_tot[1] = ib;
+      s_tot[2] = ic;
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += blockDim.x) offsets[e] = off[e];
+  if (tid == 0) offsets[E] = s_tot[0];
+
+  // Stable positions: rounds of 64 tokens per wave, lane = token.
+  unsigned long long* wm = mask + (size_t)w * E;
+  int* wc = cnt + w * E;
+  const unsigned long long below = (1ull << lane) - 1ull;
+  for (int r0 = tb; r0 < te; r0 += 64) {
+    const int t = r0 + lane;
+    const bool v = t < te;
+    for (int j = 0; j < k; ++j) {
+      const int e = v ? ids[t * k + j] : -1;
+      if ((unsigned)e < (unsigned)E) wm[e] = 0ull;
+    }
+    mx_lds_fence();
+    for (int j = 0; j < k; ++j) {
+      const int e = v ? ids[t * k + j] : -1;
+      if ((unsigned)e < (unsigned)E) atomicOr(&wm[e], 1ull << lane);
+    }
+    mx_lds_fence();
+    for (int j = 0; j < k; ++j) {
+      const int e = v ? ids[t * k + j] : -1;
+      if (!v) continue;
+      if ((unsigned)e < (unsigned)E) {
+        const unsigned long long m = ((volatile unsigned long long*)wm)[e];
+        const int pos = off[e] + wc[e] + __popcll(m & below);
+        sorted_tok[pos] = t;
+        sorted_w[pos] = tw[t * k + j];
+        pair_pos[t * k + j] = pos;
+      } else {
+        pair_pos[t * k + j] = -1;
+      }
+    }
+    mx_lds_fence();
+    for (int j = 0; j < k; ++j) {
+      const int e = v ? ids[t * k + j] : -1;
+      if ((unsigned)e < (unsigned)E) {
+        const unsigned long long m = ((volatile unsigned long long*)wm)[e];
+        if ((m & below) == 0ull) wc[e] += __popcll(m);
+      }
+    }
+    mx_lds_fence();
+  }
+  __syncthreads();
+
+  // Group table and m-tile list.
+  const int G0 = has_shared ? 1 : 0;
+  const int S0 = has_shared ? (T + m_blk - 1) / m_blk : 0;
+  for (int e = tid; e < E; e += blockDim.x) {
+    const int n = tot[e];
+    if (n > 0) {
+      const int g = G0 + gid[e];
+      g_expert[g] = e;
+      g_start[g] = off[e];
+      g_count[g] = n;
+      const int nt = (n + m_blk - 1) / m_blk;
+      for (int i = 0; i < nt; ++i) {
+        mt_group[S0 + mtb[e] + i] = g;
+        mt_row0[S0 + mtb[e] + i] = i * m_blk;
+      }
+    }
+  }
+  if (has_shared) {
+    if (tid == 0) {
+      g_expert[0] = E;
+      g_start[0] = P;
+      g_count[0] = T;
+    }
+    for (int i = tid; i < S0; i += blockDim.x) {
+      mt_group[i] = 0;
+      mt_row0[i] = i * m_blk;
+    }
+    for (int t = tid; t < T; t += blockDim.x) {
+      sorted_tok[P + t] = t;
+      sorted_w[P + t] = shw ? shw[t] : 1.f;
+    }
+  }
+  if (tid == 0) {
+    *n_groups = G0 + s_tot[1];
+    *n_mtiles = S0 + s_tot[2];
+  }
+}
+

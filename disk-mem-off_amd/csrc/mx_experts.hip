@@ -556,10 +556,23 @@ static int expert_check(const MxMoeDesc* d) {
   return MX_OK;
 }
 
+// Decode-kernel shape (compile-time tunables): column blocks of 16 per wave for gate/up
+// (x2 for the gate and up halves) and for down, and k-chunks per load batch.
+#ifndef MX_DEC_NBI_GU
+#define MX_DEC_NBI_GU 1
+#endif
+#ifndef MX_DEC_NBI_DN
+#define MX_DEC_NBI_DN 2
+#endif
+#ifndef MX_DEC_UK
+#define MX_DEC_UK 4
+#endif
+
 template <int WF, int MT, bool GU>
 static void launch_expert(const ExpertParams& p, dim3 grid, hipStream_t s) {
-  constexpr int NBI = GU ? 1 : 2;
-  constexpr int UK = (WF == MX_DT_I8) ? (MT >= 4 ? 1 : 2) : (MT >= 4 ? 2 : 4);
+  constexpr int NBI = GU ? MX_DEC_NBI_GU : MX_DEC_NBI_DN;
+  constexpr int UK = (WF == MX_DT_I8) ? (MT >= 4 ? 1 : MX_DEC_UK / 2)
+                                      : (MT >= 4 ? 2 : MX_DEC_UK);
   mx_clear_error();
   hipLaunchKernelGGL((k_expert<WF, MT, NBI, GU, UK>), grid, dim3(256), 0, s, p);
 }
@@ -603,7 +616,7 @@ static int launch_grouped(const MxMoeDesc* d, const ExpertParams& p, int tokens,
     return mx_launch_status();
   }
   if (m_blk != 16 && m_blk != 32 && m_blk != 64) return MX_ERR_INVALID;
-  dim3 grid(mt_max, mx_ceil_div(nmax, 4 * 16 * (GU ? 1 : 2)));
+  dim3 grid(mt_max, mx_ceil_div(nmax, 4 * 16 * (GU ? MX_DEC_NBI_GU : MX_DEC_NBI_DN)));
   return dispatch_expert<GU>(d->weight_dtype, m_blk / 16, p, grid, s);
 }
 

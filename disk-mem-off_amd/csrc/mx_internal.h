@@ -1,6 +1,8 @@
 // Declarations shared between the translation units of libmoe_mi355x.so (not exported).
 #pragma once
 
+#include <hip/hip_runtime.h>
+
 #include "moe_mi355x.h"
 
 // Number of H-slices the router logit kernel uses for this shape.
@@ -11,3 +13,16 @@ int mx_max_mtiles(int tokens, int top_k, int n_experts, int has_shared, int m_bl
 
 // Rows per m-tile the expert kernels use for `tokens` tokens.
 int mx_m_blk_for(int tokens, int weight_dtype);
+
+// RMSNorm launch (vectorised when the row fits the register tile).
+int mx_rmsnorm_launch(const float* x, const void* norm_w, int param_dtype, float eps, int tokens,
+                      int hidden, float* h32, void* h16, hipStream_t s);
+
+// Decode router (T <= 64): logits kernel + single-workgroup top-k/dispatch kernel;
+// MX_ERR_UNSUPPORTED outside its limits (T > 64, or dispatch tables beyond the LDS budget).
+int mx_router_decode_launch(const MxMoeDesc* d, const MxMoeWeights* w, int T, const float* h32,
+                            float* logits, int* ids, float* tw, float* shared_w, int m_blk,
+                            int* counts, int* offsets, int* sorted_tok, float* sorted_w,
+                            int* pair_pos, int* g_expert, int* g_start, int* g_count,
+                            int* n_groups, int* mt_group, int* mt_row0, int* n_mtiles,
+                            hipStream_t s);

@@ -7,6 +7,7 @@
 // allocated here.
 #include "mx_common.h"
 #include "mx_internal.h"
+#include "mx_dispatch_dev.h"
 
 namespace {
 
@@ -36,6 +37,12 @@ int check_desc(const MxMoeDesc* d) {
   return MX_OK;
 }
 
+// Decode-sized batches run the decode router (logits, then top-k + dispatch in one
+// workgroup) in place of stages 1-3.
+bool use_decode_router(const MxMoeDesc* d, int T) {
+  return T <= 64 && d->n_experts <= 1024 && d->hidden % 4 == 0;
+}
+
 int layout(const MxMoeDesc* d, int T, void* ws, MxMoeViews* v, size_t* total) {
   MX_TRY(check_desc(d));
   if (T < 0) return MX_ERR_INVALID;
@@ -43,7 +50,7 @@ int layout(const MxMoeDesc* d, int T, void* ws, MxMoeViews* v, size_t* total) {
   const size_t H = d->hidden, E = d->n_experts, k = d->top_k;
   const int e1 = d->n_experts + (d->has_shared_gate ? 1 : 0);
   const int has_sh = d->shared_inter > 0;
-  const int S = mx_router_splits_for(Tn, d->hidden, e1);
+  const int S = use_decode_router(d, Tn) ? 1 : mx_router_splits_for(Tn, d->hidden, e1);
   const int m_blk = mx_m_blk_for(Tn, d->weight_dtype);
   const size_t P = (size_t)Tn * k;
   const size_t R = P + (has_sh ? Tn : 0);
@@ -82,10 +89,19 @@ int layout(const MxMoeDesc* d, int T, void* ws, MxMoeViews* v, size_t* total) {
 int run_stage(int stage, const MxMoeDesc* d, const MxMoeWeights* w, const float* x, float* out,
               int T, const MxMoeViews& v, hipStream_t s) {
   const int has_sh = d->shared_inter > 0;
+  const bool decode = use_decode_router(d, T);
+  if (decode && (stage == 2 || stage == 3)) return MX_OK;  // done by the decode router (stage 1)
   switch (stage) {
     case 0:
-      return mx_rmsnorm(x, w->norm_w, d->param_dtype, d->eps, T, d->hidden, v.h32, v.h16, s);
+      if (!x || !w->norm_w) return MX_ERR_INVALID;
+      return mx_rmsnorm_launch(x, w->norm_w, d->param_dtype, d->eps, T, d->hidden, v.h32, v.h16,
+                               s);
     case 1:
+      if (decode)
+        return mx_router_decode_launch(d, w, T, v.h32, v.logits, v.topk_ids, v.topk_w,
+                                       v.shared_w, v.m_blk, v.counts, v.offsets, v.sorted_tok,
+                                       v.sorted_w, v.pair_pos, v.g_expert, v.g_start, v.g_count,
+                                       v.n_groups, v.mt_group, v.mt_row0, v.n_mtiles, s);
       return mx_router_logits(v.h32, w->router_w, d->has_shared_gate ? w->shared_gate_w : nullptr,
                               d->param_dtype, T, d->hidden, d->n_experts, v.router_splits,
                               v.logits, s);

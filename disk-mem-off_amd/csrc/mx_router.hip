@@ -8,34 +8,92 @@
 
 #include "mx_common.h"
 #include "mx_internal.h"
+#include "mx_route_dev.h"
 
 // ------------------------------------------------------------------------------------
 // RMSNorm: one 256-thread block per token.  h = w * (x / sqrt(mean(x^2) + eps)).
+// VEC: each thread keeps its float4 slices of the row in registers (H <= 256 * 4 * RN_V),
+// so all loads of a row are in flight together.
 // ------------------------------------------------------------------------------------
+#define RN_V 8
+
+template <bool VEC>
 __global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x,
                                                  const void* __restrict__ w, int wdt,
                                                  float eps, int H, float* __restrict__ h32,
                                                  half_t* __restrict__ h16) {
   const int t = blockIdx.x;
   const float* xr = x + (size_t)t * H;
-  float ss = 0.f;
-  for (int i = threadIdx.x; i < H; i += 256) {
-    float v = xr[i];
-    ss = fmaf(v, v, ss);
-  }
-  __shared__ float red[4];
-  ss = mx_wave_sum(ss);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
-  __syncthreads();
-  ss = (red[0] + red[1]) + (red[2] + red[3]);
-  const float rms = sqrtf(ss / (float)H + eps);
   float* hr = h32 + (size_t)t * H;
   half_t* hr16 = h16 ? h16 + (size_t)t * H : nullptr;
-  for (int i = threadIdx.x; i < H; i += 256) {
-    float v = mx_load_param(w, wdt, i) * (xr[i] / rms);
-    hr[i] = v;
-    if (hr16) hr16[i] = (half_t)v;
+  __shared__ float red[4];
+  if constexpr (VEC) {
+    float4 v[RN_V];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < RN_V; ++i) {
+      const int c = (threadIdx.x + 256 * i) * 4;
+      v[i] = c < H ? *(const float4*)(xr + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int i = 0; i < RN_V; ++i) {
+      ss = fmaf(v[i].x, v[i].x, ss);
+      ss = fmaf(v[i].y, v[i].y, ss);
+      ss = fmaf(v[i].z, v[i].z, ss);
+      ss = fmaf(v[i].w, v[i].w, ss);
+    }
+    ss = mx_wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    ss = (red[0] + red[1]) + (red[2] + red[3]);
+    const float rms = sqrtf(ss / (float)H + eps);
+#pragma unroll
+    for (int i = 0; i < RN_V; ++i) {
+      const int c = (threadIdx.x + 256 * i) * 4;
+      if (c < H) {
+        float4 o;
+        o.x = mx_load_param(w, wdt, c + 0) * (v[i].x / rms);
+        o.y = mx_load_param(w, wdt, c + 1) * (v[i].y / rms);
+        o.z = mx_load_param(w, wdt, c + 2) * (v[i].z / rms);
+        o.w = mx_load_param(w, wdt, c + 3) * (v[i].w / rms);
+        *(float4*)(hr + c) = o;
+        if (hr16) {
+          typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+          *(h4*)(hr16 + c) = (h4){(half_t)o.x, (half_t)o.y, (half_t)o.z, (half_t)o.w};
+        }
+      }
+    }
+  } else {
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < H; i += 256) {
+      float v = xr[i];
+      ss = fmaf(v, v, ss);
+    }
+    ss = mx_wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    ss = (red[0] + red[1]) + (red[2] + red[3]);
+    const float rms = sqrtf(ss / (float)H + eps);
+    for (int i = threadIdx.x; i < H; i += 256) {
+      float v = mx_load_param(w, wdt, i) * (xr[i] / rms);
+      hr[i] = v;
+      if (hr16) hr16[i] = (half_t)v;
+    }
   }
+}
+
+int mx_rmsnorm_launch(const float* x, const void* norm_w, int param_dtype, float eps, int tokens,
+                      int hidden, float* h32, void* h16, hipStream_t s) {
+  const bool vec = hidden % 4 == 0 && hidden <= 256 * 4 * RN_V && mx_aligned16(x) &&
+                   mx_aligned16(h32) && (!h16 || ((uintptr_t)h16 & 7u) == 0);
+  mx_clear_error();
+  if (vec)
+    hipLaunchKernelGGL(k_rmsnorm<true>, dim3(tokens), dim3(256), 0, s, x, norm_w, param_dtype, eps,
+                       hidden, h32, (half_t*)h16);
+  else
+    hipLaunchKernelGGL(k_rmsnorm<false>, dim3(tokens), dim3(256), 0, s, x, norm_w, param_dtype,
+                       eps, hidden, h32, (half_t*)h16);
+  return mx_launch_status();
 }
 
 extern "C" int mx_rmsnorm(const float* x, const void* norm_w, int32_t param_dtype, float eps,
@@ -43,10 +101,8 @@ extern "C" int mx_rmsnorm(const float* x, const void* norm_w, int32_t param_dtyp
   if (!x || !norm_w || !h32 || tokens < 0 || hidden <= 0) return MX_ERR_INVALID;
   if (param_dtype != MX_DT_F32 && param_dtype != MX_DT_F16) return MX_ERR_INVALID;
   if (tokens == 0) return MX_OK;
-  mx_clear_error();
-  hipLaunchKernelGGL(k_rmsnorm, dim3(tokens), dim3(256), 0, (hipStream_t)stream, x, norm_w,
-                     (int)param_dtype, eps, (int)hidden, h32, (half_t*)h16);
-  return mx_launch_status();
+  return mx_rmsnorm_launch(x, norm_w, param_dtype, eps, tokens, hidden, h32, h16,
+                           (hipStream_t)stream);
 }
 
 // ------------------------------------------------------------------------------------
@@ -100,23 +156,26 @@ __global__ __launch_bounds__(256) void k_router_logits(const float* __restrict__
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[t][j] = 0.f;
 
+  // Rows past the last token re-read the last token (results discarded): the loop body
+  // is branch-free, so its loads are issued together.
+  const float* hrow[RT_TT];
+#pragma unroll
+  for (int t = 0; t < RT_TT; ++t) hrow[t] = h32 + (size_t)min(t0 + t, T - 1) * H;
   for (int k = kb + lane * 4; k < ke; k += RT_KCH) {
     float4 wv[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) wv[j] = rt_load4<WT>(wrow[j] + k);
 #pragma unroll
     for (int t = 0; t < RT_TT; ++t) {
-      if (t < nt) {
-        float4 hv = *(const float4*)(h32 + (size_t)(t0 + t) * H + k);
+      const float4 hv = *(const float4*)(hrow[t] + k);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          float a = acc[t][j];
-          a = fmaf(hv.x, wv[j].x, a);
-          a = fmaf(hv.y, wv[j].y, a);
-          a = fmaf(hv.z, wv[j].z, a);
-          a = fmaf(hv.w, wv[j].w, a);
-          acc[t][j] = a;
-        }
+      for (int j = 0; j < 4; ++j) {
+        float a = acc[t][j];
+        a = fmaf(hv.x, wv[j].x, a);
+        a = fmaf(hv.y, wv[j].y, a);
+        a = fmaf(hv.z, wv[j].z, a);
+        a = fmaf(hv.w, wv[j].w, a);
+        acc[t][j] = a;
       }
     }
   }
@@ -188,113 +247,15 @@ extern "C" int mx_router_logits(const float* h32, const void* router_w, const vo
 // by descending key, as argpartition + argsort(-w) leave them (glm4_moe.py:189-195).
 // Then w /= (sum(w) + 1e-20) when norm_topk_prob and w *= routed_scaling.
 // ------------------------------------------------------------------------------------
-#define TK_MAXK 32
-
 template <int VPT>
 __global__ __launch_bounds__(256) void k_router_topk(
     const float* __restrict__ logits, int S, const void* __restrict__ bias, int pdt, int T,
     int E, int E1, int k, int mode, int norm, float scaling, int has_seg,
     int* __restrict__ ids, float* __restrict__ tw, float* __restrict__ shared_w) {
-  const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
-  float key[VPT], wsrc[VPT];
-  bool taken[VPT];
-#pragma unroll
-  for (int i = 0; i < VPT; ++i) {
-    const int e = lane + 64 * i;
-    taken[i] = false;
-    key[i] = -INFINITY;
-    wsrc[i] = 0.f;
-    if (e < E) {
-      float l = 0.f;
-      for (int s = 0; s < S; ++s) l += logits[((size_t)s * T + t) * E1 + e];
-      const float b = bias ? mx_load_param(bias, pdt, e) : 0.f;
-      if (mode == MX_ROUTER_SIGMOID_SELECT_BIAS) {
-        const float sg = mx_sigmoid(l);
-        key[i] = sg + b;
-        wsrc[i] = sg;
-      } else {
-        key[i] = (mode == MX_ROUTER_REF_SOFTMAX_BIAS) ? l + b : l;
-      }
-    }
-  }
-  if (mode != MX_ROUTER_SIGMOID_SELECT_BIAS) {
-    float m = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < VPT; ++i) m = fmaxf(m, key[i]);
-    m = mx_wave_max(m);
-    float sum = 0.f;
-#pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-      const int e = lane + 64 * i;
-      wsrc[i] = (e < E) ? expf(key[i] - m) : 0.f;
-      sum += wsrc[i];
-    }
-    sum = mx_wave_sum(sum);
-#pragma unroll
-    for (int i = 0; i < VPT; ++i) wsrc[i] = wsrc[i] / sum;
-  }
-#pragma unroll
-  for (int i = 0; i < VPT; ++i)
-    if (key[i] != key[i]) key[i] = -INFINITY;  // NaN never wins a slot
-
-  // Lane r keeps selection r (no dynamically indexed private arrays).
-  int my_id = 0;
-  float my_w = 0.f;
-  for (int r = 0; r < k; ++r) {
-    float bk = -INFINITY;
-    int bi = 0x7fffffff;
-#pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-      const int e = lane + 64 * i;
-      if (e < E && !taken[i] && (key[i] > bk || (key[i] == bk && e < bi))) {
-        bk = key[i];
-        bi = e;
-      }
-    }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-      const float ok = __shfl_xor(bk, m, 64);
-      const int oi = __shfl_xor(bi, m, 64);
-      if (ok > bk || (ok == bk && oi < bi)) {
-        bk = ok;
-        bi = oi;
-      }
-    }
-    const int wl = bi & 63, wi = bi >> 6;
-    float mine = 0.f;
-#pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-      if (i == wi) {
-        mine = wsrc[i];
-        if (lane == wl) taken[i] = true;
-      }
-    }
-    const float w = __shfl(mine, wl, 64);
-    if (lane == r) {
-      my_id = bi;
-      my_w = w;
-    }
-  }
-  float sum = 0.f;  // sequential over the k slots, identical on every lane
-  for (int r = 0; r < k; ++r) sum += __shfl(my_w, r, 64);
-  if (lane < k) {
-    const float w = norm ? my_w / (sum + 1e-20f) : my_w;
-    ids[(size_t)t * k + lane] = my_id;
-    tw[(size_t)t * k + lane] = w * scaling;
-  }
-  if (lane == 0) {
-    if (shared_w) {
-      float g = 1.f;
-      if (has_seg) {
-        float l = 0.f;
-        for (int s = 0; s < S; ++s) l += logits[((size_t)s * T + t) * E1 + E];
-        g = mx_sigmoid(l);
-      }
-      shared_w[t] = g;
-    }
-  }
+  mx_topk_token<VPT>(logits, S, T, t, bias, pdt, E, E1, k, mode, norm, scaling, has_seg, ids,
+                     tw, shared_w);
 }
 
 extern "C" int mx_router_topk(const float* logits, int32_t splits, const void* bias,
@@ -326,5 +287,142 @@ extern "C" int mx_router_topk(const float* logits, int32_t splits, const void* b
   else if (vpt <= 8) TK_LAUNCH(8);
   else TK_LAUNCH(16);
 #undef TK_LAUNCH
+  return mx_launch_status();
+}
+
+// ------------------------------------------------------------------------------------
+// Decode router (T <= 64): two launches.
+//   k_router_logits_decode: one wave per expert (expert E = Qwen3-Next shared gate row),
+//     all T tokens in tiles of RT_TT over the full H (no H split), branch-free loads.
+//   k_topk_dispatch: one workgroup of 8 waves; per-token top-k (one wave per token), then
+//     the dispatch.  A kernel boundary separates the two: the blocks of the logits kernel
+//     run on every XCD, and publishing their results inside one launch would need an L2
+//     write-back per block.
+// ------------------------------------------------------------------------------------
+// One block per expert row (row E = Qwen3-Next shared gate); the 4 waves split H into
+// quarters, each lane keeps TT token partials, and the quarters are added in LDS in a
+// fixed order.  Every load of a wave is issued before the first FMA needs it.
+template <typename WT, int TT>
+__global__ __launch_bounds__(256) void k_router_logits_decode(
+    const float* __restrict__ h32, const WT* __restrict__ wr, const WT* __restrict__ wseg, int T,
+    int H, int E, int E1, float* __restrict__ logits) {
+  __shared__ float part[4][TT];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int e = blockIdx.x;
+  const WT* row = (e < E) ? wr + (size_t)e * H : wseg;
+  const int hq = (H / 4 + 255) / 256 * 256;  // H quarter per wave, in 256-element sweeps
+  const int kb = wave * hq, ke = min(H, kb + hq);
+  for (int t0 = 0; t0 < T; t0 += TT) {
+    float acc[TT];
+    const float* hrow[TT];
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+      acc[t] = 0.f;
+      hrow[t] = h32 + (size_t)min(t0 + t, T - 1) * H;  // past-the-end rows: discarded
+    }
+#pragma unroll 8
+    for (int c = kb + lane * 4; c < ke; c += RT_KCH) {
+      const float4 wv = rt_load4<WT>(row + c);
+#pragma unroll
+      for (int t = 0; t < TT; ++t) {
+        const float4 hv = *(const float4*)(hrow[t] + c);
+        float a = acc[t];
+        a = fmaf(hv.x, wv.x, a);
+        a = fmaf(hv.y, wv.y, a);
+        a = fmaf(hv.z, wv.z, a);
+        a = fmaf(hv.w, wv.w, a);
+        acc[t] = a;
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+      const float v = mx_wave_sum(acc[t]);
+      if (lane == 0) part[wave][t] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x < TT && t0 + (int)threadIdx.x < T) {
+      const int t = threadIdx.x;
+      logits[(size_t)(t0 + t) * E1 + e] = (part[0][t] + part[1][t]) + (part[2][t] + part[3][t]);
+    }
+    __syncthreads();
+  }
+}
+
+template <int VPT>
+__global__ __launch_bounds__(1024) void k_topk_dispatch(
+    const float* __restrict__ logits, const void* __restrict__ bias, int pdt, int T, int E,
+    int E1, int k, int mode, int norm, float scaling, int has_seg, int has_shared, int m_blk,
+    int* __restrict__ ids, float* __restrict__ tw, float* __restrict__ shared_w,
+    int* __restrict__ counts, int* __restrict__ offsets, int* __restrict__ sorted_tok,
+    float* __restrict__ sorted_w, int* __restrict__ pair_pos, int* __restrict__ g_expert,
+    int* __restrict__ g_start, int* __restrict__ g_count, int* __restrict__ n_groups,
+    int* __restrict__ mt_group, int* __restrict__ mt_row0, int* __restrict__ n_mtiles) {
+  // Dynamic LDS: dispatch tables, then the staged top-k results (ids, weights, shared
+  // weights) so the dispatch phases never go back to global memory.
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int nw = blockDim.x >> 6;
+  unsigned char* stage = smem + mx_dispatch_lds_bytes(nw, E);
+  int* sid = (int*)stage;
+  float* sw = (float*)(sid + T * k);
+  float* ssw = sw + T * k;
+  for (int t = threadIdx.x >> 6; t < T; t += nw)
+    mx_topk_token<VPT>(logits, 1, T, t, bias, pdt, E, E1, k, mode, norm, scaling, has_seg, ids,
+                       tw, shared_w, sid, sw, ssw);
+  __syncthreads();
+  mx_dispatch_block(smem, sid, sw, shared_w ? ssw : nullptr, T, k, E, has_shared, m_blk, counts,
+                    offsets, sorted_tok, sorted_w, pair_pos, g_expert, g_start, g_count, n_groups,
+                    mt_group, mt_row0, n_mtiles);
+}
+
+int mx_router_decode_launch(const MxMoeDesc* d, const MxMoeWeights* w, int T, const float* h32,
+                            float* logits, int* ids, float* tw, float* shared_w, int m_blk,
+                            int* counts, int* offsets, int* sorted_tok, float* sorted_w,
+                            int* pair_pos, int* g_expert, int* g_start, int* g_count,
+                            int* n_groups, int* mt_group, int* mt_row0, int* n_mtiles,
+                            hipStream_t s) {
+  const int E = d->n_experts, H = d->hidden;
+  const int e1 = E + (d->has_shared_gate ? 1 : 0);
+  const int has_shared = d->shared_inter > 0;
+  const size_t staged = (size_t)T * d->top_k * 8 + (size_t)T * 4;
+  int nw = 16;
+  while (nw > 1 && mx_dispatch_lds_bytes(nw, E) + staged > 60 * 1024) nw >>= 1;
+  const size_t lds = mx_dispatch_lds_bytes(nw, E) + staged;
+  if (T > 64 || lds > 60 * 1024 || E > 1024 || H % 4) return MX_ERR_UNSUPPORTED;
+  const uintptr_t walign = d->param_dtype == MX_DT_F16 ? 7u : 15u;
+  if (((uintptr_t)w->router_w & walign) || ((uintptr_t)w->shared_gate_w & walign) ||
+      !mx_aligned16(h32))
+    return MX_ERR_ALIGNMENT;
+  const void* b = (d->router_mode == MX_ROUTER_SOFTMAX || !d->has_bias) ? nullptr : w->bias;
+  const void* seg = d->has_shared_gate ? w->shared_gate_w : nullptr;
+  mx_clear_error();
+#define RL_LAUNCH(WT_, TT_)                                                                 \
+  hipLaunchKernelGGL((k_router_logits_decode<WT_, TT_>), dim3(e1), dim3(256), 0, s, h32,       \
+                     (const WT_*)w->router_w, (const WT_*)seg, T, H, E, e1, logits)
+#define RL_TT(WT_)                                  \
+  if (T <= 1) RL_LAUNCH(WT_, 1);                    \
+  else if (T <= 2) RL_LAUNCH(WT_, 2);               \
+  else if (T <= 4) RL_LAUNCH(WT_, 4);               \
+  else RL_LAUNCH(WT_, 8);
+  if (d->param_dtype == MX_DT_F16) {
+    RL_TT(half_t)
+  } else {
+    RL_TT(float)
+  }
+#undef RL_TT
+#undef RL_LAUNCH
+  MX_TRY(mx_launch_status());
+  const int vpt = mx_ceil_div(E, 64);
+#define TD_LAUNCH(V)                                                                           \
+  hipLaunchKernelGGL((k_topk_dispatch<V>), dim3(1), dim3(64 * nw), lds, s, logits, b,           \
+                     d->param_dtype, T, E, e1, d->top_k, d->router_mode, d->norm_topk_prob,     \
+                     d->routed_scaling, d->has_shared_gate, has_shared, m_blk, ids, tw,         \
+                     shared_w, counts, offsets, sorted_tok, sorted_w, pair_pos, g_expert,       \
+                     g_start, g_count, n_groups, mt_group, mt_row0, n_mtiles)
+  if (vpt <= 1) TD_LAUNCH(1);
+  else if (vpt <= 2) TD_LAUNCH(2);
+  else if (vpt <= 4) TD_LAUNCH(4);
+  else if (vpt <= 8) TD_LAUNCH(8);
+  else TD_LAUNCH(16);
+#undef TD_LAUNCH
   return mx_launch_status();
 }
