@@ -12,6 +12,100 @@ __device__ __forceinline__ void mx_lds_fence() {
   __builtin_amdgcn_wave_barrier();
 }
 
+// Three exclusive scans over experts by wave 0 of the block: rows (off), active flags
+// (gid) and m-tiles (mtb); totals into s_tot.  Callers synchronise before and after.
+__device__ __forceinline__ void mx_dispatch_scan(const int* tot, int* off, int* gid, int* mtb,
+                                                 int* s_tot, int E, int m_blk) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  // Three exclusive scans over experts by wave 0: rows, active flags, m-tiles.
+  if (w == 0) {
+    const int per = (E + 63) / 64;
+    const int beg = min(E, lane * per), end = min(E, beg + per);
+    int a = 0, b = 0, c = 0;
+    for (int e = beg; e < end; ++e) {
+      const int n = tot[e];
+      a += n;
+      b += n > 0;
+      c += (n + m_blk - 1) / m_blk;
+    }
+    int ia = a, ib = b, ic = c;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int xa = __shfl_up(ia, d, 64), xb = __shfl_up(ib, d, 64), xc = __shfl_up(ic, d, 64);
+      if (lane >= d) {
+        ia += xa;
+        ib += xb;
+        ic += xc;
+      }
+    }
+    int ea = ia - a, eb = ib - b, ec = ic - c;
+    for (int e = beg; e < end; ++e) {
+      const int n = tot[e];
+      off[e] = ea;
+      gid[e] = eb;
+      mtb[e] = ec;
+      ea += n;
+      eb += n > 0;
+      ec += (n + m_blk - 1) / m_blk;
+    }
+    if (lane == 63) {
+      s_tot[0] = ia;
+      s_tot[1] = ib;
+      s_tot[2] = ic;
+    }
+  }
+}
+
+// Offsets, group table, m-tile list and the shared-expert rows, from the scanned tables.
+__device__ __forceinline__ void mx_dispatch_tail(
+    const int* tot, const int* off, const int* gid, const int* mtb, const int* s_tot, int T,
+    int k, int E, int has_shared, int m_blk, const float* __restrict__ shw,
+    int* __restrict__ offsets, int* __restrict__ sorted_tok, float* __restrict__ sorted_w,
+    int* __restrict__ g_expert, int* __restrict__ g_start, int* __restrict__ g_count,
+    int* __restrict__ n_groups, int* __restrict__ mt_group, int* __restrict__ mt_row0,
+    int* __restrict__ n_mtiles) {
+  const int tid = threadIdx.x;
+  const int P = T * k;
+  for (int e = tid; e < E; e += blockDim.x) offsets[e] = off[e];
+  if (tid == 0) offsets[E] = s_tot[0];
+  // Group table and m-tile list.
+  const int G0 = has_shared ? 1 : 0;
+  const int S0 = has_shared ? (T + m_blk - 1) / m_blk : 0;
+  for (int e = tid; e < E; e += blockDim.x) {
+    const int n = tot[e];
+    if (n > 0) {
+      const int g = G0 + gid[e];
+      g_expert[g] = e;
+      g_start[g] = off[e];
+      g_count[g] = n;
+      const int nt = (n + m_blk - 1) / m_blk;
+      for (int i = 0; i < nt; ++i) {
+        mt_group[S0 + mtb[e] + i] = g;
+        mt_row0[S0 + mtb[e] + i] = i * m_blk;
+      }
+    }
+  }
+  if (has_shared) {
+    if (tid == 0) {
+      g_expert[0] = E;
+      g_start[0] = P;
+      g_count[0] = T;
+    }
+    for (int i = tid; i < S0; i += blockDim.x) {
+      mt_group[i] = 0;
+      mt_row0[i] = i * m_blk;
+    }
+    for (int t = tid; t < T; t += blockDim.x) {
+      sorted_tok[P + t] = t;
+      sorted_w[P + t] = shw ? shw[t] : 1.f;
+    }
+  }
+  if (tid == 0) {
+    *n_groups = G0 + s_tot[1];
+    *n_mtiles = S0 + s_tot[2];
+  }
+}
+
 // Whole-workgroup dispatch (every thread of the block must call it).  `smem` holds
 // mx_dispatch_lds_bytes(blockDim.x / 64, E) bytes.
 __device__ __forceinline__ void mx_dispatch_block(
@@ -54,46 +148,8 @@ __device__ __forceinline__ void mx_dispatch_block(
     counts[e] = run;
   }
   __syncthreads();
-  // Three exclusive scans over experts by wave 0: rows, active flags, m-tiles.
-  if (w == 0) {
-    const int per = (E + 63) / 64;
-    const int beg = min(E, lane * per), end = min(E, beg + per);
-    int a = 0, b = 0, c = 0;
-    for (int e = beg; e < end; ++e) {
-      const int n = tot[e];
-      a += n;
-      b += n > 0;
-      c += (n + m_blk - 1) / m_blk;
-    }
-    int ia = a, ib = b, ic = c;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const int xa = __shfl_up(ia, d, 64), xb = __shfl_up(ib, d, 64), xc = __shfl_up(ic, d, 64);
-      if (lane >= d) {
-        ia += xa;
-        ib += xb;
-        ic += xc;
-      }
-    }
-    int ea = ia - a, eb = ib - b, ec = ic - c;
-    for (int e = beg; e < end; ++e) {
-      const int n = tot[e];
-      off[e] = ea;
-      gid[e] = eb;
-      mtb[e] = ec;
-      ea += n;
-      eb += n > 0;
-      ec += (n + m_blk - 1) / m_blk;
-    }
-    if (lane == 63) {
-      s_tot[0] = ia;
-      s_tot[1] = ib;
-      s_tot[2] = ic;
-    }
-  }
+  mx_dispatch_scan(tot, off, gid, mtb, s_tot, E, m_blk);
   __syncthreads();
-  for (int e = tid; e < E; e += blockDim.x) offsets[e] = off[e];
-  if (tid == 0) offsets[E] = s_tot[0];
 
   // Stable positions: rounds of 64 tokens per wave, lane = token.
   unsigned long long* wm = mask + (size_t)w * E;
@@ -137,41 +193,8 @@ __device__ __forceinline__ void mx_dispatch_block(
   }
   __syncthreads();
 
-  // Group table and m-tile list.
-  const int G0 = has_shared ? 1 : 0;
-  const int S0 = has_shared ? (T + m_blk - 1) / m_blk : 0;
-  for (int e = tid; e < E; e += blockDim.x) {
-    const int n = tot[e];
-    if (n > 0) {
-      const int g = G0 + gid[e];
-      g_expert[g] = e;
-      g_start[g] = off[e];
-      g_count[g] = n;
-      const int nt = (n + m_blk - 1) / m_blk;
-      for (int i = 0; i < nt; ++i) {
-        mt_group[S0 + mtb[e] + i] = g;
-        mt_row0[S0 + mtb[e] + i] = i * m_blk;
-      }
-    }
-  }
-  if (has_shared) {
-    if (tid == 0) {
-      g_expert[0] = E;
-      g_start[0] = P;
-      g_count[0] = T;
-    }
-    for (int i = tid; i < S0; i += blockDim.x) {
-      mt_group[i] = 0;
-      mt_row0[i] = i * m_blk;
-    }
-    for (int t = tid; t < T; t += blockDim.x) {
-      sorted_tok[P + t] = t;
-      sorted_w[P + t] = shw ? shw[t] : 1.f;
-    }
-  }
-  if (tid == 0) {
-    *n_groups = G0 + s_tot[1];
-    *n_mtiles = S0 + s_tot[2];
-  }
+  mx_dispatch_tail(tot, off, gid, mtb, s_tot, T, k, E, has_shared, m_blk, shw, offsets,
+                   sorted_tok, sorted_w, g_expert, g_start, g_count, n_groups, mt_group, mt_row0,
+                   n_mtiles);
 }
 

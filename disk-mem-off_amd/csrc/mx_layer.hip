@@ -43,7 +43,8 @@ bool use_decode_router(const MxMoeDesc* d, int T) {
   return T <= 64 && d->n_experts <= 1024 && d->hidden % 4 == 0;
 }
 
-int layout(const MxMoeDesc* d, int T, void* ws, MxMoeViews* v, size_t* total) {
+int layout(const MxMoeDesc* d, int T, void* ws, MxMoeViews* v, size_t* total,
+           void** scratch = nullptr) {
   MX_TRY(check_desc(d));
   if (T < 0) return MX_ERR_INVALID;
   const int Tn = T > 0 ? T : 1;
@@ -81,13 +82,17 @@ int layout(const MxMoeDesc* d, int T, void* ws, MxMoeViews* v, size_t* total) {
   t.m_blk = m_blk;
   t.act = c.take(R * imax * aesz);
   t.y = (float*)c.take(R * H * 4);
+  size_t dscr = 0;
+  MX_TRY(mx_dispatch_scratch_size(Tn, d->top_k, d->n_experts, &dscr));
+  void* dispatch_scratch = c.take(dscr);
+  if (scratch) *scratch = dispatch_scratch;
   if (v) *v = t;
   if (total) *total = mx_align_up(c.off, 256);
   return MX_OK;
 }
 
 int run_stage(int stage, const MxMoeDesc* d, const MxMoeWeights* w, const float* x, float* out,
-              int T, const MxMoeViews& v, hipStream_t s) {
+              int T, const MxMoeViews& v, void* scratch, hipStream_t s) {
   const int has_sh = d->shared_inter > 0;
   const bool decode = use_decode_router(d, T);
   if (decode && (stage == 2 || stage == 3)) return MX_OK;  // done by the decode router (stage 1)
@@ -111,6 +116,12 @@ int run_stage(int stage, const MxMoeDesc* d, const MxMoeWeights* w, const float*
                             d->norm_topk_prob, d->routed_scaling, d->has_shared_gate, v.topk_ids,
                             v.topk_w, v.shared_w, s);
     case 3:
+      // Many-workgroup dispatch once the single workgroup's serial token walk dominates.
+      if (scratch && T >= 512 && d->n_experts * 48 <= 64 * 1024)
+        return mx_dispatch_chunked(v.topk_ids, v.topk_w, v.shared_w, T, d->top_k, d->n_experts,
+                                   has_sh, v.m_blk, scratch, v.counts, v.offsets, v.sorted_tok,
+                                   v.sorted_w, v.pair_pos, v.g_expert, v.g_start, v.g_count,
+                                   v.n_groups, v.mt_group, v.mt_row0, v.n_mtiles, s);
       return mx_dispatch(v.topk_ids, v.topk_w, v.shared_w, T, d->top_k, d->n_experts, has_sh,
                          v.m_blk, v.counts, v.offsets, v.sorted_tok, v.sorted_w, v.pair_pos,
                          v.g_expert, v.g_start, v.g_count, v.n_groups, v.mt_group, v.mt_row0,
@@ -140,11 +151,12 @@ int forward(const MxMoeDesc* d, const MxMoeWeights* w, const float* x, float* ou
   if (T == 0) return MX_OK;
   MxMoeViews v;
   size_t need = 0;
-  MX_TRY(layout(d, T, ws, &v, &need));
+  void* scratch = nullptr;
+  MX_TRY(layout(d, T, ws, &v, &need, &scratch));
   if (ws_bytes < need) return MX_ERR_WORKSPACE;
   for (int st = 0; st < MX_N_STAGES; ++st) {
     if (events) MX_TRY(mx_status(hipEventRecord((hipEvent_t)events[st], s)));
-    MX_TRY(run_stage(st, d, w, x, out, T, v, s));
+    MX_TRY(run_stage(st, d, w, x, out, T, v, scratch, s));
   }
   if (events) MX_TRY(mx_status(hipEventRecord((hipEvent_t)events[MX_N_STAGES], s)));
   return MX_OK;

@@ -120,6 +120,10 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                       c_void_p, c_void_p, c_void_p]),
     "mx_dispatch": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32,
                                    c_int32, c_int32] + [c_void_p] * 12 + [c_void_p]),
+    "mx_dispatch_scratch_size": (ctypes.c_int, [c_int32, c_int32, c_int32, P(c_size_t)]),
+    "mx_dispatch_chunked": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_int32, c_int32,
+                                           c_int32, c_int32, c_int32, c_void_p] +
+                            [c_void_p] * 12 + [c_void_p]),
     "mx_expert_gate_up": (ctypes.c_int, [P(MxMoeDesc), c_void_p, c_int32, c_void_p, c_void_p,
                                          c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                          c_void_p, c_int32, c_void_p, c_void_p]),

@@ -210,6 +210,19 @@ int mx_dispatch(const int32_t* topk_ids, const float* topk_w, const float* share
                 int32_t* g_count, int32_t* n_groups, int32_t* mt_group, int32_t* mt_row0,
                 int32_t* n_mtiles, void* stream);
 
+/* The same tables built by three launches (per-chunk counts and ranks over many
+ * workgroups, one scan workgroup, a placement pass): the large-batch form of mx_dispatch
+ * (glm4_moe.py:206-215).  `scratch` holds mx_dispatch_scratch_size() bytes; n_experts
+ * up to 1365 (MX_ERR_UNSUPPORTED above).                                               */
+int mx_dispatch_scratch_size(int32_t tokens, int32_t top_k, int32_t n_experts, size_t* nbytes);
+int mx_dispatch_chunked(const int32_t* topk_ids, const float* topk_w, const float* shared_w,
+                        int32_t tokens, int32_t top_k, int32_t n_experts, int32_t has_shared,
+                        int32_t m_blk, void* scratch, int32_t* counts, int32_t* offsets,
+                        int32_t* sorted_tok, float* sorted_w, int32_t* pair_pos,
+                        int32_t* g_expert, int32_t* g_start, int32_t* g_count,
+                        int32_t* n_groups, int32_t* mt_group, int32_t* mt_row0,
+                        int32_t* n_mtiles, void* stream);
+
 /* Grouped expert products over the dispatch tables (glm4_moe.py:218-224, :234-237):
  * gate/up: act[row] = silu(A[tok(row)] . Wg^T) * (A[tok(row)] . Wu^T)
  * down:    y[row]   = sorted_w[row] * (act[row] . Wd^T)

@@ -235,3 +235,69 @@ def test_zero_tokens_is_a_no_op(mi355x, stream):
         assert out.shape == (0, 64)
     finally:
         dl.close()
+
+
+# ---- dispatch: chunked (many workgroups) == single workgroup ---------------------------
+
+@pytest.mark.parametrize("T,k,E,m_blk", [(1000, 8, 160, 128), (4096, 10, 512, 128),
+                                         (300, 4, 24, 64), (257, 3, 8, 32)])
+def test_chunked_dispatch_matches_single_workgroup(mi355x, stream, T, k, E, m_blk):
+    say(f"[gpu] dispatch T={T} k={k} E={E}")
+    lib = _lib.load()
+    rng = np.random.default_rng(T + E)
+    # skewed expert popularity, distinct ids per token
+    p = rng.zipf(1.3, size=E * 4).astype(np.float64)[:E]
+    p = p / p.sum()
+    ids = np.stack([rng.choice(E, size=k, replace=False, p=p) for _ in range(T)]).astype(np.int32)
+    tw = rng.random((T, k)).astype(np.float32)
+    shw = rng.random(T).astype(np.float32)
+    P = T * k
+    R = P + T
+    mtmax = P // m_blk + min(P, E) + (T + m_blk - 1) // m_blk
+    sizes = {"counts": E, "offsets": E + 1, "sorted_tok": R, "sorted_w": R, "pair_pos": P,
+             "g_expert": E + 1, "g_start": E + 1, "g_count": E + 1, "n_groups": 1,
+             "mt_group": mtmax, "mt_row0": mtmax, "n_mtiles": 1}
+    n = ctypes.c_size_t()
+    assert lib.mx_dispatch_scratch_size(T, k, E, ctypes.byref(n)) == 0
+    bufs = []
+
+    def dev(nbytes):
+        b = mi355x.alloc_device(max(nbytes, 16))
+        bufs.append(b)
+        return b.handle
+
+    try:
+        d_ids, d_tw, d_sw = dev(ids.nbytes), dev(tw.nbytes), dev(shw.nbytes)
+        for h, a in ((d_ids, ids), (d_tw, tw), (d_sw, shw)):
+            mi355x.copy_h2d_ptr_async(h, a.ctypes.data, a.nbytes, stream)
+        scratch = dev(n.value)
+        outs = {}
+        for variant in ("single", "chunked"):
+            o = {name: dev(cnt * 4) for name, cnt in sizes.items()}
+            args = [o[name] for name in sizes]
+            if variant == "single":
+                rc = lib.mx_dispatch(d_ids, d_tw, d_sw, T, k, E, 1, m_blk, *args, stream)
+            else:
+                rc = lib.mx_dispatch_chunked(d_ids, d_tw, d_sw, T, k, E, 1, m_blk, scratch, *args,
+                                             stream)
+            assert rc == 0
+            mi355x.synchronize_stream(stream)
+            outs[variant] = {name: read_device(mi355x, o[name],
+                                               np.float32 if name == "sorted_w" else np.int32,
+                                               cnt, stream) for name, cnt in sizes.items()}
+        a, b = outs["single"], outs["chunked"]
+        ng, nm = int(a["n_groups"][0]), int(a["n_mtiles"][0])
+        assert ng == int(b["n_groups"][0]) and nm == int(b["n_mtiles"][0])
+        for name in ("counts", "offsets", "sorted_tok", "sorted_w", "pair_pos"):
+            assert np.array_equal(a[name], b[name]), name
+        for name in ("g_expert", "g_start", "g_count"):
+            assert np.array_equal(a[name][:ng], b[name][:ng]), name
+        for name in ("mt_group", "mt_row0"):
+            assert np.array_equal(a[name][:nm], b[name][:nm]), name
+        ref = orc.dispatch(ids, E)
+        assert np.array_equal(a["counts"], ref["counts"])
+        assert np.array_equal(a["sorted_tok"][:P], ref["sorted_tok"])
+        assert np.array_equal(a["pair_pos"].reshape(T, k), ref["pair_pos"])
+    finally:
+        for b in bufs:
+            mi355x.free_device(b)
