@@ -34,16 +34,39 @@ __device__ __forceinline__ float mx_load_param(const void* p, int dtype, int i) 
   return dtype == MX_DT_F16 ? (float)((const half_t*)p)[i] : ((const float*)p)[i];
 }
 
+// Wave reductions: DPP swaps inside each 16-lane row (quad pairs, quads, half-rows), then
+// the four row totals are read with v_readlane, so no step goes through LDS.  The result
+// is wave-uniform and bit-identical on every lane.  Callers must be converged.
+template <int CTRL>
+__device__ __forceinline__ float mx_dpp(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float mx_readlane(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+#define MX_DPP_XOR1 0xB1       // quad_perm [1,0,3,2]
+#define MX_DPP_XOR2 0x4E       // quad_perm [2,3,0,1]
+#define MX_DPP_HALF_MIRROR 0x141
+#define MX_DPP_MIRROR 0x140
+
 __device__ __forceinline__ float mx_wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, MX_WAVE);
-  return v;
+  v += mx_dpp<MX_DPP_XOR1>(v);
+  v += mx_dpp<MX_DPP_XOR2>(v);
+  v += mx_dpp<MX_DPP_HALF_MIRROR>(v);
+  v += mx_dpp<MX_DPP_MIRROR>(v);
+  return (mx_readlane(v, 0) + mx_readlane(v, 16)) + (mx_readlane(v, 32) + mx_readlane(v, 48));
 }
 
 __device__ __forceinline__ float mx_wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, MX_WAVE));
-  return v;
+  v = fmaxf(v, mx_dpp<MX_DPP_XOR1>(v));
+  v = fmaxf(v, mx_dpp<MX_DPP_XOR2>(v));
+  v = fmaxf(v, mx_dpp<MX_DPP_HALF_MIRROR>(v));
+  v = fmaxf(v, mx_dpp<MX_DPP_MIRROR>(v));
+  return fmaxf(fmaxf(mx_readlane(v, 0), mx_readlane(v, 16)),
+               fmaxf(mx_readlane(v, 32), mx_readlane(v, 48)));
 }
 
 // Reference silu: x / (1 + exp(-x))  (_common.py:83-84).

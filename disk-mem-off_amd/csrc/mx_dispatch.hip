@@ -50,7 +50,7 @@ extern "C" int mx_dispatch(const int32_t* topk_ids, const float* topk_w, const f
       !g_expert || !g_start || !g_count || !n_groups || !mt_group || !mt_row0 || !n_mtiles)
     return MX_ERR_INVALID;
   if (tokens < 0 || top_k < 1 || n_experts < 1 || m_blk < 1) return MX_ERR_INVALID;
-  if (n_experts > 2048) return MX_ERR_UNSUPPORTED;
+  if (n_experts > 2048 || top_k > MX_DISPATCH_MAXK) return MX_ERR_UNSUPPORTED;
   if ((long)tokens * top_k > (1l << 30)) return MX_ERR_UNSUPPORTED;
   int nw = 8;
   while (nw > 1 && mx_dispatch_lds_bytes(nw, n_experts) > 60 * 1024) nw >>= 1;
@@ -85,30 +85,40 @@ __global__ __launch_bounds__(256) void k_dispatch_count(const int* __restrict__ 
   int* wcnt = (int*)(mask + 4 * (size_t)E);               // [4][E]
   const int c = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   for (int i = tid; i < 4 * E; i += 256) wcnt[i] = 0;
-  __syncthreads();
+  mx_lds_sync();
   const int t = c * DC_TOK + w * 64 + lane;
   const bool v = t < T;
   unsigned long long* wm = mask + (size_t)w * E;
   int* wc = wcnt + w * E;
   const unsigned long long below = (1ull << lane) - 1ull;
-  for (int j = 0; j < k; ++j) {
-    const int e = v ? ids[t * k + j] : -1;
-    if ((unsigned)e < (unsigned)E) wm[e] = 0ull;
-  }
-  mx_lds_fence();
-  for (int j = 0; j < k; ++j) {
-    const int e = v ? ids[t * k + j] : -1;
-    if ((unsigned)e < (unsigned)E) atomicOr(&wm[e], 1ull << lane);
-  }
-  mx_lds_fence();
-  for (int j = 0; j < k; ++j) {  // one lane per (wave, expert) publishes the wave's count
-    const int e = v ? ids[t * k + j] : -1;
-    if ((unsigned)e < (unsigned)E) {
-      const unsigned long long m = ((volatile unsigned long long*)wm)[e];
-      if ((m & below) == 0ull) wc[e] = __popcll(m);
+  int ev[MX_DISPATCH_MAXK];
+#pragma unroll
+  for (int j = 0; j < MX_DISPATCH_MAXK; ++j) {
+    ev[j] = -1;
+    if (j < k) {
+      const int e = v ? ids[t * k + j] : -1;
+      ev[j] = (unsigned)e < (unsigned)E ? e : -1;
     }
   }
-  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < MX_DISPATCH_MAXK; ++j)
+    if (j < k && ev[j] >= 0) wm[ev[j]] = 0ull;
+  mx_lds_fence();
+#pragma unroll
+  for (int j = 0; j < MX_DISPATCH_MAXK; ++j)
+    if (j < k && ev[j] >= 0) atomicOr(&wm[ev[j]], 1ull << lane);
+  mx_lds_fence();
+  unsigned long long mv[MX_DISPATCH_MAXK];
+#pragma unroll
+  for (int j = 0; j < MX_DISPATCH_MAXK; ++j) {
+    mv[j] = 0ull;
+    if (j < k && ev[j] >= 0) mv[j] = wm[ev[j]];
+  }
+  // One lane per (wave, expert) publishes the wave's count.
+#pragma unroll
+  for (int j = 0; j < MX_DISPATCH_MAXK; ++j)
+    if (j < k && ev[j] >= 0 && (mv[j] & below) == 0ull) wc[ev[j]] = __popcll(mv[j]);
+  mx_lds_sync();
   for (int e = tid; e < E; e += 256) {
     int run = 0;
 #pragma unroll
@@ -119,15 +129,10 @@ __global__ __launch_bounds__(256) void k_dispatch_count(const int* __restrict__ 
     }
     chunk_counts[(size_t)c * E + e] = run;
   }
-  __syncthreads();
-  for (int j = 0; j < k; ++j) {
-    if (!v) break;
-    const int e = ids[t * k + j];
-    if ((unsigned)e < (unsigned)E) {
-      const unsigned long long m = ((volatile unsigned long long*)wm)[e];
-      rank[t * k + j] = wc[e] + __popcll(m & below);
-    }
-  }
+  mx_lds_sync();
+#pragma unroll
+  for (int j = 0; j < MX_DISPATCH_MAXK; ++j)
+    if (j < k && ev[j] >= 0) rank[t * k + j] = wc[ev[j]] + __popcll(mv[j] & below);
 }
 
 __global__ __launch_bounds__(1024) void k_dispatch_scan(
@@ -152,9 +157,9 @@ __global__ __launch_bounds__(1024) void k_dispatch_scan(
     tot[e] = run;
     counts[e] = run;
   }
-  __syncthreads();
+  mx_lds_sync();
   mx_dispatch_scan(tot, off, gid, mtb, s_tot, E, m_blk);
-  __syncthreads();
+  mx_lds_sync();
   mx_dispatch_tail(tot, off, gid, mtb, s_tot, T, k, E, has_shared, m_blk, shw, offsets,
                    sorted_tok, sorted_w, g_expert, g_start, g_count, n_groups, mt_group, mt_row0,
                    n_mtiles);
@@ -200,7 +205,7 @@ extern "C" int mx_dispatch_chunked(const int32_t* topk_ids, const float* topk_w,
       !n_mtiles)
     return MX_ERR_INVALID;
   if (tokens < 0 || top_k < 1 || n_experts < 1 || m_blk < 1) return MX_ERR_INVALID;
-  if (n_experts > 2048) return MX_ERR_UNSUPPORTED;
+  if (n_experts > 2048 || top_k > MX_DISPATCH_MAXK) return MX_ERR_UNSUPPORTED;
   if ((long)tokens * top_k > (1l << 30)) return MX_ERR_UNSUPPORTED;
   if ((size_t)n_experts * 48 > 64 * 1024) return MX_ERR_UNSUPPORTED;  // count-kernel LDS
   if (tokens == 0) return MX_OK;

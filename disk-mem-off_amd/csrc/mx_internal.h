@@ -18,11 +18,13 @@ int mx_m_blk_for(int tokens, int weight_dtype);
 int mx_rmsnorm_launch(const float* x, const void* norm_w, int param_dtype, float eps, int tokens,
                       int hidden, float* h32, void* h16, hipStream_t s);
 
-// Decode router (T <= 64): logits kernel + single-workgroup top-k/dispatch kernel;
-// MX_ERR_UNSUPPORTED outside its limits (T > 64, or dispatch tables beyond the LDS budget).
-int mx_router_decode_launch(const MxMoeDesc* d, const MxMoeWeights* w, int T, const float* h32,
-                            float* logits, int* ids, float* tw, float* shared_w, int m_blk,
-                            int* counts, int* offsets, int* sorted_tok, float* sorted_w,
-                            int* pair_pos, int* g_expert, int* g_start, int* g_count,
-                            int* n_groups, int* mt_group, int* mt_row0, int* n_mtiles,
-                            hipStream_t s);
+// Decode router (T <= 64): RMSNorm + logits kernel, then a single-workgroup
+// top-k/dispatch kernel.  mx_router_decode_ok tells whether the shape and the pointer
+// alignment fit it; the launch returns MX_ERR_UNSUPPORTED otherwise.
+bool mx_router_decode_ok(const MxMoeDesc* d, const MxMoeWeights* w, int T, const float* x);
+int mx_router_decode_launch(const MxMoeDesc* d, const MxMoeWeights* w, int T, const float* x,
+                            float* h32, void* h16, float* logits, int* ids, float* tw,
+                            float* shared_w, int m_blk, int* counts, int* offsets,
+                            int* sorted_tok, float* sorted_w, int* pair_pos, int* g_expert,
+                            int* g_start, int* g_count, int* n_groups, int* mt_group,
+                            int* mt_row0, int* n_mtiles, hipStream_t s);

@@ -37,10 +37,10 @@ int check_desc(const MxMoeDesc* d) {
   return MX_OK;
 }
 
-// Decode-sized batches run the decode router (logits, then top-k + dispatch in one
-// workgroup) in place of stages 1-3.
-bool use_decode_router(const MxMoeDesc* d, int T) {
-  return T <= 64 && d->n_experts <= 1024 && d->hidden % 4 == 0;
+// Decode-sized batches run the decode router (RMSNorm + logits, then top-k + dispatch in
+// one workgroup) in place of stages 0-3.
+bool use_decode_router(const MxMoeDesc* d, const MxMoeWeights* w, int T, const float* x) {
+  return mx_router_decode_ok(d, w, T, x);
 }
 
 int layout(const MxMoeDesc* d, int T, void* ws, MxMoeViews* v, size_t* total,
@@ -51,7 +51,7 @@ int layout(const MxMoeDesc* d, int T, void* ws, MxMoeViews* v, size_t* total,
   const size_t H = d->hidden, E = d->n_experts, k = d->top_k;
   const int e1 = d->n_experts + (d->has_shared_gate ? 1 : 0);
   const int has_sh = d->shared_inter > 0;
-  const int S = use_decode_router(d, Tn) ? 1 : mx_router_splits_for(Tn, d->hidden, e1);
+  const int S = mx_router_splits_for(Tn, d->hidden, e1);
   const int m_blk = mx_m_blk_for(Tn, d->weight_dtype);
   const size_t P = (size_t)Tn * k;
   const size_t R = P + (has_sh ? Tn : 0);
@@ -94,8 +94,8 @@ int layout(const MxMoeDesc* d, int T, void* ws, MxMoeViews* v, size_t* total,
 int run_stage(int stage, const MxMoeDesc* d, const MxMoeWeights* w, const float* x, float* out,
               int T, const MxMoeViews& v, void* scratch, hipStream_t s) {
   const int has_sh = d->shared_inter > 0;
-  const bool decode = use_decode_router(d, T);
-  if (decode && (stage == 2 || stage == 3)) return MX_OK;  // done by the decode router (stage 1)
+  const bool decode = use_decode_router(d, w, T, x);
+  if (decode && (stage == 0 || stage == 2 || stage == 3)) return MX_OK;  // in stage 1
   switch (stage) {
     case 0:
       if (!x || !w->norm_w) return MX_ERR_INVALID;
@@ -103,7 +103,7 @@ int run_stage(int stage, const MxMoeDesc* d, const MxMoeWeights* w, const float*
                                s);
     case 1:
       if (decode)
-        return mx_router_decode_launch(d, w, T, v.h32, v.logits, v.topk_ids, v.topk_w,
+        return mx_router_decode_launch(d, w, T, x, v.h32, v.h16, v.logits, v.topk_ids, v.topk_w,
                                        v.shared_w, v.m_blk, v.counts, v.offsets, v.sorted_tok,
                                        v.sorted_w, v.pair_pos, v.g_expert, v.g_start, v.g_count,
                                        v.n_groups, v.mt_group, v.mt_row0, v.n_mtiles, s);

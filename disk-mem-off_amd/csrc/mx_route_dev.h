@@ -4,6 +4,7 @@
 #include <math.h>
 
 #include "mx_common.h"
+#include "mx_dispatch_dev.h"
 
 #define TK_MAXK 32
 
@@ -15,25 +16,36 @@ __device__ __forceinline__ void mx_topk_token(
     int* __restrict__ ids, float* __restrict__ tw, float* __restrict__ shared_w,
     int* lds_ids = nullptr, float* lds_w = nullptr, float* lds_sw = nullptr) {
   const int lane = threadIdx.x & 63;
-  float key[VPT], wsrc[VPT];
-  bool taken[VPT];
+  // All logit and bias loads first, at clamped indices, so they are in flight together.
+  float lg[VPT], bs[VPT];
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
-    const int e = lane + 64 * i;
-    taken[i] = false;
-    key[i] = -INFINITY;
-    wsrc[i] = 0.f;
-    if (e < E) {
-      float l = 0.f;
-      for (int s = 0; s < S; ++s) l += logits[((size_t)s * T + t) * E1 + e];
-      const float b = bias ? mx_load_param(bias, pdt, e) : 0.f;
-      if (mode == MX_ROUTER_SIGMOID_SELECT_BIAS) {
-        const float sg = mx_sigmoid(l);
-        key[i] = sg + b;
-        wsrc[i] = sg;
-      } else {
-        key[i] = (mode == MX_ROUTER_REF_SOFTMAX_BIAS) ? l + b : l;
-      }
+    lg[i] = logits[(size_t)t * E1 + min(lane + 64 * i, E - 1)];
+    bs[i] = 0.f;
+  }
+  if (bias && pdt == MX_DT_F16) {
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) bs[i] = (float)((const half_t*)bias)[min(lane + 64 * i, E - 1)];
+  } else if (bias) {
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) bs[i] = ((const float*)bias)[min(lane + 64 * i, E - 1)];
+  }
+  for (int s = 1; s < S; ++s)
+#pragma unroll
+    for (int i = 0; i < VPT; ++i)
+      lg[i] += logits[((size_t)s * T + t) * E1 + min(lane + 64 * i, E - 1)];
+  float key[VPT], wsrc[VPT];
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const bool valid = lane + 64 * i < E;
+    const float l = lg[i];
+    if (mode == MX_ROUTER_SIGMOID_SELECT_BIAS) {
+      const float sg = mx_sigmoid(l);
+      key[i] = valid ? sg + bs[i] : -INFINITY;
+      wsrc[i] = valid ? sg : 0.f;
+    } else {
+      key[i] = valid ? ((mode == MX_ROUTER_REF_SOFTMAX_BIAS) ? l + bs[i] : l) : -INFINITY;
+      wsrc[i] = 0.f;
     }
   }
   if (mode != MX_ROUTER_SIGMOID_SELECT_BIAS) {
@@ -52,50 +64,78 @@ __device__ __forceinline__ void mx_topk_token(
 #pragma unroll
     for (int i = 0; i < VPT; ++i) wsrc[i] = wsrc[i] / sum;
   }
-#pragma unroll
-  for (int i = 0; i < VPT; ++i)
-    if (key[i] != key[i]) key[i] = -INFINITY;  // NaN never wins a slot
 
-  // Lane r keeps selection r (no dynamically indexed private arrays).
-  int my_id = 0;
-  float my_w = 0.f;
-  for (int r = 0; r < k; ++r) {
-    float bk = -INFINITY;
-    int bi = 0x7fffffff;
+  // Selection without a per-round arg-max.  Keys map to order-preserving 32-bit images
+  // (NaN counts as -inf, -0 as +0; 0 marks an absent expert).  A most-significant-bit-first
+  // search with wave ballots finds tau, the k-th largest image; every image above tau is
+  // taken, and the ties at tau in ascending expert id until k are filled.  A chosen
+  // expert's slot is the number of chosen experts ahead of it (larger key, or equal key
+  // and lower id), i.e. the order k rounds of arg-max with ties to the lower id give.
+  uint32_t u[VPT];
 #pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-      const int e = lane + 64 * i;
-      if (e < E && !taken[i] && (key[i] > bk || (key[i] == bk && e < bi))) {
-        bk = key[i];
-        bi = e;
-      }
-    }
+  for (int i = 0; i < VPT; ++i) {
+    float kv = key[i];
+    if (kv != kv) kv = -INFINITY;
+    if (kv == 0.f) kv = 0.f;
+    const uint32_t b = __builtin_bit_cast(uint32_t, kv);
+    u[i] = (lane + 64 * i < E) ? ((b & 0x80000000u) ? ~b : (b | 0x80000000u)) : 0u;
+  }
+  uint32_t tau = 0;
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cand = tau | (1u << bit);
+    unsigned long long m[VPT];  // all compares first: independent mask registers
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-      const float ok = __shfl_xor(bk, m, 64);
-      const int oi = __shfl_xor(bi, m, 64);
-      if (ok > bk || (ok == bk && oi < bi)) {
-        bk = ok;
-        bi = oi;
-      }
-    }
-    const int wl = bi & 63, wi = bi >> 6;
-    float mine = 0.f;
+    for (int i = 0; i < VPT; ++i) m[i] = __builtin_amdgcn_uicmp(u[i], cand, 35 /* uge */);
+    int c = 0;
 #pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-      if (i == wi) {
-        mine = wsrc[i];
-        if (lane == wl) taken[i] = true;
-      }
-    }
-    const float w = __shfl(mine, wl, 64);
-    if (lane == r) {
-      my_id = bi;
-      my_w = w;
+    for (int i = 0; i < VPT; ++i) c += __popcll(m[i]);
+    if (c >= k) tau = cand;
+  }
+  const unsigned long long below = (1ull << lane) - 1ull;
+  int ngt = 0;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) ngt += __popcll(__ballot(u[i] > tau));
+  bool sel[VPT];
+  int ties = 0;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const unsigned long long eq = __ballot(u[i] == tau);
+    sel[i] = u[i] > tau || (u[i] == tau && ties + __popcll(eq & below) < k - ngt);
+    ties += __popcll(eq);
+  }
+  int rank[VPT];
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) rank[i] = 0;
+#pragma unroll
+  for (int iy = 0; iy < VPT; ++iy) {
+    unsigned long long m = __ballot(sel[iy]);
+    while (m) {
+      const int ly = __builtin_ctzll(m);
+      m &= m - 1ull;
+      const uint32_t uy = (uint32_t)__builtin_amdgcn_readlane((int)u[iy], ly);
+      const int ey = ly + 64 * iy;
+#pragma unroll
+      for (int i = 0; i < VPT; ++i)
+        rank[i] += (uy > u[i] || (uy == u[i] && ey < lane + 64 * i)) ? 1 : 0;
     }
   }
+  // Chosen experts land in their slots of a per-wave LDS row; lane r then owns slot r.
+  __shared__ int s_id[16][TK_MAXK];
+  __shared__ float s_w[16][TK_MAXK];
+  const int wv = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    if (sel[i]) {
+      s_id[wv][rank[i]] = lane + 64 * i;
+      s_w[wv][rank[i]] = wsrc[i];
+    }
+  }
+  mx_lds_fence();
+  const int my_id = lane < k ? s_id[wv][lane] : 0;
+  const float my_w = lane < k ? s_w[wv][lane] : 0.f;
+  mx_lds_fence();  // the row is reused by this wave's next token
   float sum = 0.f;  // sequential over the k slots, identical on every lane
-  for (int r = 0; r < k; ++r) sum += __shfl(my_w, r, 64);
+  for (int r = 0; r < k; ++r) sum += mx_readlane(my_w, r);
   if (lane < k) {
     const float w = (norm ? my_w / (sum + 1e-20f) : my_w) * scaling;
     ids[(size_t)t * k + lane] = my_id;
@@ -119,5 +159,3 @@ __device__ __forceinline__ void mx_topk_token(
   }
 }
 
-
-#include "mx_dispatch_dev.h"

@@ -283,73 +283,115 @@ extern "C" int mx_router_topk(const float* logits, int32_t splits, const void* b
                      (int)has_shared_gate, topk_ids, topk_w, shared_w)
   if (vpt <= 1) TK_LAUNCH(1);
   else if (vpt <= 2) TK_LAUNCH(2);
+  else if (vpt <= 3) TK_LAUNCH(3);
   else if (vpt <= 4) TK_LAUNCH(4);
+  else if (vpt <= 6) TK_LAUNCH(6);
   else if (vpt <= 8) TK_LAUNCH(8);
+  else if (vpt <= 12) TK_LAUNCH(12);
   else TK_LAUNCH(16);
 #undef TK_LAUNCH
   return mx_launch_status();
 }
 
 // ------------------------------------------------------------------------------------
-// Decode router (T <= 64): two launches.
-//   k_router_logits_decode: one wave per expert (expert E = Qwen3-Next shared gate row),
-//     all T tokens in tiles of RT_TT over the full H (no H split), branch-free loads.
-//   k_topk_dispatch: one workgroup of 8 waves; per-token top-k (one wave per token), then
-//     the dispatch.  A kernel boundary separates the two: the blocks of the logits kernel
-//     run on every XCD, and publishing their results inside one launch would need an L2
-//     write-back per block.
+// Decode router (T <= 64): two launches, the RMSNorm folded into the first.
+//   k_router_logits_decode: one block per (expert row, group of up to 8 tokens) over the
+//     full H (no H split); also writes the normalised activations.
+//   k_topk_dispatch: one workgroup of up to 16 waves; per-token top-k (one wave per
+//     token), then the dispatch.  A kernel boundary separates the two: the blocks of the
+//     logits kernel run on every XCD, and publishing their results inside one launch
+//     would need an L2 write-back per block.
 // ------------------------------------------------------------------------------------
-// One block per expert row (row E = Qwen3-Next shared gate); the 4 waves split H into
-// quarters, each lane keeps TT token partials, and the quarters are added in LDS in a
-// fixed order.  Every load of a wave is issued before the first FMA needs it.
+// Block (e, g): expert row e (row E = Qwen3-Next shared gate) against tokens g*TT ..
+// g*TT+TT-1, with the RMSNorm folded in: each lane accumulates x . (norm_w * w_e) and
+// x . x over its H columns, the 4 waves (H quarters) are added in LDS in a fixed order,
+// and logit = dot / rms with rms = sqrt(mean(x^2) + eps) (_common.py:73-75).  The blocks
+// also write the normalised rows h = norm_w * (x / rms) (fp32, and fp16 when h16 is
+// given) for the expert kernels.  Rows past the last token re-read the last token
+// (results discarded), so the loop body is branch-free and its loads issue together.
+// At most 2 waves per SIMD: the register budget lets every load of a loop step be
+// issued before the first FMA waits (at the default occupancy target the compiler
+// serialises load -> wait -> FMA per token row).
 template <typename WT, int TT>
-__global__ __launch_bounds__(256) void k_router_logits_decode(
-    const float* __restrict__ h32, const WT* __restrict__ wr, const WT* __restrict__ wseg, int T,
-    int H, int E, int E1, float* __restrict__ logits) {
-  __shared__ float part[4][TT];
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void
+k_router_logits_decode(
+    const float* __restrict__ x, const WT* __restrict__ norm_w, float eps,
+    const WT* __restrict__ wr, const WT* __restrict__ wseg, int T, int H, int E, int E1,
+    float* __restrict__ logits, float* __restrict__ h32, half_t* __restrict__ h16) {
+  __shared__ float part[4][TT], sq[4][TT];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int e = blockIdx.x;
+  const int t0 = blockIdx.y * TT;
   const WT* row = (e < E) ? wr + (size_t)e * H : wseg;
   const int hq = (H / 4 + 255) / 256 * 256;  // H quarter per wave, in 256-element sweeps
   const int kb = wave * hq, ke = min(H, kb + hq);
-  for (int t0 = 0; t0 < T; t0 += TT) {
-    float acc[TT];
-    const float* hrow[TT];
+  float acc[TT], ss[TT];
+  const float* xrow[TT];
+#pragma unroll
+  for (int t = 0; t < TT; ++t) {
+    acc[t] = 0.f;
+    ss[t] = 0.f;
+    xrow[t] = x + (size_t)min(t0 + t, T - 1) * H;
+  }
+#pragma unroll 4
+  for (int c = kb + lane * 4; c < ke; c += RT_KCH) {
+    const float4 wv = rt_load4<WT>(row + c);
+    const float4 nv = rt_load4<WT>(norm_w + c);
+    const float4 g = make_float4(nv.x * wv.x, nv.y * wv.y, nv.z * wv.z, nv.w * wv.w);
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
-      acc[t] = 0.f;
-      hrow[t] = h32 + (size_t)min(t0 + t, T - 1) * H;  // past-the-end rows: discarded
+      const float4 xv = *(const float4*)(xrow[t] + c);
+      float a = acc[t], q = ss[t];
+      a = fmaf(xv.x, g.x, a);
+      q = fmaf(xv.x, xv.x, q);
+      a = fmaf(xv.y, g.y, a);
+      q = fmaf(xv.y, xv.y, q);
+      a = fmaf(xv.z, g.z, a);
+      q = fmaf(xv.z, xv.z, q);
+      a = fmaf(xv.w, g.w, a);
+      q = fmaf(xv.w, xv.w, q);
+      acc[t] = a;
+      ss[t] = q;
     }
-#pragma unroll 8
-    for (int c = kb + lane * 4; c < ke; c += RT_KCH) {
-      const float4 wv = rt_load4<WT>(row + c);
+  }
 #pragma unroll
-      for (int t = 0; t < TT; ++t) {
-        const float4 hv = *(const float4*)(hrow[t] + c);
-        float a = acc[t];
-        a = fmaf(hv.x, wv.x, a);
-        a = fmaf(hv.y, wv.y, a);
-        a = fmaf(hv.z, wv.z, a);
-        a = fmaf(hv.w, wv.w, a);
-        acc[t] = a;
-      }
+  for (int t = 0; t < TT; ++t) {
+    const float v = mx_wave_sum(acc[t]);
+    const float q = mx_wave_sum(ss[t]);
+    if (lane == 0) {
+      part[wave][t] = v;
+      sq[wave][t] = q;
     }
-#pragma unroll
-    for (int t = 0; t < TT; ++t) {
-      const float v = mx_wave_sum(acc[t]);
-      if (lane == 0) part[wave][t] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x < TT && t0 + (int)threadIdx.x < T) {
+    const int t = threadIdx.x;
+    const float rms = sqrtf(((sq[0][t] + sq[1][t]) + (sq[2][t] + sq[3][t])) / (float)H + eps);
+    logits[(size_t)(t0 + t) * E1 + e] = ((part[0][t] + part[1][t]) + (part[2][t] + part[3][t])) / rms;
+  }
+  // Normalised rows of this token group, spread over all blocks of the group: one
+  // float4 per thread (the x reads hit L2).  Every block reduced the same values in the
+  // same order, so all of them hold the same rms.
+  const int ng = min(TT, T - t0), h4 = H / 4;
+  for (int i = e * 256 + (int)threadIdx.x; i < ng * h4; i += E1 * 256) {
+    const int t = i / h4, c = (i - t * h4) * 4;
+    const float rms = sqrtf(((sq[0][t] + sq[1][t]) + (sq[2][t] + sq[3][t])) / (float)H + eps);
+    const size_t o = (size_t)(t0 + t) * H + c;
+    const float4 xv = *(const float4*)(x + o);
+    const float4 nv = rt_load4<WT>(norm_w + c);
+    const float4 hv = make_float4(nv.x * (xv.x / rms), nv.y * (xv.y / rms), nv.z * (xv.z / rms),
+                                  nv.w * (xv.w / rms));
+    *(float4*)(h32 + o) = hv;
+    if (h16) {
+      typedef _Float16 h4v __attribute__((ext_vector_type(4)));
+      *(h4v*)(h16 + o) = (h4v){(half_t)hv.x, (half_t)hv.y, (half_t)hv.z, (half_t)hv.w};
     }
-    __syncthreads();
-    if (threadIdx.x < TT && t0 + (int)threadIdx.x < T) {
-      const int t = threadIdx.x;
-      logits[(size_t)(t0 + t) * E1 + e] = (part[0][t] + part[1][t]) + (part[2][t] + part[3][t]);
-    }
-    __syncthreads();
   }
 }
 
+// 16 waves; 8 for E > 512 (the wider selection state needs the larger register budget).
 template <int VPT>
-__global__ __launch_bounds__(1024) void k_topk_dispatch(
+__global__ __launch_bounds__(VPT > 8 ? 512 : 1024) void k_topk_dispatch(
     const float* __restrict__ logits, const void* __restrict__ bias, int pdt, int T, int E,
     int E1, int k, int mode, int norm, float scaling, int has_seg, int has_shared, int m_blk,
     int* __restrict__ ids, float* __restrict__ tw, float* __restrict__ shared_w,
@@ -361,43 +403,53 @@ __global__ __launch_bounds__(1024) void k_topk_dispatch(
   // weights) so the dispatch phases never go back to global memory.
   extern __shared__ __align__(16) unsigned char smem[];
   const int nw = blockDim.x >> 6;
-  unsigned char* stage = smem + mx_dispatch_lds_bytes(nw, E);
+  unsigned char* stage = smem + mx_dispatch_small_lds_bytes(E);
   int* sid = (int*)stage;
   float* sw = (float*)(sid + T * k);
   float* ssw = sw + T * k;
   for (int t = threadIdx.x >> 6; t < T; t += nw)
     mx_topk_token<VPT>(logits, 1, T, t, bias, pdt, E, E1, k, mode, norm, scaling, has_seg, ids,
                        tw, shared_w, sid, sw, ssw);
-  __syncthreads();
-  mx_dispatch_block(smem, sid, sw, shared_w ? ssw : nullptr, T, k, E, has_shared, m_blk, counts,
-                    offsets, sorted_tok, sorted_w, pair_pos, g_expert, g_start, g_count, n_groups,
-                    mt_group, mt_row0, n_mtiles);
+  mx_lds_sync();
+  mx_dispatch_block_small(smem, sid, sw, shared_w ? ssw : nullptr, T, k, E, has_shared, m_blk,
+                          counts, offsets, sorted_tok, sorted_w, pair_pos, g_expert, g_start,
+                          g_count, n_groups, mt_group, mt_row0, n_mtiles);
 }
 
-int mx_router_decode_launch(const MxMoeDesc* d, const MxMoeWeights* w, int T, const float* h32,
-                            float* logits, int* ids, float* tw, float* shared_w, int m_blk,
-                            int* counts, int* offsets, int* sorted_tok, float* sorted_w,
-                            int* pair_pos, int* g_expert, int* g_start, int* g_count,
-                            int* n_groups, int* mt_group, int* mt_row0, int* n_mtiles,
-                            hipStream_t s) {
+// Dynamic LDS of the top-k/dispatch workgroup: dispatch tables, then the staged top-k
+// results (the top-k rows take 4 KB of static LDS besides).
+static size_t decode_lds_bytes(const MxMoeDesc* d, int T) {
+  return mx_dispatch_small_lds_bytes(d->n_experts) + (size_t)T * d->top_k * 8 + (size_t)T * 4;
+}
+
+bool mx_router_decode_ok(const MxMoeDesc* d, const MxMoeWeights* w, int T, const float* x) {
+  const uintptr_t walign = d->param_dtype == MX_DT_F16 ? 7u : 15u;
+  return T >= 1 && T <= 64 && d->n_experts <= 1024 && d->top_k <= MX_DISPATCH_MAXK &&
+         d->hidden % 4 == 0 && decode_lds_bytes(d, T) <= 56 * 1024 && mx_aligned16(x) && !((uintptr_t)w->norm_w & walign) &&
+         !((uintptr_t)w->router_w & walign) && !((uintptr_t)w->shared_gate_w & walign);
+}
+
+int mx_router_decode_launch(const MxMoeDesc* d, const MxMoeWeights* w, int T, const float* x,
+                            float* h32, void* h16, float* logits, int* ids, float* tw,
+                            float* shared_w, int m_blk, int* counts, int* offsets,
+                            int* sorted_tok, float* sorted_w, int* pair_pos, int* g_expert,
+                            int* g_start, int* g_count, int* n_groups, int* mt_group,
+                            int* mt_row0, int* n_mtiles, hipStream_t s) {
   const int E = d->n_experts, H = d->hidden;
   const int e1 = E + (d->has_shared_gate ? 1 : 0);
   const int has_shared = d->shared_inter > 0;
-  const size_t staged = (size_t)T * d->top_k * 8 + (size_t)T * 4;
-  int nw = 16;
-  while (nw > 1 && mx_dispatch_lds_bytes(nw, E) + staged > 60 * 1024) nw >>= 1;
-  const size_t lds = mx_dispatch_lds_bytes(nw, E) + staged;
-  if (T > 64 || lds > 60 * 1024 || E > 1024 || H % 4) return MX_ERR_UNSUPPORTED;
-  const uintptr_t walign = d->param_dtype == MX_DT_F16 ? 7u : 15u;
-  if (((uintptr_t)w->router_w & walign) || ((uintptr_t)w->shared_gate_w & walign) ||
-      !mx_aligned16(h32))
-    return MX_ERR_ALIGNMENT;
+  if (!mx_router_decode_ok(d, w, T, x)) return MX_ERR_UNSUPPORTED;
+  const int vpt = mx_ceil_div(E, 64);
+  const int nw = vpt > 8 ? 8 : 16;
+  const size_t lds = decode_lds_bytes(d, T);
+  if (!mx_aligned16(h32) || ((uintptr_t)h16 & 7u)) return MX_ERR_ALIGNMENT;
   const void* b = (d->router_mode == MX_ROUTER_SOFTMAX || !d->has_bias) ? nullptr : w->bias;
   const void* seg = d->has_shared_gate ? w->shared_gate_w : nullptr;
   mx_clear_error();
-#define RL_LAUNCH(WT_, TT_)                                                                 \
-  hipLaunchKernelGGL((k_router_logits_decode<WT_, TT_>), dim3(e1), dim3(256), 0, s, h32,       \
-                     (const WT_*)w->router_w, (const WT_*)seg, T, H, E, e1, logits)
+#define RL_LAUNCH(WT_, TT_)                                                                    \
+  hipLaunchKernelGGL((k_router_logits_decode<WT_, TT_>), dim3(e1, mx_ceil_div(T, TT_)),        \
+                     dim3(256), 0, s, x, (const WT_*)w->norm_w, d->eps, (const WT_*)w->router_w, \
+                     (const WT_*)seg, T, H, E, e1, logits, h32, (half_t*)h16)
 #define RL_TT(WT_)                                  \
   if (T <= 1) RL_LAUNCH(WT_, 1);                    \
   else if (T <= 2) RL_LAUNCH(WT_, 2);               \
@@ -411,7 +463,6 @@ int mx_router_decode_launch(const MxMoeDesc* d, const MxMoeWeights* w, int T, co
 #undef RL_TT
 #undef RL_LAUNCH
   MX_TRY(mx_launch_status());
-  const int vpt = mx_ceil_div(E, 64);
 #define TD_LAUNCH(V)                                                                           \
   hipLaunchKernelGGL((k_topk_dispatch<V>), dim3(1), dim3(64 * nw), lds, s, logits, b,           \
                      d->param_dtype, T, E, e1, d->top_k, d->router_mode, d->norm_topk_prob,     \
@@ -420,8 +471,11 @@ int mx_router_decode_launch(const MxMoeDesc* d, const MxMoeWeights* w, int T, co
                      g_start, g_count, n_groups, mt_group, mt_row0, n_mtiles)
   if (vpt <= 1) TD_LAUNCH(1);
   else if (vpt <= 2) TD_LAUNCH(2);
+  else if (vpt <= 3) TD_LAUNCH(3);
   else if (vpt <= 4) TD_LAUNCH(4);
+  else if (vpt <= 6) TD_LAUNCH(6);
   else if (vpt <= 8) TD_LAUNCH(8);
+  else if (vpt <= 12) TD_LAUNCH(12);
   else TD_LAUNCH(16);
 #undef TD_LAUNCH
   return mx_launch_status();
