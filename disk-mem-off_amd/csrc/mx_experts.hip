@@ -6,11 +6,12 @@
 //
 // Work decomposition.  The dispatch kernel cuts every group (one expert's rows in the
 // expert-sorted order) into m-tiles of m_blk = 16*MT rows.  Block (x, y) takes m-tile x
-// and four consecutive 16*NBI-column slabs of the output, one per wave.  Each wave owns
-// its output columns outright, so waves never synchronise and no LDS is used: every
-// weight row is streamed from HBM exactly once per m-tile with 16-byte buffer loads
-// (out-of-range lanes read zero through the buffer descriptor's bounds check) and fed
-// straight into MFMA B-operand registers.
+// and 4/KS consecutive 16*NBI-column slabs of the output; the KS waves of a slab split
+// the reduction and add their partial tiles through LDS at the end (KS = 1: each wave
+// owns its columns outright and no LDS is used).  Every weight row is streamed from HBM
+// exactly once per m-tile with 16-byte buffer loads (out-of-range lanes read zero
+// through the buffer descriptor's bounds check) and fed straight into MFMA B-operand
+// registers.
 //
 // Fragment layout (16x16 output tile, lane = 16*q + j):
 //   B operand: lane holds EPL consecutive elements of weight row n0+j at column
@@ -90,14 +91,17 @@ struct ExpertParams {
   int N_s, K_s;           // shared expert
 };
 
-template <int WF, int MT, int NBI, bool GU, int UK>
+template <int WF, int MT, int NBI, bool GU, int UK, int KS>
 __global__ __launch_bounds__(256) void k_expert(const ExpertParams p) {
   using Tr = WTr<WF>;
   constexpr int EPL = Tr::EPL, ESZ = Tr::ESZ, AESZ = Tr::AESZ, AV = Tr::AV;
   constexpr int KC = 4 * EPL;          // reduction columns per chunk (per wave)
   constexpr int NF = GU ? 2 * NBI : NBI;
+  constexpr int SPB = 4 / KS;          // column slabs per block; KS waves share a slab
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int slab = wave / KS, ks = wave % KS;
   const int mt = blockIdx.x;
   if (mt >= *p.n_mtiles) return;
   const int g = p.mt_group[mt];
@@ -108,8 +112,9 @@ __global__ __launch_bounds__(256) void k_expert(const ExpertParams p) {
   const bool sh = eid == p.E;
   const int N = sh ? p.N_s : p.N_r;
   const int K = sh ? p.K_s : p.K_r;
-  const int n0 = (blockIdx.y * 4 + wave) * 16 * NBI;
-  if (n0 >= N) return;
+  if ((int)blockIdx.y * SPB * 16 * NBI >= N) return;  // whole block past this expert
+  const int n0 = (blockIdx.y * SPB + slab) * 16 * NBI;
+  const bool wact = n0 < N;  // a wave without columns computes zeros and stores nothing
   const int mrows = min(16 * MT, gcount - row0);
   const int j = lane & 15, q = lane >> 4;
   const MxExpertPtrs ep = p.experts[eid];
@@ -143,6 +148,11 @@ __global__ __launch_bounds__(256) void k_expert(const ExpertParams p) {
   for (int mi = 0; mi < MT; ++mi)
 #pragma unroll
     for (int f = 0; f < NF; ++f) acc[mi][f] = (float4_t){0.f, 0.f, 0.f, 0.f};
+
+  // This wave's chunks: [cb, ce) of the ceil(K / KC) chunks (K split KS ways in the block).
+  const int nchunks = (K + KC - 1) / KC;
+  const int cps = (nchunks + KS - 1) / KS;
+  const int cb = min(nchunks, ks * cps), ce = min(nchunks, cb + cps);
 
   // One chunk of loads.  kin = false turns the lane's loads into zero reads (K tail).
   auto load_chunk = [&](int c, bool kin, int4_t (&b)[NF], int4_t (&a)[MT][AV]) {
@@ -198,56 +208,82 @@ __global__ __launch_bounds__(256) void k_expert(const ExpertParams p) {
 
   // Full chunks in batches of UK, ping-ponging two register sets so the loads of batch
   // i+1 are in flight while batch i runs on the MFMA pipe.
-  const int nfull = K / KC;
+  const int nfull = max(0, min(ce, K / KC) - cb);
   const int nbatch = nfull / UK;
   int4_t bx[UK][NF], ax[UK][MT][AV], by[UK][NF], ay[UK][MT][AV];
   if (nbatch > 0) {
 #pragma unroll
-    for (int u = 0; u < UK; ++u) load_chunk(u, true, bx[u], ax[u]);
+    for (int u = 0; u < UK; ++u) load_chunk(cb + u, true, bx[u], ax[u]);
   }
   for (int bt = 0; bt < nbatch; bt += 2) {
     if (bt + 1 < nbatch) {
 #pragma unroll
-      for (int u = 0; u < UK; ++u) load_chunk((bt + 1) * UK + u, true, by[u], ay[u]);
+      for (int u = 0; u < UK; ++u) load_chunk(cb + (bt + 1) * UK + u, true, by[u], ay[u]);
     }
 #pragma unroll
     for (int u = 0; u < UK; ++u) mma_chunk(bx[u], ax[u]);
     if (bt + 1 < nbatch) {
       if (bt + 2 < nbatch) {
 #pragma unroll
-        for (int u = 0; u < UK; ++u) load_chunk((bt + 2) * UK + u, true, bx[u], ax[u]);
+        for (int u = 0; u < UK; ++u) load_chunk(cb + (bt + 2) * UK + u, true, bx[u], ax[u]);
       }
 #pragma unroll
       for (int u = 0; u < UK; ++u) mma_chunk(by[u], ay[u]);
     }
   }
-  // Remaining chunks (fewer than UK full ones, then a partial one).
-  const int nchunks = (K + KC - 1) / KC;
-  for (int c = nbatch * UK; c < nchunks; ++c) {
+  // Remaining chunks of the range (fewer than UK full ones, then a partial one).
+  for (int c = cb + nbatch * UK; c < ce; ++c) {
     const bool kin = c * KC + q * EPL < K;
     load_chunk(c, kin, bx[0], ax[0]);
     mma_chunk(bx[0], ax[0]);
   }
 
-  // Epilogue.
+  // K split: the waves of a slab add their partial tiles in a fixed order.
+  if constexpr (KS > 1) {
+    __shared__ float4_t red[4][MT * NF][64];
+    if (ks > 0) {
+#pragma unroll
+      for (int mi = 0; mi < MT; ++mi)
+#pragma unroll
+        for (int f = 0; f < NF; ++f) red[wave][mi * NF + f][lane] = acc[mi][f];
+    }
+    __syncthreads();
+    if (ks > 0) return;
+#pragma unroll
+    for (int s2 = 1; s2 < KS; ++s2)
+#pragma unroll
+      for (int mi = 0; mi < MT; ++mi)
+#pragma unroll
+        for (int f = 0; f < NF; ++f) acc[mi][f] += red[wave + s2][mi * NF + f][lane];
+  }
+  if (!wact) return;
+
+  // Epilogue.  Scales and routing weights are loaded first, at clamped indices, so the
+  // loads are in flight together rather than one per predicated store.
   if constexpr (GU) {
+    float sg[NBI], su[NBI];
+#pragma unroll
+    for (int f = 0; f < NBI; ++f) {
+      sg[f] = 1.f;
+      su[f] = 1.f;
+      if constexpr (WF == MX_DT_I8) {
+        const int n = min(n0 + 16 * f + j, N - 1);
+        sg[f] = (float)((const half_t*)ep.gate_scale)[n];
+        su[f] = (float)((const half_t*)ep.up_scale)[n];
+      }
+    }
 #pragma unroll
     for (int f = 0; f < NBI; ++f) {
       const int n = n0 + 16 * f + j;
       if (n >= N) continue;
-      float sg = 1.f, su = 1.f;
-      if constexpr (WF == MX_DT_I8) {
-        sg = (float)((const half_t*)ep.gate_scale)[n];
-        su = (float)((const half_t*)ep.up_scale)[n];
-      }
 #pragma unroll
       for (int mi = 0; mi < MT; ++mi)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int m = 16 * mi + 4 * q + r;
           if (m < mrows) {
-            const float gv = acc[mi][f][r] * sg;
-            const float uv = acc[mi][NBI + f][r] * su;
+            const float gv = acc[mi][f][r] * sg[f];
+            const float uv = acc[mi][NBI + f][r] * su[f];
             const float av = mx_silu(gv) * uv;
             const size_t o = (size_t)(gstart + row0 + m) * p.ldo + n;
             if constexpr (WF == MX_DT_F32)
@@ -258,12 +294,22 @@ __global__ __launch_bounds__(256) void k_expert(const ExpertParams p) {
         }
     }
   } else {
+    float sd[NBI], wr[MT][4];
+#pragma unroll
+    for (int f = 0; f < NBI; ++f) {
+      sd[f] = 1.f;
+      if constexpr (WF == MX_DT_I8)
+        sd[f] = (float)((const half_t*)ep.down_scale)[min(n0 + 16 * f + j, N - 1)];
+    }
+#pragma unroll
+    for (int mi = 0; mi < MT; ++mi)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        wr[mi][r] = p.sorted_w[gstart + row0 + min(16 * mi + 4 * q + r, mrows - 1)];
 #pragma unroll
     for (int f = 0; f < NBI; ++f) {
       const int n = n0 + 16 * f + j;
       if (n >= N) continue;
-      float sd = 1.f;
-      if constexpr (WF == MX_DT_I8) sd = (float)((const half_t*)ep.down_scale)[n];
 #pragma unroll
       for (int mi = 0; mi < MT; ++mi)
 #pragma unroll
@@ -271,7 +317,7 @@ __global__ __launch_bounds__(256) void k_expert(const ExpertParams p) {
           const int m = 16 * mi + 4 * q + r;
           if (m < mrows) {
             const int row = gstart + row0 + m;
-            ((float*)p.out)[(size_t)row * p.ldo + n] = p.sorted_w[row] * (acc[mi][f][r] * sd);
+            ((float*)p.out)[(size_t)row * p.ldo + n] = wr[mi][r] * (acc[mi][f][r] * sd[f]);
           }
         }
     }
@@ -568,24 +614,48 @@ static int expert_check(const MxMoeDesc* d) {
 #define MX_DEC_UK 4
 #endif
 
-template <int WF, int MT, bool GU>
-static void launch_expert(const ExpertParams& p, dim3 grid, hipStream_t s) {
+// K split inside a block for single-m-frag tiles (m_blk 16).  The split is picked from
+// the number of waves the launch would have unsplit (measured on MI355X, fp16 GLM-4.7 and
+// Qwen3-Next shapes at 1-8 tokens): a launch far below one wave per SIMD gains from more,
+// shorter weight streams; one near a wave per SIMD loses from splitting (gate/up); a
+// launch of several waves per SIMD gains tail balance from short waves.
+static int decode_ksplit(bool gu, long waves_unsplit) {
+  if (gu) return waves_unsplit < 512 ? 2 : (waves_unsplit < 2048 ? 1 : 4);
+  return waves_unsplit < 1024 ? 4 : (waves_unsplit < 4096 ? 2 : 1);
+}
+
+template <int WF, int MT, bool GU, int KS>
+static void launch_expert_ks(const ExpertParams& p, int mt_max, int nmax, hipStream_t s) {
   constexpr int NBI = GU ? MX_DEC_NBI_GU : MX_DEC_NBI_DN;
   constexpr int UK = (WF == MX_DT_I8) ? (MT >= 4 ? 1 : MX_DEC_UK / 2)
                                       : (MT >= 4 ? 2 : MX_DEC_UK);
+  const dim3 grid(mt_max, mx_ceil_div(nmax, (4 / KS) * 16 * NBI));
   mx_clear_error();
-  hipLaunchKernelGGL((k_expert<WF, MT, NBI, GU, UK>), grid, dim3(256), 0, s, p);
+  hipLaunchKernelGGL((k_expert<WF, MT, NBI, GU, UK, KS>), grid, dim3(256), 0, s, p);
+}
+
+template <int WF, int MT, bool GU>
+static void launch_expert(const ExpertParams& p, int mt_max, int nmax, hipStream_t s) {
+  if constexpr (MT == 1) {
+    constexpr int NBI = GU ? MX_DEC_NBI_GU : MX_DEC_NBI_DN;
+    const long waves = (long)mt_max * mx_ceil_div(nmax, 4 * 16 * NBI) * 4;
+    const int ks = decode_ksplit(GU, waves);
+    if (ks == 4) return launch_expert_ks<WF, 1, GU, 4>(p, mt_max, nmax, s);
+    if (ks == 2) return launch_expert_ks<WF, 1, GU, 2>(p, mt_max, nmax, s);
+  }
+  launch_expert_ks<WF, MT, GU, 1>(p, mt_max, nmax, s);
 }
 
 template <bool GU>
-static int dispatch_expert(int wdt, int mt, const ExpertParams& p, dim3 grid, hipStream_t s) {
-#define MX_EXP_CASE(W)                                   \
-  if (wdt == W) {                                        \
-    if (mt == 1) launch_expert<W, 1, GU>(p, grid, s);    \
-    else if (mt == 2) launch_expert<W, 2, GU>(p, grid, s); \
-    else if (mt == 4) launch_expert<W, 4, GU>(p, grid, s); \
-    else return MX_ERR_INVALID;                          \
-    return mx_launch_status();                           \
+static int dispatch_expert(int wdt, int mt, const ExpertParams& p, int mt_max, int nmax,
+                           hipStream_t s) {
+#define MX_EXP_CASE(W)                                                \
+  if (wdt == W) {                                                     \
+    if (mt == 1) launch_expert<W, 1, GU>(p, mt_max, nmax, s);         \
+    else if (mt == 2) launch_expert<W, 2, GU>(p, mt_max, nmax, s);    \
+    else if (mt == 4) launch_expert<W, 4, GU>(p, mt_max, nmax, s);    \
+    else return MX_ERR_INVALID;                                       \
+    return mx_launch_status();                                        \
   }
   MX_EXP_CASE(MX_DT_F16)
   MX_EXP_CASE(MX_DT_I8)
@@ -616,8 +686,7 @@ static int launch_grouped(const MxMoeDesc* d, const ExpertParams& p, int tokens,
     return mx_launch_status();
   }
   if (m_blk != 16 && m_blk != 32 && m_blk != 64) return MX_ERR_INVALID;
-  dim3 grid(mt_max, mx_ceil_div(nmax, 4 * 16 * (GU ? MX_DEC_NBI_GU : MX_DEC_NBI_DN)));
-  return dispatch_expert<GU>(d->weight_dtype, m_blk / 16, p, grid, s);
+  return dispatch_expert<GU>(d->weight_dtype, m_blk / 16, p, mt_max, nmax, s);
 }
 
 extern "C" int mx_expert_gate_up(const MxMoeDesc* desc, const MxExpertPtrs* experts,
