@@ -286,6 +286,9 @@ def main() -> int:
     ap.add_argument("--no-sweep", action="store_true", help="headline only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default=None, help="run one sweep workload (profiling)")
+    ap.add_argument("--weight-layout", choices=("frag16", "rows"), default="frag16",
+                    help="expert weight layout in HBM: re-tiled 1 KiB MFMA fragments (one "
+                         "device pass after the layer is built) or the loader's row-major")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a 1 GiB device copy (HBM counter calibration)")
     args = ap.parse_args()
@@ -314,6 +317,8 @@ def main() -> int:
         t0 = time.perf_counter()
         layer = DeviceMoeLayer.synthetic(backend, G, SEED, stream, weight_dtype="float16",
                                          param_dtype="float32")
+        if args.weight_layout == "frag16":
+            layer.tile()
         log(f"GLM-4.7 fp16 layer: {layer.layer.nbytes / 1e9:.2f} GB built on device in "
             f"{time.perf_counter() - t0:.1f}s")
         mode = _lib.MX_ROUTER_SIGMOID_SELECT_BIAS
@@ -375,6 +380,8 @@ def main() -> int:
                                                and "stream" not in only)):
         layer = DeviceMoeLayer.synthetic(backend, G, SEED, stream, weight_dtype="int8",
                                          param_dtype="float32")
+        if args.weight_layout == "frag16":
+            layer.tile()
         for T in (1, 16):
             name = f"glm47_int8_decode_t{T}"
             if not want(name):
@@ -391,6 +398,8 @@ def main() -> int:
         Q = syn.QWEN3_NEXT
         layer = DeviceMoeLayer.synthetic(backend, Q, SEED, stream, weight_dtype="float16",
                                          param_dtype="float32")
+        if args.weight_layout == "frag16":
+            layer.tile()
         for T in (1, 4096):
             name = f"qwen3next_fp16_t{T}"
             if not want(name):
@@ -444,6 +453,7 @@ def main() -> int:
                    "top_k": G.top_k, "moe_intermediate": G.inter,
                    "shared_intermediate": G.shared_inter, "routing": "sigmoid_select_bias",
                    "routed_scaling": G.routed_scaling, "weights": "fp16",
+                   "weight_layout": args.weight_layout,
                    "tokens": args.tokens, "active_experts": head["active_experts"],
                    "parallelism": "single-gpu"},
         "roofline": {"kernel": "k_expert gate/up (fp16 MFMA, fused SiLU*up)", "bound": "hbm",

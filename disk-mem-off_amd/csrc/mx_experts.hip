@@ -89,7 +89,19 @@ struct ExpertParams {
   int E;
   int N_r, K_r;           // routed expert: output columns, reduction length
   int N_s, K_s;           // shared expert
+  int tiled;              // weights in MX_LAYOUT_FRAG16 (else row-major)
 };
+
+// Byte offset of the 16-byte piece lane (j, q) loads from fragment row block n16 (first
+// row, a multiple of 16 for tiled weights) at chunk 0, and the byte step per chunk.
+// Row-major: row n16 + j, column q * EPL.  MX_LAYOUT_FRAG16: 1 KiB fragment per
+// (16 rows, KC columns), lane 16 q + j at byte 16 * (16 q + j).
+template <int EPL, int ESZ>
+__device__ __forceinline__ uint32_t mx_bfrag_base(bool tiled, int n16, int j, int q, int K) {
+  constexpr int KC = 4 * EPL;
+  return tiled ? (uint32_t)(n16 / 16) * (uint32_t)(K / KC) * 1024u + (uint32_t)(16 * q + j) * 16u
+               : (uint32_t)(n16 + j) * (uint32_t)K * ESZ + (uint32_t)q * EPL * ESZ;
+}
 
 template <int WF, int MT, int NBI, bool GU, int UK, int KS>
 __global__ __launch_bounds__(256) void k_expert(const ExpertParams p) {
@@ -123,11 +135,12 @@ __global__ __launch_bounds__(256) void k_expert(const ExpertParams p) {
   const uint32_t matb = (uint32_t)N * rowb;
   const mx_rsrc_t rb0 = mx_rsrc(GU ? ep.gate : ep.down, matb);
   const mx_rsrc_t rb1 = mx_rsrc(GU ? ep.up : ep.down, matb);
+  const uint32_t bstep = p.tiled ? 1024u : (uint32_t)KC * ESZ;  // bytes per K chunk
   uint32_t boff[NBI];
 #pragma unroll
   for (int f = 0; f < NBI; ++f) {
     const int n = n0 + 16 * f + j;
-    boff[f] = n < N ? (uint32_t)n * rowb + q * EPL * ESZ : MX_OOB;
+    boff[f] = n < N ? mx_bfrag_base<EPL, ESZ>(p.tiled, n0 + 16 * f, j, q, K) : MX_OOB;
   }
   const mx_rsrc_t ra = mx_rsrc(p.a, p.a_bytes);
   uint32_t aoff[MT];
@@ -156,7 +169,7 @@ __global__ __launch_bounds__(256) void k_expert(const ExpertParams p) {
 
   // One chunk of loads.  kin = false turns the lane's loads into zero reads (K tail).
   auto load_chunk = [&](int c, bool kin, int4_t (&b)[NF], int4_t (&a)[MT][AV]) {
-    const uint32_t kb = (uint32_t)c * KC * ESZ;
+    const uint32_t kb = (uint32_t)c * bstep;
     const uint32_t ka = (uint32_t)c * KC * AESZ;
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
@@ -329,42 +342,59 @@ __global__ __launch_bounds__(256) void k_expert(const ExpertParams p) {
 //
 // With many rows per expert the activation tile is reused by every column slab, so it is
 // staged once per block in LDS (double-buffered, rows padded by 16 bytes so the 16-byte
-// fragment reads of 8 consecutive lanes hit distinct banks) and shared by the 4 waves.
-// Weights still go straight from HBM into MFMA B registers; each wave holds 4 B
+// fragment reads of 8 consecutive lanes hit distinct banks) and shared by the waves of
+// its half.  Weights go straight from HBM into MFMA B registers; each wave holds 4 B
 // fragments per k-chunk (gate/up: 2 gate + 2 up column blocks; down: 4 column blocks),
-// so every A fragment read from LDS feeds 4 MFMAs.  A stage covers 64 reduction columns.
+// so every A fragment read from LDS feeds 4 MFMAs.
+//
+// A block holds HV halves of 4 waves; half h computes m-tile HV*pair + h for the
+// block's column slab.  The halves run in lock step (one barrier per stage), so when
+// both m-tiles belong to the same expert (hot experts have many consecutive m-tiles)
+// their weight loads hit the same addresses at the same time and HBM serves them once.
+// fp16 uses HV = 2 (8 waves, 2 per SIMD); the int8 variant needs the full register file
+// of one wave per SIMD, so it runs HV = 1.
 //
 // Blocks are numbered so that consecutive logical ids run on the same XCD: hardware
 // block b goes to XCD b % 8, logical id = (b % 8) * (grid / 8) + b / 8.  Logical ids walk
-// the m-tiles of one column slab before moving to the next slab, so the m-tiles of one
-// expert (which read the same weight rows) are co-resident on one XCD and share its L2.
+// the m-tile pairs of one column slab before moving to the next slab.
 // ------------------------------------------------------------------------------------
 // Tunables (compile-time; the defaults are the measured best on MI355X).
-//   MX_LDS_ORDER 0: XCD-grouped, column slab major; 1: hardware order; 2: XCD-grouped,
-//                   m-tile major.
 //   MX_LDS_RB:      weight stages in flight per wave (even).
-//   MX_LDS_OCC_F16: blocks per CU the fp16 variant is register-limited to.
-#ifndef MX_LDS_ORDER
-#define MX_LDS_ORDER 0
-#endif
+//   MX_LDS_RA:      activation stages in flight (fp16 gate/up).
+//   MX_LDS_HV_F16:  m-tiles per block for fp16 (1 or 2).
 #ifndef MX_LDS_RB
 #define MX_LDS_RB 4
-#endif
-#ifndef MX_LDS_OCC_F16
-#define MX_LDS_OCC_F16 2
 #endif
 #ifndef MX_LDS_RA
 #define MX_LDS_RA 4
 #endif
+#ifndef MX_LDS_HV_F16
+#define MX_LDS_HV_F16 1
+#endif
+#ifndef MX_LDS_KM_F16
+#define MX_LDS_KM_F16 1
+#endif
+#ifndef MX_LDS_RB_KM2
+#define MX_LDS_RB_KM2 2
+#endif
 
-// fp16 fits two blocks per CU; the int8 variant (conversion temporaries, 64-column
-// stages) needs the full register file of one block per CU to avoid spills.
+template <int WF>
+struct LdsShape {
+  static constexpr int HV = WF == MX_DT_F16 ? MX_LDS_HV_F16 : 1;
+  // fp16 at HV = 1 fits two 4-wave blocks per CU; the int8 variant one.
+  static constexpr int OCC = WF == MX_DT_F16 ? (HV == 1 ? 2 : 1) : 1;
+  // MFMA k-steps per stage: each weight row is read KM * 64 contiguous bytes per stage.
+  static constexpr int KM = WF == MX_DT_F16 ? MX_LDS_KM_F16 : 1;
+};
+
 template <int WF, bool GU>
-__global__ __launch_bounds__(256, WF == MX_DT_F16 ? MX_LDS_OCC_F16 : 1) void k_expert_lds(
+__global__ __launch_bounds__(256 * LdsShape<WF>::HV, LdsShape<WF>::OCC) void k_expert_lds(
     const ExpertParams p, int mt_max, int nblk) {
   using Tr = WTr<WF>;
+  constexpr int HV = LdsShape<WF>::HV;
   constexpr int EPL = Tr::EPL, ESZ = Tr::ESZ;
-  constexpr int KS = 4 * EPL;                // reduction columns per stage: 32 fp16, 64 int8
+  constexpr int KM = LdsShape<WF>::KM;
+  constexpr int KS = 4 * EPL * KM;           // reduction columns per stage: 32 / 64 fp16, 64 int8
   constexpr int MT = 8, MB = 128;
   constexpr int NBI = GU ? 2 : 4;
   constexpr int NF = GU ? 2 * NBI : NBI;
@@ -372,39 +402,45 @@ __global__ __launch_bounds__(256, WF == MX_DT_F16 ? MX_LDS_OCC_F16 : 1) void k_e
   constexpr int ATILE = MB * AROW;
   constexpr int CPR = KS * 2 / 16;           // 16-byte chunks per row and stage
   constexpr int ACH = MB * CPR / 256;        // chunks each thread stages
-  constexpr int RB = MX_LDS_RB;              // weight stages in flight per wave
-  constexpr int RA = (WF == MX_DT_F16 && GU) ? MX_LDS_RA : 2;  // activation stages in flight
+  constexpr int RB = KM == 1 ? MX_LDS_RB : MX_LDS_RB_KM2;  // weight stages in flight per wave
+  constexpr int RA = (WF == MX_DT_F16 && GU && KM == 1) ? MX_LDS_RA : 2;  // activation stages
   static_assert(RB % RA == 0 && RA % 2 == 0, "ring sizes must divide the unroll");
-  __shared__ __align__(16) char lds[2 * ATILE];
+  __shared__ __align__(16) char lds[HV][2 * ATILE];
 
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // provably wave-uniform
+  const int tid = threadIdx.x & 255, lane = tid & 63;
+  const int half = __builtin_amdgcn_readfirstlane(threadIdx.x >> 8);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave inside the half
   const int b = blockIdx.x;
-#if MX_LDS_ORDER == 1
-  const int logical = b;
-#else
   const int logical = (b & 7) * (gridDim.x >> 3) + (b >> 3);
-#endif
-#if MX_LDS_ORDER == 2
-  const int mt = logical / nblk;
-  const int nb = logical - mt * nblk;
-#else
-  const int nb = logical / mt_max;
-  const int mt = logical - nb * mt_max;
-#endif
-  if (nb >= nblk || mt >= mt_max || mt >= *p.n_mtiles) return;
-  const int g = p.mt_group[mt];
-  const int row0 = p.mt_row0[mt];
+  const int npair = (mt_max + HV - 1) / HV;
+  const int nb = logical / npair;
+  const int pair = logical - nb * npair;
+  const int n_mt = min(*p.n_mtiles, mt_max);
+  if (nb >= nblk || pair * HV >= n_mt) return;  // whole block idle
+
+  // Both halves' tiles are read by every wave: the stage count must agree block-wide.
+  int kmax = 0;
+#pragma unroll
+  for (int h = 0; h < HV; ++h) {
+    const int m2 = pair * HV + h;
+    if (m2 < n_mt) {
+      const int e2 = p.g_expert[p.mt_group[m2]];
+      kmax = max(kmax, e2 == p.E ? p.K_s : p.K_r);
+    }
+  }
+  const int mt = pair * HV + half;
+  const bool tile = mt < n_mt;  // a half without a tile streams zeros and stores nothing
+  const int g = tile ? p.mt_group[mt] : 0;
+  const int row0 = tile ? p.mt_row0[mt] : 0;
   const int eid = p.g_expert[g];
   const int gstart = p.g_start[g];
   const int gcount = p.g_count[g];
   const bool sh = eid == p.E;
   const int N = sh ? p.N_s : p.N_r;
   const int K = sh ? p.K_s : p.K_r;
-  if (nb * 4 * 16 * NBI >= N) return;  // whole block past this expert's columns
   const int n0 = (nb * 4 + wave) * 16 * NBI;
-  const bool wact = n0 < N;
-  const int mrows = min(MB, gcount - row0);
+  const bool wact = tile && n0 < N;
+  const int mrows = tile ? min(MB, gcount - row0) : 0;
   const int j = lane & 15, q = lane >> 4;
   const MxExpertPtrs ep = p.experts[eid];
 
@@ -412,11 +448,12 @@ __global__ __launch_bounds__(256, WF == MX_DT_F16 ? MX_LDS_OCC_F16 : 1) void k_e
   const uint32_t matb = (uint32_t)N * rowb;
   const mx_rsrc_t rb0 = mx_rsrc(GU ? ep.gate : ep.down, matb);
   const mx_rsrc_t rb1 = mx_rsrc(GU ? ep.up : ep.down, matb);
+  const uint32_t bstep = p.tiled ? 1024u : (uint32_t)4 * EPL * ESZ;  // bytes per K chunk
   uint32_t boff[NBI];
 #pragma unroll
   for (int f = 0; f < NBI; ++f) {
     const int n = n0 + 16 * f + j;
-    boff[f] = (wact && n < N) ? (uint32_t)n * rowb + q * EPL * ESZ : MX_OOB;
+    boff[f] = (wact && n < N) ? mx_bfrag_base<EPL, ESZ>(p.tiled, n0 + 16 * f, j, q, K) : MX_OOB;
   }
 
   // Activation chunks this thread stages: fixed rows, advancing columns.
@@ -444,42 +481,48 @@ __global__ __launch_bounds__(256, WF == MX_DT_F16 ? MX_LDS_OCC_F16 : 1) void k_e
 #pragma unroll
     for (int f = 0; f < NF; ++f) acc[mi][f] = (float4_t){0.f, 0.f, 0.f, 0.f};
 
+  char* const my_lds = lds[half];
   auto load_a = [&](int st, int4_t (&ar)[ACH]) {
     const int k0 = st * KS;
 #pragma unroll
     for (int i = 0; i < ACH; ++i)
       ar[i] = mx_ld16(ra, (k0 + acol[i] < K) ? agoff[i] + (uint32_t)k0 * 2 : MX_OOB);
   };
-  auto load_b = [&](int st, int4_t (&br)[NF]) {
-    const bool kin = st * KS + q * EPL < K;
-    const uint32_t kb = (uint32_t)st * KS * ESZ;
+  auto load_b = [&](int st, int4_t (&br)[KM][NF]) {
 #pragma unroll
-    for (int f = 0; f < NF; ++f) {
-      const int fi = GU ? (f % NBI) : f;
-      br[f] = mx_ld16((GU && f >= NBI) ? rb1 : rb0, kin ? boff[fi] + kb : MX_OOB);
+    for (int km = 0; km < KM; ++km) {
+      const bool kin = st * KS + km * 4 * EPL + q * EPL < K;
+      const uint32_t kb = ((uint32_t)st * KM + km) * bstep;
+#pragma unroll
+      for (int f = 0; f < NF; ++f) {
+        const int fi = GU ? (f % NBI) : f;
+        br[km][f] = mx_ld16((GU && f >= NBI) ? rb1 : rb0, kin ? boff[fi] + kb : MX_OOB);
+      }
     }
   };
   auto store_a = [&](int buf, const int4_t (&ar)[ACH]) {
-    char* base = lds + buf * ATILE;
+    char* base = my_lds + buf * ATILE;
 #pragma unroll
     for (int i = 0; i < ACH; ++i) *(int4_t*)(base + alds[i]) = ar[i];
   };
-  auto compute = [&](int buf, const int4_t (&br)[NF]) {
-    const char* base = lds + buf * ATILE;
+  auto compute = [&](int buf, const int4_t (&br)[KM][NF]) {
+    const char* base = my_lds + buf * ATILE;
     if constexpr (WF == MX_DT_F16) {
 #pragma unroll
-      for (int mi = 0; mi < MT; ++mi) {
-        const int4_t a = *(const int4_t*)(base + (16 * mi + j) * AROW + q * 16);
+      for (int km = 0; km < KM; ++km)
 #pragma unroll
-        for (int f = 0; f < NF; ++f)
-          acc[mi][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-              __builtin_bit_cast(half8_t, a), __builtin_bit_cast(half8_t, br[f]), acc[mi][f],
-              0, 0, 0);
-      }
+        for (int mi = 0; mi < MT; ++mi) {
+          const int4_t a = *(const int4_t*)(base + (16 * mi + j) * AROW + km * 64 + q * 16);
+#pragma unroll
+          for (int f = 0; f < NF; ++f)
+            acc[mi][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                __builtin_bit_cast(half8_t, a), __builtin_bit_cast(half8_t, br[km][f]),
+                acc[mi][f], 0, 0, 0);
+        }
     } else {
       half8_t blo[NF], bhi[NF];
 #pragma unroll
-      for (int f = 0; f < NF; ++f) mx_i8_to_f16(br[f], blo[f], bhi[f]);
+      for (int f = 0; f < NF; ++f) mx_i8_to_f16(br[0][f], blo[f], bhi[f]);
 #pragma unroll
       for (int mi = 0; mi < MT; ++mi) {
         const char* ap = base + (16 * mi + j) * AROW + q * 32;
@@ -501,14 +544,15 @@ __global__ __launch_bounds__(256, WF == MX_DT_F16 ? MX_LDS_OCC_F16 : 1) void k_e
   // are in flight; the activations of stage s + 1 go to LDS at the end of stage s.  The
   // global latency is hidden by the ring depths, not by the LDS double buffer.  The loop
   // body is branch-free so the in-order load counter is never drained: stages past the
-  // end of K read zeros through the descriptors' bounds check and the stage count is
-  // padded to a multiple of RB (a multiple of RA), which also makes every register-set
-  // index static.  A wave without columns (edge of a narrower shared expert) has
-  // out-of-range weight offsets, computes zeros and skips the epilogue.
-  const int nst = (K + KS - 1) / KS;
+  // end of K read zeros through the descriptors' bounds check and the stage count (of
+  // the block's longest reduction) is padded to a multiple of RB (a multiple of RA),
+  // which also makes every register-set index static.  A wave without columns (edge of
+  // a narrower shared expert, or a half without a tile) has out-of-range weight offsets,
+  // computes zeros and skips the epilogue.
+  const int nst = (kmax + KS - 1) / KS;
   const int nst_pad = (nst + RB - 1) / RB * RB;
   int4_t aring[RA][ACH];
-  int4_t bring[RB][NF];
+  int4_t bring[RB][KM][NF];
 #pragma unroll
   for (int u = 0; u < RA; ++u) load_a(u, aring[u]);
 #pragma unroll
@@ -518,11 +562,11 @@ __global__ __launch_bounds__(256, WF == MX_DT_F16 ? MX_LDS_OCC_F16 : 1) void k_e
   for (int s0 = 0; s0 < nst_pad; s0 += RB) {
 #pragma unroll
     for (int u = 0; u < RB; ++u) {
-      const int s = s0 + u;
-      load_b(s + RB - 1, bring[(u + RB - 1) % RB]);
+      const int st = s0 + u;
+      load_b(st + RB - 1, bring[(u + RB - 1) % RB]);
       compute(u % 2, bring[u]);
       store_a((u + 1) % 2, aring[(u + 1) % RA]);
-      load_a(s + RA, aring[u % RA]);
+      load_a(st + RA, aring[u % RA]);
       __syncthreads();
     }
   }
@@ -595,6 +639,12 @@ static int expert_check(const MxMoeDesc* d) {
   }
   // Each lane's 16-byte piece must sit inside one row.
   if (d->hidden % epl || d->inter % epl || d->shared_inter % epl) return MX_ERR_UNSUPPORTED;
+  if (d->weight_layout != MX_LAYOUT_ROWS && d->weight_layout != MX_LAYOUT_FRAG16)
+    return MX_ERR_INVALID;
+  // Fragment layout: whole fragments only (16 rows, KC = 4 * epl columns).
+  if (d->weight_layout == MX_LAYOUT_FRAG16 &&
+      (d->hidden % (4 * epl) || d->inter % (4 * epl) || d->shared_inter % (4 * epl)))
+    return MX_ERR_UNSUPPORTED;
   // Buffer descriptors address < 2 GiB per matrix.
   const int esz = d->weight_dtype == MX_DT_F32 ? 4 : (d->weight_dtype == MX_DT_F16 ? 2 : 1);
   const long mx = (long)d->hidden * (d->inter > d->shared_inter ? d->inter : d->shared_inter) * esz;
@@ -674,15 +724,16 @@ static int launch_grouped(const MxMoeDesc* d, const ExpertParams& p, int tokens,
     if (d->weight_dtype == MX_DT_F32) return MX_ERR_INVALID;
     const int cols = 4 * 16 * (GU ? 2 : 4);
     const int nblk = mx_ceil_div(nmax, cols);
-    const long blocks = ((long)mt_max * nblk + 7) / 8 * 8;
+    const int hv = d->weight_dtype == MX_DT_F16 ? LdsShape<MX_DT_F16>::HV : LdsShape<MX_DT_I8>::HV;
+    const long blocks = ((long)mx_ceil_div(mt_max, hv) * nblk + 7) / 8 * 8;
     if (blocks > (1l << 31) - 1) return MX_ERR_UNSUPPORTED;
     mx_clear_error();
     if (d->weight_dtype == MX_DT_F16)
-      hipLaunchKernelGGL((k_expert_lds<MX_DT_F16, GU>), dim3((unsigned)blocks), dim3(256), 0, s,
-                         p, mt_max, nblk);
+      hipLaunchKernelGGL((k_expert_lds<MX_DT_F16, GU>), dim3((unsigned)blocks), dim3(256 * hv), 0,
+                         s, p, mt_max, nblk);
     else
-      hipLaunchKernelGGL((k_expert_lds<MX_DT_I8, GU>), dim3((unsigned)blocks), dim3(256), 0, s,
-                         p, mt_max, nblk);
+      hipLaunchKernelGGL((k_expert_lds<MX_DT_I8, GU>), dim3((unsigned)blocks), dim3(256 * hv), 0,
+                         s, p, mt_max, nblk);
     return mx_launch_status();
   }
   if (m_blk != 16 && m_blk != 32 && m_blk != 64) return MX_ERR_INVALID;
@@ -725,6 +776,7 @@ extern "C" int mx_expert_gate_up(const MxMoeDesc* desc, const MxExpertPtrs* expe
   p.K_r = desc->hidden;
   p.N_s = desc->shared_inter;
   p.K_s = desc->hidden;
+  p.tiled = desc->weight_layout == MX_LAYOUT_FRAG16;
   return launch_grouped<true>(desc, p, tokens, m_blk, p.ldo, (hipStream_t)stream);
 }
 
@@ -766,5 +818,51 @@ extern "C" int mx_expert_down(const MxMoeDesc* desc, const MxExpertPtrs* experts
   p.K_r = desc->inter;
   p.N_s = desc->hidden;
   p.K_s = desc->shared_inter;
+  p.tiled = desc->weight_layout == MX_LAYOUT_FRAG16;
   return launch_grouped<false>(desc, p, tokens, m_blk, desc->hidden, (hipStream_t)stream);
+}
+
+// ------------------------------------------------------------------------------------
+// Row-major -> MX_LAYOUT_FRAG16.  One thread per 16-byte piece: piece l of fragment
+// (g, c) comes from row 16 g + (l % 16), bytes 64 c + 16 (l / 16) of that row, and goes
+// to byte (g * nch + c) * 1024 + 16 l.  Writes are contiguous per wave; the reads are
+// the row-strided pattern the layout exists to avoid, paid once per bound layer.
+// ------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_tile_weights(int4_t* __restrict__ dst,
+                                                      const char* __restrict__ src,
+                                                      long pieces, uint32_t rowb, int nch) {
+  const long t = (long)blockIdx.x * 256 + threadIdx.x;
+  if (t >= pieces) return;
+  const long frag = t >> 6;
+  const int l = (int)(t & 63);
+  const long g = frag / nch;
+  const int c = (int)(frag - g * nch);
+  const size_t so = (size_t)(g * 16 + (l & 15)) * rowb + (size_t)c * 64 + (size_t)(l >> 4) * 16;
+  dst[t] = *(const int4_t*)(src + so);
+}
+
+extern "C" int mx_tile_weights(void* dst, const void* src, int32_t rows, int32_t cols,
+                               int32_t weight_dtype, void* stream) {
+  if (!dst || !src || rows <= 0 || cols <= 0) return MX_ERR_INVALID;
+  int esz;
+  switch (weight_dtype) {
+    case MX_DT_F32: esz = 4; break;
+    case MX_DT_F16: esz = 2; break;
+    case MX_DT_I8: esz = 1; break;
+    default: return MX_ERR_INVALID;
+  }
+  const long rowb = (long)cols * esz;
+  if (rows % 16 || rowb % 64) return MX_ERR_UNSUPPORTED;
+  if (!mx_aligned16(dst) || !mx_aligned16(src)) return MX_ERR_ALIGNMENT;
+  const long bytes = (long)rows * rowb;
+  const char* d0 = (const char*)dst;
+  const char* s0 = (const char*)src;
+  if (d0 < s0 + bytes && s0 < d0 + bytes) return MX_ERR_INVALID;  // overlap
+  if (rowb >= (1l << 32)) return MX_ERR_UNSUPPORTED;
+  const long pieces = bytes / 16;
+  mx_clear_error();
+  hipLaunchKernelGGL(k_tile_weights, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, (int4_t*)dst, (const char*)src, pieces,
+                     (uint32_t)rowb, (int)(rowb / 64));
+  return mx_launch_status();
 }

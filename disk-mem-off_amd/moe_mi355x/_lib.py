@@ -29,6 +29,8 @@ MX_DT_I8 = 2
 MX_ROUTER_REF_SOFTMAX_BIAS = 0
 MX_ROUTER_SIGMOID_SELECT_BIAS = 1
 MX_ROUTER_SOFTMAX = 2
+MX_LAYOUT_ROWS = 0
+MX_LAYOUT_FRAG16 = 1
 
 MX_N_STAGES = 7
 STAGE_NAMES = ("rmsnorm", "router_logits", "router_topk", "dispatch", "expert_gate_up",
@@ -52,7 +54,7 @@ class MxMoeDesc(ctypes.Structure):
         ("n_experts", c_int32), ("top_k", c_int32), ("router_mode", c_int32),
         ("norm_topk_prob", c_int32), ("weight_dtype", c_int32), ("param_dtype", c_int32),
         ("has_bias", c_int32), ("has_shared_gate", c_int32),
-        ("routed_scaling", c_float), ("eps", c_float),
+        ("routed_scaling", c_float), ("eps", c_float), ("weight_layout", c_int32),
     ]
 
 
@@ -134,6 +136,7 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                   c_int32, c_void_p, c_void_p]),
     "mx_fill_normal": (ctypes.c_int, [c_void_p, c_int32, c_size_t, c_uint64, c_uint64,
                                       c_uint64, c_float, c_void_p]),
+    "mx_tile_weights": (ctypes.c_int, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p]),
     "mx_quantize_rows_i8": (ctypes.c_int, [c_void_p, c_int32, c_int32, c_int32, c_void_p,
                                            c_void_p, c_void_p]),
 }

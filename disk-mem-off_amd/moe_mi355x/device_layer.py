@@ -18,8 +18,8 @@ import numpy as np
 
 from . import _lib, gen
 from .backends import MI355XBackend
-from .layout import MoeLayerLayout, make_layer_spec, pack_tensors
-from .moe import MoeConfig, MoeRunner
+from .layout import MoeLayerLayout, frag16_to_rows, make_layer_spec, pack_tensors
+from .moe import MoeConfig, MoeRunner, tile_experts
 from .synthetic import MoeShape, stream_of, tensor_specs
 from .types import DeviceBuffer, LayerSpec
 
@@ -50,6 +50,15 @@ class DeviceMoeLayer:
         self.layout = MoeLayerLayout.from_meta(layer.metadata["tensors"])
         self.runner = MoeRunner(backend)
         self._weights = None
+        self.weight_layout = _lib.MX_LAYOUT_ROWS
+
+    def tile(self) -> "DeviceMoeLayer":
+        """Re-lay the expert weights in place into MX_LAYOUT_FRAG16 (one device pass); the
+        configs made afterwards carry the layout."""
+        if self.weight_layout != _lib.MX_LAYOUT_FRAG16:
+            tile_experts(self.backend, self.layout, self.buf.handle, self.stream)
+            self.weight_layout = _lib.MX_LAYOUT_FRAG16
+        return self
 
     # -- construction --
     @classmethod
@@ -137,7 +146,7 @@ class DeviceMoeLayer:
                norm_topk_prob: bool = True) -> MoeConfig:
         return MoeConfig.from_layout(self.layout, top_k=top_k, router_mode=router_mode,
                                      norm_topk_prob=norm_topk_prob, routed_scaling=routed_scaling,
-                                     eps=eps)
+                                     eps=eps, weight_layout=self.weight_layout)
 
     def prepare(self, cfg: MoeConfig, max_tokens: int) -> _lib.MxMoeWeights:
         self.runner.reserve(cfg.desc(), max_tokens)
@@ -156,6 +165,9 @@ class DeviceMoeLayer:
         self.backend.copy_d2h_ptr_async(out.ctypes.data, self.buf.handle + m["offset"],
                                         out.nbytes, self.stream)
         self.backend.synchronize_stream(self.stream)
+        if self.weight_layout == _lib.MX_LAYOUT_FRAG16 and out.ndim == 2 and \
+                any(o == m["offset"] for o, _, _ in self.layout.expert_matrices()):
+            out = frag16_to_rows(out, out.shape[0], out.shape[1], out.dtype)
         return out
 
     def read_tensors(self, names: list[str]) -> dict[str, np.ndarray]:

@@ -83,6 +83,27 @@ def unpack_host(raw: Any, meta: list[dict[str, Any]]) -> dict[str, np.ndarray]:
     return out
 
 
+def rows_to_frag16(mat: np.ndarray) -> np.ndarray:
+    """Row-major [rows, cols] -> MX_LAYOUT_FRAG16 bytes: 1 KiB per (16 rows, 64 bytes of
+    columns) fragment, fragments column-block-minor, lane 16 q + j of a fragment holding
+    bytes 16 q .. 16 q + 15 of the fragment's row j (the device converter's layout)."""
+    rows = mat.shape[0]
+    b = np.ascontiguousarray(mat).view(np.uint8).reshape(rows, -1)
+    nch = b.shape[1] // 64
+    if rows % 16 or b.shape[1] % 64:
+        raise ValueError("no whole fragments")
+    return np.ascontiguousarray(
+        b.reshape(rows // 16, 16, nch, 4, 16).transpose(0, 2, 3, 1, 4)).reshape(-1)
+
+
+def frag16_to_rows(buf: np.ndarray, rows: int, cols: int, dtype: Any) -> np.ndarray:
+    """Inverse of ``rows_to_frag16``."""
+    esz = np.dtype(dtype).itemsize
+    nch = cols * esz // 64
+    b = np.ascontiguousarray(buf).view(np.uint8).reshape(rows // 16, nch, 4, 16, 16)
+    return np.ascontiguousarray(b.transpose(0, 3, 1, 2, 4)).reshape(rows, cols * esz).view(dtype)
+
+
 @dataclass
 class MoeLayerLayout:
     """Where each MoE tensor lives inside a packed layer buffer, with derived shapes."""
@@ -178,6 +199,18 @@ class MoeLayerLayout:
         else:
             rows.append((-1,) * 6)
         return rows
+
+    def expert_matrices(self) -> list[tuple[int, int, int]]:
+        """(byte offset, rows, cols) of every expert weight matrix, shared expert last."""
+        out = []
+        for offs in self.expert_offsets():
+            if offs[0] < 0:
+                continue
+            shared = len(out) >= 3 * self.n_experts
+            inter = self.shared_inter if shared else self.inter
+            out += [(offs[0], inter, self.hidden), (offs[1], inter, self.hidden),
+                    (offs[2], self.hidden, inter)]
+        return out
 
     def expert_table(self, base: int) -> ctypes.Array:
         """Device pointer table (E + 1 ``MxExpertPtrs``) for a buffer at address ``base``.

@@ -41,10 +41,12 @@ class MoeConfig:
     param_dtype: int
     has_bias: bool
     has_shared_gate: bool
+    weight_layout: int = _lib.MX_LAYOUT_ROWS
 
     @classmethod
     def from_layout(cls, layout: MoeLayerLayout, *, top_k: int, router_mode: int | str,
-                    norm_topk_prob: bool, routed_scaling: float, eps: float) -> "MoeConfig":
+                    norm_topk_prob: bool, routed_scaling: float, eps: float,
+                    weight_layout: int = _lib.MX_LAYOUT_ROWS) -> "MoeConfig":
         if isinstance(router_mode, str):
             router_mode = ROUTER_MODES[router_mode]
         return cls(hidden=layout.hidden, inter=layout.inter, shared_inter=layout.shared_inter,
@@ -53,7 +55,7 @@ class MoeConfig:
                    eps=float(eps), weight_dtype=layout.weight_dtype,
                    param_dtype=layout.param_dtype,
                    has_bias=layout.has_bias and router_mode != _lib.MX_ROUTER_SOFTMAX,
-                   has_shared_gate=layout.has_shared_gate)
+                   has_shared_gate=layout.has_shared_gate, weight_layout=int(weight_layout))
 
     def desc(self) -> _lib.MxMoeDesc:
         return _lib.MxMoeDesc(
@@ -62,7 +64,32 @@ class MoeConfig:
             norm_topk_prob=int(self.norm_topk_prob), weight_dtype=self.weight_dtype,
             param_dtype=self.param_dtype, has_bias=int(self.has_bias),
             has_shared_gate=int(self.has_shared_gate), routed_scaling=self.routed_scaling,
-            eps=self.eps)
+            eps=self.eps, weight_layout=self.weight_layout)
+
+
+_ELEM = {_lib.MX_DT_F32: 4, _lib.MX_DT_F16: 2, _lib.MX_DT_I8: 1}
+
+
+def tile_experts(backend: Any, layout: MoeLayerLayout, base: int, stream: Any) -> None:
+    """Re-lay every expert matrix of the layer at device address ``base`` from the loader's
+    row-major form into MX_LAYOUT_FRAG16, in place (through one scratch matrix).  Raises
+    ``ValueError`` when a shape has no whole fragments (rows % 16, cols % (64 / size))."""
+    lib = _lib.load()
+    esz = _ELEM[layout.weight_dtype]
+    mats = layout.expert_matrices()
+    for _, r, c in mats:
+        if r % 16 or (c * esz) % 64:
+            raise ValueError(f"expert matrix {r}x{c} has no whole 16 x {64 // esz} fragments")
+    scratch = backend.alloc_device(max(r * c * esz for _, r, c in mats))
+    try:
+        for off, r, c in mats:
+            _lib.check(lib.mx_memcpy_d2d_async(scratch.handle, base + off, r * c * esz, stream),
+                       "hipMemcpyAsync")
+            _lib.check(lib.mx_tile_weights(base + off, scratch.handle, r, c,
+                                           layout.weight_dtype, stream), "mx_tile_weights")
+        backend.synchronize_stream(stream)
+    finally:
+        backend.free_device(scratch)
 
 
 def workspace_bytes(desc: _lib.MxMoeDesc, tokens: int) -> int:

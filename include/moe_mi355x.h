@@ -51,6 +51,21 @@ extern "C" {
 #define MX_ROUTER_SIGMOID_SELECT_BIAS 1
 #define MX_ROUTER_SOFTMAX 2
 
+/* ---- expert weight layouts ------------------------------------------------------------
+ * MX_LAYOUT_ROWS   : nn.Linear row-major [out, in], as the loader packs the layer.
+ * MX_LAYOUT_FRAG16 : the same bytes regrouped into 1 KiB fragments, one per (16 output
+ *                    rows, KC input columns) block with KC = 64 bytes / element size
+ *                    (16 fp32, 32 fp16, 64 int8); fragment (g, c) sits at byte
+ *                    (g * in / KC + c) * 1024 and holds, at byte 16 * (16 q + j), the
+ *                    KC / 4 elements W[16 g + j][KC c + (KC / 4) q ...].  The expert
+ *                    kernels then read every fragment as one contiguous 1 KiB (the
+ *                    row-major form costs a DRAM page per 64 bytes in the prefill
+ *                    kernel).  Produced on the device by mx_tile_weights; needs
+ *                    out % 16 == 0 and in % KC == 0 for every expert matrix.  Scales
+ *                    of int8 weights keep their per-row layout.                      */
+#define MX_LAYOUT_ROWS 0
+#define MX_LAYOUT_FRAG16 1
+
 /* Per-expert weight pointers (device addresses).  gate/up are [inter, hidden] and down is
  * [hidden, inter], nn.Linear row-major ([out, in]) exactly as packed in the layer buffer
  * (loader/huggingface.py:458-591).  For MX_DT_I8 the *_scale pointers give one fp16 scale
@@ -81,6 +96,7 @@ typedef struct MxMoeDesc {
   int32_t has_shared_gate; /* Qwen3-Next shared_expert_gate present                    */
   float routed_scaling;    /* routed_scaling_factor (1.0 for Qwen3-Next)               */
   float eps;               /* rms_norm_eps                                             */
+  int32_t weight_layout;   /* MX_LAYOUT_ROWS / MX_LAYOUT_FRAG16 of the expert weights  */
 } MxMoeDesc;
 
 /* Device pointers of one layer's MoE tensors. */
@@ -257,6 +273,14 @@ int mx_fill_normal(void* dst, int32_t dtype, size_t n, uint64_t seed, uint64_t s
  * [rows, cols] on the device; q int8 [rows, cols]; scale fp16 [rows].                */
 int mx_quantize_rows_i8(const void* w, int32_t w_dtype, int32_t rows, int32_t cols, int8_t* q,
                         void* scale, void* stream);
+
+/* Re-layout of one expert matrix [rows, cols] of weight_dtype from MX_LAYOUT_ROWS (src)
+ * to MX_LAYOUT_FRAG16 (dst); dst and src must not overlap, both 16-byte aligned;
+ * rows % 16 == 0 and cols % KC == 0 (MX_ERR_UNSUPPORTED otherwise).  No counterpart in
+ * the reference, whose expert products read the loader layout directly
+ * (glm4_moe.py:222-224): it prepares a bound layer for the prefill kernel.           */
+int mx_tile_weights(void* dst, const void* src, int32_t rows, int32_t cols,
+                    int32_t weight_dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -3,6 +3,7 @@ metadata parsing and the device pointer table."""
 from __future__ import annotations
 
 import ctypes
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -95,4 +96,41 @@ def test_misaligned_expert_is_reported():
 
 def test_expert_ptrs_struct_matches_header():
     assert ctypes.sizeof(_lib.MxExpertPtrs) == 48
-    assert ctypes.sizeof(_lib.MxMoeDesc) == 13 * 4
+    assert ctypes.sizeof(_lib.MxMoeDesc) == 14 * 4
+
+
+# ---- MX_LAYOUT_FRAG16 host reference (the device converter is checked against it) -------
+
+@pytest.mark.parametrize("dt,cols", [(np.float16, 64), (np.float16, 96), (np.int8, 128),
+                                     (np.float32, 48)])
+def test_frag16_round_trip_and_placement(dt, cols):
+    from moe_mi355x.layout import frag16_to_rows, rows_to_frag16
+    rng = np.random.default_rng(cols)
+    m = (rng.standard_normal((48, cols)) * 50).astype(dt)
+    t = rows_to_frag16(m)
+    assert t.nbytes == m.nbytes
+    assert np.array_equal(frag16_to_rows(t, 48, cols, dt).view(np.uint8), m.view(np.uint8))
+    rb = m.view(np.uint8).reshape(48, -1)
+    nch = rb.shape[1] // 64
+    frags = t.reshape(-1, 64, 16)
+    # every 16-byte piece: fragment (g, c), lane 16 q + j <- row 16 g + j, bytes 64 c + 16 q
+    for g in range(3):
+        for c in range(nch):
+            for q in range(4):
+                for j in range(16):
+                    assert np.array_equal(frags[g * nch + c, 16 * q + j],
+                                          rb[16 * g + j, 64 * c + 16 * q: 64 * c + 16 * q + 16])
+
+
+def test_frag16_rejects_partial_fragments():
+    from moe_mi355x.layout import rows_to_frag16
+    with pytest.raises(ValueError):
+        rows_to_frag16(np.zeros((24, 64), np.float16))
+    with pytest.raises(ValueError):
+        rows_to_frag16(np.zeros((16, 40), np.float16))
+
+
+def test_layout_constants_match_header():
+    hdr = (Path(__file__).resolve().parents[1] / "include" / "moe_mi355x.h").read_text()
+    assert "#define MX_LAYOUT_ROWS 0" in hdr and "#define MX_LAYOUT_FRAG16 1" in hdr
+    assert _lib.MX_LAYOUT_ROWS == 0 and _lib.MX_LAYOUT_FRAG16 == 1
