@@ -106,16 +106,20 @@ extern "C" int mx_rmsnorm(const float* x, const void* norm_w, int32_t param_dtyp
 }
 
 // ------------------------------------------------------------------------------------
-// Router logits, split over H.  Block = 4 waves; wave w owns experts e0..e0+3 of the
-// block's 16-expert tile and RT_TT tokens.  Lanes stride H by 4 elements; each wave
-// reduces its RT_TT x 4 partial dot products at the end.  Row e == E is the Qwen3-Next
-// shared-expert gate (qwen3_next.py:328), which rides along as an extra "expert".
-// out[s][t][e] holds the partial sum of H-slice s; the top-k kernel adds the slices in
-// ascending order, so the result does not depend on scheduling.
+// Router logits on fp32 MFMA (v_mfma_f32_16x16x4_f32: full fp32 products and sums).
+// Block = 4 waves over a 64-token x 64-expert tile; wave w takes the 32 x 32 quarter
+// (tokens (w & 1) * 32.., experts (w >> 1) * 32..), i.e. 2 x 2 fragments of 16 x 16.
+// Row e == E is the Qwen3-Next shared-expert gate (qwen3_next.py:328), which rides along
+// as an extra "expert".  Grid z splits H into slices; out[s][t][e] holds the partial sum
+// of slice s and the top-k kernel adds the slices in ascending order, so the result does
+// not depend on scheduling.
+//
+// Per 16-column chunk lane (i, q) loads 4 consecutive columns 4q .. 4q+3 of its token
+// row and of its expert row (float4); MFMA e (0..3) takes element e of both, so the
+// four MFMAs cover the chunk's 16 columns once each.  Loads are clamped in bounds and
+// masked (branch-free), and a chunk batch is in flight while the previous one runs.
 // ------------------------------------------------------------------------------------
-#define RT_TT 8
-#define RT_EPB 16
-#define RT_KCH 256  // H elements per lane sweep (64 lanes x 4)
+#define RT_KCH 256  // H-slice granularity (elements)
 
 template <typename WT>
 __device__ __forceinline__ float4 rt_load4(const WT* p);
@@ -130,75 +134,99 @@ __device__ __forceinline__ float4 rt_load4<half_t>(const half_t* p) {
   return make_float4((float)v[0], (float)v[1], (float)v[2], (float)v[3]);
 }
 
-template <typename WT>
-__global__ __launch_bounds__(256) void k_router_logits(const float* __restrict__ h32,
-                                                       const WT* __restrict__ wr,
-                                                       const WT* __restrict__ wseg, int T,
-                                                       int H, int E, int E1, int kslice,
-                                                       float* __restrict__ out) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int e0 = blockIdx.x * RT_EPB + wave * 4;
-  const int t0 = blockIdx.y * RT_TT;
-  const int s = blockIdx.z;
-  if (e0 >= E1) return;
-  const int kb = s * kslice;
-  const int ke = min(H, kb + kslice);
-  const WT* wrow[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    int e = e0 + j;
-    wrow[j] = (e < E) ? wr + (size_t)e * H : ((e == E && wseg) ? wseg : wr);
-  }
-  const int nt = min(RT_TT, T - t0);
-  float acc[RT_TT][4];
-#pragma unroll
-  for (int t = 0; t < RT_TT; ++t)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[t][j] = 0.f;
+#define RM_UK 4  // chunks per load batch
 
-  // Rows past the last token re-read the last token (results discarded): the loop body
-  // is branch-free, so its loads are issued together.
-  const float* hrow[RT_TT];
+template <typename WT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void
+k_router_logits(const float* __restrict__ h32, const WT* __restrict__ wr,
+                const WT* __restrict__ wseg, int T, int H, int E, int E1, int kslice,
+                float* __restrict__ out) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 15, q = lane >> 4;
+  const int t0 = blockIdx.x * 64 + (wave & 1) * 32;
+  const int e0 = blockIdx.y * 64 + (wave >> 1) * 32;
+  const int s = blockIdx.z;
+  const int kb = s * kslice, ke = min(H, kb + kslice);
+  if (kb >= ke) return;
+  const float* arow[2];
+  const WT* brow[2];
 #pragma unroll
-  for (int t = 0; t < RT_TT; ++t) hrow[t] = h32 + (size_t)min(t0 + t, T - 1) * H;
-  for (int k = kb + lane * 4; k < ke; k += RT_KCH) {
-    float4 wv[4];
+  for (int a = 0; a < 2; ++a) arow[a] = h32 + (size_t)min(t0 + 16 * a + j, T - 1) * H;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) wv[j] = rt_load4<WT>(wrow[j] + k);
+  for (int b = 0; b < 2; ++b) {
+    const int e = e0 + 16 * b + j;
+    brow[b] = e < E ? wr + (size_t)e * H : ((e == E && wseg) ? wseg : wr + (size_t)(E - 1) * H);
+  }
+  float4_t acc[2][2];
 #pragma unroll
-    for (int t = 0; t < RT_TT; ++t) {
-      const float4 hv = *(const float4*)(hrow[t] + k);
+  for (int a = 0; a < 2; ++a)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float a = acc[t][j];
-        a = fmaf(hv.x, wv[j].x, a);
-        a = fmaf(hv.y, wv[j].y, a);
-        a = fmaf(hv.z, wv[j].z, a);
-        a = fmaf(hv.w, wv[j].w, a);
-        acc[t][j] = a;
-      }
+    for (int b = 0; b < 2; ++b) acc[a][b] = (float4_t){0.f, 0.f, 0.f, 0.f};
+
+  const int nch = (ke - kb + 15) / 16;
+  auto load = [&](int c, float4 (&av)[2], float4 (&bv)[2]) {
+    const int k = kb + 16 * c + 4 * q;
+    const bool in = k < ke;
+    const int kk = in ? k : ke - 4;  // clamped in bounds, masked below
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+      const float4 v = *(const float4*)(arow[a] + kk);
+      av[a] = in ? v : make_float4(0.f, 0.f, 0.f, 0.f);
     }
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const float4 v = rt_load4<WT>(brow[b] + kk);
+      bv[b] = in ? v : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  auto mma = [&](const float4 (&av)[2], const float4 (&bv)[2]) {
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[a].x, bv[b].x, acc[a][b], 0, 0, 0);
+        acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[a].y, bv[b].y, acc[a][b], 0, 0, 0);
+        acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[a].z, bv[b].z, acc[a][b], 0, 0, 0);
+        acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[a].w, bv[b].w, acc[a][b], 0, 0, 0);
+      }
+  };
+  // Batches of RM_UK chunks, two register sets; the batch count is padded to even and
+  // padding chunks read (masked) zeros.
+  const int nb = (nch + RM_UK - 1) / RM_UK;
+  float4 ax[RM_UK][2], bx[RM_UK][2], ay[RM_UK][2], by[RM_UK][2];
+#pragma unroll
+  for (int u = 0; u < RM_UK; ++u) load(u, ax[u], bx[u]);
+  for (int bt = 0; bt < nb; bt += 2) {
+#pragma unroll
+    for (int u = 0; u < RM_UK; ++u) load((bt + 1) * RM_UK + u, ay[u], by[u]);
+#pragma unroll
+    for (int u = 0; u < RM_UK; ++u) mma(ax[u], bx[u]);
+#pragma unroll
+    for (int u = 0; u < RM_UK; ++u) load((bt + 2) * RM_UK + u, ax[u], bx[u]);
+#pragma unroll
+    for (int u = 0; u < RM_UK; ++u) mma(ay[u], by[u]);
   }
 #pragma unroll
-  for (int t = 0; t < RT_TT; ++t) {
-    if (t < nt) {
+  for (int a = 0; a < 2; ++a)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float v = mx_wave_sum(acc[t][j]);
-        if (lane == 0 && e0 + j < E1) out[((size_t)s * T + t0 + t) * E1 + e0 + j] = v;
+    for (int b = 0; b < 2; ++b) {
+      const int e = e0 + 16 * b + j;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = t0 + 16 * a + 4 * q + r;
+        if (t < T && e < E1) out[((size_t)s * T + t) * E1 + e] = acc[a][b][r];
       }
     }
-  }
 }
 
-// Number of H-slices the router uses for T tokens (a pure function of the shape).
+// Number of H-slices the router uses for T tokens (a pure function of the shape): enough
+// 64 x 64 tiles x slices to give about 1024 blocks, at most one slice per RT_KCH columns.
 int mx_router_splits_for(int tokens, int hidden, int e1) {
-  int eblocks = mx_ceil_div(e1, RT_EPB);
-  int tblocks = mx_ceil_div(tokens > 0 ? tokens : 1, RT_TT);
-  int kch = mx_ceil_div(hidden, RT_KCH);
+  const int tiles = mx_ceil_div(tokens > 0 ? tokens : 1, 64) * mx_ceil_div(e1, 64);
+  const int kch = mx_ceil_div(hidden, RT_KCH);
   int s = 1;
-  while (eblocks * tblocks * s < 256 && s * 2 <= kch) s *= 2;
-  int per = mx_ceil_div(kch, s);
+  while (tiles * s < 1024 && s * 2 <= kch && s < 16) s *= 2;
+  const int per = mx_ceil_div(kch, s);
   return mx_ceil_div(kch, per);
 }
 
@@ -224,7 +252,7 @@ extern "C" int mx_router_logits(const float* h32, const void* router_w, const vo
   const int kslice = router_kslice(hidden, splits);
   if (mx_ceil_div(hidden, kslice) != splits) return MX_ERR_INVALID;
   const int e1 = n_experts + (shared_gate_w ? 1 : 0);
-  dim3 grid(mx_ceil_div(e1, RT_EPB), mx_ceil_div(tokens, RT_TT), splits);
+  dim3 grid(mx_ceil_div(tokens, 64), mx_ceil_div(e1, 64), splits);
   mx_clear_error();
   hipStream_t s = (hipStream_t)stream;
   if (param_dtype == MX_DT_F16)
