@@ -342,34 +342,27 @@ __global__ __launch_bounds__(256) void k_expert(const ExpertParams p) {
 //
 // With many rows per expert the activation tile is reused by every column slab, so it is
 // staged once per block in LDS (double-buffered, rows padded by 16 bytes so the 16-byte
-// fragment reads of 8 consecutive lanes hit distinct banks) and shared by the waves of
-// its half.  Weights go straight from HBM into MFMA B registers; each wave holds 4 B
-// fragments per k-chunk (gate/up: 2 gate + 2 up column blocks; down: 4 column blocks),
-// so every A fragment read from LDS feeds 4 MFMAs.
-//
-// A block holds HV halves of 4 waves; half h computes m-tile HV*pair + h for the
-// block's column slab.  The halves run in lock step (one barrier per stage), so when
-// both m-tiles belong to the same expert (hot experts have many consecutive m-tiles)
-// their weight loads hit the same addresses at the same time and HBM serves them once.
-// fp16 uses HV = 2 (8 waves, 2 per SIMD); the int8 variant needs the full register file
-// of one wave per SIMD, so it runs HV = 1.
+// fragment reads of 8 consecutive lanes hit distinct banks) and shared by the 4 waves.
+// Weights go straight from HBM into MFMA B registers; each wave holds 4 B fragments per
+// k-chunk (gate/up: 2 gate + 2 up column blocks; down: 4 column blocks), so every A
+// fragment read from LDS feeds 4 MFMAs, and each wave owns a 128-row x 4-fragment tile.
 //
 // Blocks are numbered so that consecutive logical ids run on the same XCD: hardware
 // block b goes to XCD b % 8, logical id = (b % 8) * (grid / 8) + b / 8.  Logical ids walk
-// the m-tile pairs of one column slab before moving to the next slab.
+// the m-tiles of one column slab before moving to the next slab.  (Sharing an expert's
+// weights between its m-tiles, through L2 or by 256-row tiles, measured slower on
+// MI355X: the sibling tiles drift apart, and the taller tile doubles the LDS reads.)
 // ------------------------------------------------------------------------------------
 // Tunables (compile-time; the defaults are the measured best on MI355X).
 //   MX_LDS_RB:      weight stages in flight per wave (even).
-//   MX_LDS_RA:      activation stages in flight (fp16 gate/up).
-//   MX_LDS_HV_F16:  m-tiles per block for fp16 (1 or 2).
+//   MX_LDS_RA:      activation stages in flight (even, divides RB).
+//   MX_LDS_KM_F16:  MFMA k-steps per stage for fp16 (each weight fragment row is read
+//                   KM * 64 contiguous bytes per stage).
 #ifndef MX_LDS_RB
 #define MX_LDS_RB 4
 #endif
 #ifndef MX_LDS_RA
 #define MX_LDS_RA 4
-#endif
-#ifndef MX_LDS_HV_F16
-#define MX_LDS_HV_F16 1
 #endif
 #ifndef MX_LDS_KM_F16
 #define MX_LDS_KM_F16 1
@@ -380,67 +373,41 @@ __global__ __launch_bounds__(256) void k_expert(const ExpertParams p) {
 
 template <int WF>
 struct LdsShape {
-  static constexpr int HV = WF == MX_DT_F16 ? MX_LDS_HV_F16 : 1;
-  // fp16 at HV = 1 fits two 4-wave blocks per CU; the int8 variant one.
-  static constexpr int OCC = WF == MX_DT_F16 ? (HV == 1 ? 2 : 1) : 1;
+  // fp16 fits two 4-wave blocks per CU; the int8 variant (conversion temporaries, 64-
+  // column stages) needs the full register file of one block per CU to avoid spills.
+  static constexpr int OCC = WF == MX_DT_F16 ? 2 : 1;
   // MFMA k-steps per stage: each weight row is read KM * 64 contiguous bytes per stage.
   static constexpr int KM = WF == MX_DT_F16 ? MX_LDS_KM_F16 : 1;
 };
 
-template <int WF, bool GU>
-__global__ __launch_bounds__(256 * LdsShape<WF>::HV, LdsShape<WF>::OCC) void k_expert_lds(
-    const ExpertParams p, int mt_max, int nblk) {
+// One block's work: MB = 16 * MTX rows (from `base` of group g) x 4 waves of 16 * NBIX
+// columns (x 2 for gate and up) starting at column n0b.
+template <int WF, bool GU, int MTX, int NBIX>
+__device__ __forceinline__ void expert_lds_tile(const ExpertParams& p, char* lds, int g,
+                                                int base, int trows, int n0b) {
   using Tr = WTr<WF>;
-  constexpr int HV = LdsShape<WF>::HV;
   constexpr int EPL = Tr::EPL, ESZ = Tr::ESZ;
   constexpr int KM = LdsShape<WF>::KM;
-  constexpr int KS = 4 * EPL * KM;           // reduction columns per stage: 32 / 64 fp16, 64 int8
-  constexpr int MT = 8, MB = 128;
-  constexpr int NBI = GU ? 2 : 4;
-  constexpr int NF = GU ? 2 * NBI : NBI;
+  constexpr int KS = 4 * EPL * KM;           // reduction columns per stage
+  constexpr int MB = 16 * MTX;
+  constexpr int NF = GU ? 2 * NBIX : NBIX;
   constexpr int AROW = KS * 2 + 16;          // LDS bytes per staged activation row
   constexpr int ATILE = MB * AROW;
   constexpr int CPR = KS * 2 / 16;           // 16-byte chunks per row and stage
   constexpr int ACH = MB * CPR / 256;        // chunks each thread stages
-  constexpr int RB = KM == 1 ? MX_LDS_RB : MX_LDS_RB_KM2;  // weight stages in flight per wave
+  constexpr int RB = KM == 1 ? MX_LDS_RB : MX_LDS_RB_KM2;  // weight stages in flight
   constexpr int RA = (WF == MX_DT_F16 && GU && KM == 1) ? MX_LDS_RA : 2;  // activation stages
   static_assert(RB % RA == 0 && RA % 2 == 0, "ring sizes must divide the unroll");
-  __shared__ __align__(16) char lds[HV][2 * ATILE];
 
-  const int tid = threadIdx.x & 255, lane = tid & 63;
-  const int half = __builtin_amdgcn_readfirstlane(threadIdx.x >> 8);
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave inside the half
-  const int b = blockIdx.x;
-  const int logical = (b & 7) * (gridDim.x >> 3) + (b >> 3);
-  const int npair = (mt_max + HV - 1) / HV;
-  const int nb = logical / npair;
-  const int pair = logical - nb * npair;
-  const int n_mt = min(*p.n_mtiles, mt_max);
-  if (nb >= nblk || pair * HV >= n_mt) return;  // whole block idle
-
-  // Both halves' tiles are read by every wave: the stage count must agree block-wide.
-  int kmax = 0;
-#pragma unroll
-  for (int h = 0; h < HV; ++h) {
-    const int m2 = pair * HV + h;
-    if (m2 < n_mt) {
-      const int e2 = p.g_expert[p.mt_group[m2]];
-      kmax = max(kmax, e2 == p.E ? p.K_s : p.K_r);
-    }
-  }
-  const int mt = pair * HV + half;
-  const bool tile = mt < n_mt;  // a half without a tile streams zeros and stores nothing
-  const int g = tile ? p.mt_group[mt] : 0;
-  const int row0 = tile ? p.mt_row0[mt] : 0;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int eid = p.g_expert[g];
   const int gstart = p.g_start[g];
-  const int gcount = p.g_count[g];
   const bool sh = eid == p.E;
   const int N = sh ? p.N_s : p.N_r;
   const int K = sh ? p.K_s : p.K_r;
-  const int n0 = (nb * 4 + wave) * 16 * NBI;
-  const bool wact = tile && n0 < N;
-  const int mrows = tile ? min(MB, gcount - row0) : 0;
+  const int n0 = n0b + wave * 16 * NBIX;
+  const bool wact = n0 < N;
   const int j = lane & 15, q = lane >> 4;
   const MxExpertPtrs ep = p.experts[eid];
 
@@ -449,14 +416,14 @@ __global__ __launch_bounds__(256 * LdsShape<WF>::HV, LdsShape<WF>::OCC) void k_e
   const mx_rsrc_t rb0 = mx_rsrc(GU ? ep.gate : ep.down, matb);
   const mx_rsrc_t rb1 = mx_rsrc(GU ? ep.up : ep.down, matb);
   const uint32_t bstep = p.tiled ? 1024u : (uint32_t)4 * EPL * ESZ;  // bytes per K chunk
-  uint32_t boff[NBI];
+  uint32_t boff[NBIX];
 #pragma unroll
-  for (int f = 0; f < NBI; ++f) {
+  for (int f = 0; f < NBIX; ++f) {
     const int n = n0 + 16 * f + j;
     boff[f] = (wact && n < N) ? mx_bfrag_base<EPL, ESZ>(p.tiled, n0 + 16 * f, j, q, K) : MX_OOB;
   }
 
-  // Activation chunks this thread stages: fixed rows, advancing columns.
+  // Activation chunks this thread stages: fixed rows of the tile, advancing columns.
   const mx_rsrc_t ra = mx_rsrc(p.a, p.a_bytes);
   uint32_t agoff[ACH];
   int alds[ACH], acol[ACH];
@@ -466,8 +433,8 @@ __global__ __launch_bounds__(256 * LdsShape<WF>::HV, LdsShape<WF>::OCC) void k_e
     const int row = c / CPR, cc = c % CPR;
     acol[i] = cc * 8;
     alds[i] = row * AROW + cc * 16;
-    if (row < mrows) {
-      const int r = gstart + row0 + row;
+    if (row < trows) {
+      const int r = gstart + base + row;
       const int arow = GU ? p.sorted_tok[r] : r;
       agoff[i] = (uint32_t)arow * (uint32_t)p.lda * 2 + cc * 16;
     } else {
@@ -475,13 +442,12 @@ __global__ __launch_bounds__(256 * LdsShape<WF>::HV, LdsShape<WF>::OCC) void k_e
     }
   }
 
-  float4_t acc[MT][NF];
+  float4_t acc[MTX][NF];
 #pragma unroll
-  for (int mi = 0; mi < MT; ++mi)
+  for (int mi = 0; mi < MTX; ++mi)
 #pragma unroll
     for (int f = 0; f < NF; ++f) acc[mi][f] = (float4_t){0.f, 0.f, 0.f, 0.f};
 
-  char* const my_lds = lds[half];
   auto load_a = [&](int st, int4_t (&ar)[ACH]) {
     const int k0 = st * KS;
 #pragma unroll
@@ -495,24 +461,24 @@ __global__ __launch_bounds__(256 * LdsShape<WF>::HV, LdsShape<WF>::OCC) void k_e
       const uint32_t kb = ((uint32_t)st * KM + km) * bstep;
 #pragma unroll
       for (int f = 0; f < NF; ++f) {
-        const int fi = GU ? (f % NBI) : f;
-        br[km][f] = mx_ld16((GU && f >= NBI) ? rb1 : rb0, kin ? boff[fi] + kb : MX_OOB);
+        const int fi = GU ? (f % NBIX) : f;
+        br[km][f] = mx_ld16((GU && f >= NBIX) ? rb1 : rb0, kin ? boff[fi] + kb : MX_OOB);
       }
     }
   };
   auto store_a = [&](int buf, const int4_t (&ar)[ACH]) {
-    char* base = my_lds + buf * ATILE;
+    char* sbase = lds + buf * ATILE;
 #pragma unroll
-    for (int i = 0; i < ACH; ++i) *(int4_t*)(base + alds[i]) = ar[i];
+    for (int i = 0; i < ACH; ++i) *(int4_t*)(sbase + alds[i]) = ar[i];
   };
   auto compute = [&](int buf, const int4_t (&br)[KM][NF]) {
-    const char* base = my_lds + buf * ATILE;
+    const char* cbase = lds + buf * ATILE;
     if constexpr (WF == MX_DT_F16) {
 #pragma unroll
       for (int km = 0; km < KM; ++km)
 #pragma unroll
-        for (int mi = 0; mi < MT; ++mi) {
-          const int4_t a = *(const int4_t*)(base + (16 * mi + j) * AROW + km * 64 + q * 16);
+        for (int mi = 0; mi < MTX; ++mi) {
+          const int4_t a = *(const int4_t*)(cbase + (16 * mi + j) * AROW + km * 64 + q * 16);
 #pragma unroll
           for (int f = 0; f < NF; ++f)
             acc[mi][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
@@ -524,8 +490,8 @@ __global__ __launch_bounds__(256 * LdsShape<WF>::HV, LdsShape<WF>::OCC) void k_e
 #pragma unroll
       for (int f = 0; f < NF; ++f) mx_i8_to_f16(br[0][f], blo[f], bhi[f]);
 #pragma unroll
-      for (int mi = 0; mi < MT; ++mi) {
-        const char* ap = base + (16 * mi + j) * AROW + q * 32;
+      for (int mi = 0; mi < MTX; ++mi) {
+        const char* ap = cbase + (16 * mi + j) * AROW + q * 32;
         const int4_t a0 = *(const int4_t*)ap;
         const int4_t a1 = *(const int4_t*)(ap + 16);
 #pragma unroll
@@ -544,12 +510,11 @@ __global__ __launch_bounds__(256 * LdsShape<WF>::HV, LdsShape<WF>::OCC) void k_e
   // are in flight; the activations of stage s + 1 go to LDS at the end of stage s.  The
   // global latency is hidden by the ring depths, not by the LDS double buffer.  The loop
   // body is branch-free so the in-order load counter is never drained: stages past the
-  // end of K read zeros through the descriptors' bounds check and the stage count (of
-  // the block's longest reduction) is padded to a multiple of RB (a multiple of RA),
-  // which also makes every register-set index static.  A wave without columns (edge of
-  // a narrower shared expert, or a half without a tile) has out-of-range weight offsets,
-  // computes zeros and skips the epilogue.
-  const int nst = (kmax + KS - 1) / KS;
+  // end of K read zeros through the descriptors' bounds check and the stage count is
+  // padded to a multiple of RB (a multiple of RA), which also makes every register-set
+  // index static.  A wave without columns (edge of a narrower shared expert) has
+  // out-of-range weight offsets, computes zeros and skips the epilogue.
+  const int nst = (K + KS - 1) / KS;
   const int nst_pad = (nst + RB - 1) / RB * RB;
   int4_t aring[RA][ACH];
   int4_t bring[RB][KM][NF];
@@ -572,9 +537,10 @@ __global__ __launch_bounds__(256 * LdsShape<WF>::HV, LdsShape<WF>::OCC) void k_e
   }
   if (!wact) return;
 
+  const int orow = gstart + base;  // sorted row of the tile's row 0
   if constexpr (GU) {
 #pragma unroll
-    for (int f = 0; f < NBI; ++f) {
+    for (int f = 0; f < NBIX; ++f) {
       const int n = n0 + 16 * f + j;
       if (n >= N) continue;
       float sg = 1.f, su = 1.f;
@@ -583,36 +549,57 @@ __global__ __launch_bounds__(256 * LdsShape<WF>::HV, LdsShape<WF>::OCC) void k_e
         su = (float)((const half_t*)ep.up_scale)[n];
       }
 #pragma unroll
-      for (int mi = 0; mi < MT; ++mi)
+      for (int mi = 0; mi < MTX; ++mi)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int m = 16 * mi + 4 * q + r;
-          if (m < mrows) {
+          if (m < trows) {
             const float gv = acc[mi][f][r] * sg;
-            const float uv = acc[mi][NBI + f][r] * su;
-            ((half_t*)p.out)[(size_t)(gstart + row0 + m) * p.ldo + n] = (half_t)(mx_silu(gv) * uv);
+            const float uv = acc[mi][NBIX + f][r] * su;
+            ((half_t*)p.out)[(size_t)(orow + m) * p.ldo + n] = (half_t)(mx_silu(gv) * uv);
           }
         }
     }
   } else {
 #pragma unroll
-    for (int f = 0; f < NBI; ++f) {
+    for (int f = 0; f < NBIX; ++f) {
       const int n = n0 + 16 * f + j;
       if (n >= N) continue;
       float sd = 1.f;
       if constexpr (WF == MX_DT_I8) sd = (float)((const half_t*)ep.down_scale)[n];
 #pragma unroll
-      for (int mi = 0; mi < MT; ++mi)
+      for (int mi = 0; mi < MTX; ++mi)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int m = 16 * mi + 4 * q + r;
-          if (m < mrows) {
-            const int row = gstart + row0 + m;
+          if (m < trows) {
+            const int row = orow + m;
             ((float*)p.out)[(size_t)row * p.ldo + n] = p.sorted_w[row] * (acc[mi][f][r] * sd);
           }
         }
     }
   }
+}
+
+template <int WF, bool GU>
+__global__ __launch_bounds__(256, LdsShape<WF>::OCC) void k_expert_lds(
+    const ExpertParams p, int mt_max, int nblk) {
+  constexpr int KS = 4 * WTr<WF>::EPL * LdsShape<WF>::KM;
+  constexpr int NBI = GU ? 2 : 4;
+  constexpr int MB = 128;
+  __shared__ __align__(16) char lds[2 * MB * (KS * 2 + 16)];
+
+  const int b = blockIdx.x;
+  const int logical = (b & 7) * (gridDim.x >> 3) + (b >> 3);
+  const int nb = logical / mt_max;
+  const int mt = logical - nb * mt_max;
+  if (nb >= nblk || mt >= mt_max || mt >= *p.n_mtiles) return;
+  const int g = p.mt_group[mt];
+  const int row0 = p.mt_row0[mt];
+  const int N = p.g_expert[g] == p.E ? p.N_s : p.N_r;
+  const int n0b = nb * 4 * 16 * NBI;
+  if (n0b >= N) return;  // whole block past this expert's columns
+  expert_lds_tile<WF, GU, 8, NBI>(p, lds, g, row0, min(MB, p.g_count[g] - row0), n0b);
 }
 
 // ------------------------------------------------------------------------------------
@@ -724,16 +711,15 @@ static int launch_grouped(const MxMoeDesc* d, const ExpertParams& p, int tokens,
     if (d->weight_dtype == MX_DT_F32) return MX_ERR_INVALID;
     const int cols = 4 * 16 * (GU ? 2 : 4);
     const int nblk = mx_ceil_div(nmax, cols);
-    const int hv = d->weight_dtype == MX_DT_F16 ? LdsShape<MX_DT_F16>::HV : LdsShape<MX_DT_I8>::HV;
-    const long blocks = ((long)mx_ceil_div(mt_max, hv) * nblk + 7) / 8 * 8;
+    const long blocks = ((long)mt_max * nblk + 7) / 8 * 8;
     if (blocks > (1l << 31) - 1) return MX_ERR_UNSUPPORTED;
     mx_clear_error();
     if (d->weight_dtype == MX_DT_F16)
-      hipLaunchKernelGGL((k_expert_lds<MX_DT_F16, GU>), dim3((unsigned)blocks), dim3(256 * hv), 0,
-                         s, p, mt_max, nblk);
+      hipLaunchKernelGGL((k_expert_lds<MX_DT_F16, GU>), dim3((unsigned)blocks), dim3(256), 0, s,
+                         p, mt_max, nblk);
     else
-      hipLaunchKernelGGL((k_expert_lds<MX_DT_I8, GU>), dim3((unsigned)blocks), dim3(256 * hv), 0,
-                         s, p, mt_max, nblk);
+      hipLaunchKernelGGL((k_expert_lds<MX_DT_I8, GU>), dim3((unsigned)blocks), dim3(256), 0, s,
+                         p, mt_max, nblk);
     return mx_launch_status();
   }
   if (m_blk != 16 && m_blk != 32 && m_blk != 64) return MX_ERR_INVALID;
