@@ -142,7 +142,8 @@ int run_stage(int stage, const MxMoeDesc* d, const MxMoeWeights* w, const float*
 }
 
 int forward(const MxMoeDesc* d, const MxMoeWeights* w, const float* x, float* out, int T, void* ws,
-            size_t ws_bytes, hipStream_t s, void* const* events) {
+            size_t ws_bytes, hipStream_t s, void* const* events, int st_begin = 0,
+            int st_end = MX_N_STAGES) {
   MX_TRY(check_desc(d));
   if (!w || !x || !out || !ws || T < 0) return MX_ERR_INVALID;
   if (!w->norm_w || !w->router_w || !w->experts) return MX_ERR_INVALID;
@@ -154,7 +155,7 @@ int forward(const MxMoeDesc* d, const MxMoeWeights* w, const float* x, float* ou
   void* scratch = nullptr;
   MX_TRY(layout(d, T, ws, &v, &need, &scratch));
   if (ws_bytes < need) return MX_ERR_WORKSPACE;
-  for (int st = 0; st < MX_N_STAGES; ++st) {
+  for (int st = st_begin; st < st_end; ++st) {
     if (events) MX_TRY(mx_status(hipEventRecord((hipEvent_t)events[st], s)));
     MX_TRY(run_stage(st, d, w, x, out, T, v, scratch, s));
   }
@@ -191,4 +192,14 @@ extern "C" int mx_moe_forward_profiled(const MxMoeDesc* desc, const MxMoeWeights
     if (!events[i]) return MX_ERR_INVALID;
   return forward(desc, weights, x, out, tokens, workspace, workspace_bytes, (hipStream_t)stream,
                  events);
+}
+
+extern "C" int mx_moe_forward_stages(const MxMoeDesc* desc, const MxMoeWeights* weights,
+                                     const float* x, float* out, int32_t tokens, void* workspace,
+                                     size_t workspace_bytes, int32_t stage_begin,
+                                     int32_t stage_end, void* stream) {
+  if (stage_begin < 0 || stage_end > MX_N_STAGES || stage_begin > stage_end)
+    return MX_ERR_INVALID;
+  return forward(desc, weights, x, out, tokens, workspace, workspace_bytes, (hipStream_t)stream,
+                 nullptr, stage_begin, stage_end);
 }

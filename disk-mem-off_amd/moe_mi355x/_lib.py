@@ -29,6 +29,7 @@ MX_DT_I8 = 2
 MX_ROUTER_REF_SOFTMAX_BIAS = 0
 MX_ROUTER_SIGMOID_SELECT_BIAS = 1
 MX_ROUTER_SOFTMAX = 2
+MX_STAGE_ROUTE_END = 4
 MX_LAYOUT_ROWS = 0
 MX_LAYOUT_FRAG16 = 1
 
@@ -136,6 +137,9 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                   c_int32, c_void_p, c_void_p]),
     "mx_fill_normal": (ctypes.c_int, [c_void_p, c_int32, c_size_t, c_uint64, c_uint64,
                                       c_uint64, c_float, c_void_p]),
+    "mx_moe_forward_stages": (ctypes.c_int, [P(MxMoeDesc), P(MxMoeWeights), c_void_p, c_void_p,
+                                             c_int32, c_void_p, c_size_t, c_int32, c_int32,
+                                             c_void_p]),
     "mx_tile_weights": (ctypes.c_int, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p]),
     "mx_quantize_rows_i8": (ctypes.c_int, [c_void_p, c_int32, c_int32, c_int32, c_void_p,
                                            c_void_p, c_void_p]),

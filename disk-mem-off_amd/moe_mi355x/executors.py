@@ -88,6 +88,45 @@ class _MoeExecutorBase:
         weights = self._runner.bind(layout, int(device_weights.handle), stream)
         return self._runner.forward_numpy(desc, weights, x, stream)
 
+    def moe_block_granular(self, layer: LayerSpec, x: np.ndarray, device_weights: DeviceBuffer,
+                           backend: Any, stream: Any,
+                           fetch: Callable[[list[int]], None]) -> np.ndarray:
+        """The MoE step when only the layer's non-expert bytes are on the device yet: route
+        on the device, ``fetch(expert_ids)`` (the caller copies those routed experts into
+        ``device_weights`` and makes ``stream`` wait for the copies), then the experts."""
+        if device_weights.backend != "rocm":
+            raise RuntimeError("the MoE step needs the MI355X backend; got "
+                               f"{device_weights.backend!r} device buffers")
+        if device_weights.nbytes < layer.nbytes:
+            raise RuntimeError(f"Layer {layer.layer_id}: device buffer size "
+                               f"{device_weights.nbytes} < expected {layer.nbytes}")
+        layout = self._layout(layer)
+        desc = self.moe_config(layout).desc()
+        if self._runner is None:
+            self._runner = MoeRunner(backend)
+        T = int(np.shape(x)[0])
+        self._runner.reserve(desc, max(T, self.max_tokens, 1))
+        weights = self._runner.bind(layout, int(device_weights.handle), stream)
+        active = self._runner.route_numpy(desc, weights, x, stream)
+        fetch(active)
+        return self._runner.finish_numpy(desc, weights, stream)
+
+    def expert_ranges(self, layer: LayerSpec) -> tuple[list[tuple[int, int]], list[tuple[int, int]]]:
+        """(core byte ranges, per-routed-expert byte ranges) of a packed MoE layer."""
+        lay = self._layout(layer)
+        return lay.core_ranges(layer.nbytes), lay.routed_expert_ranges()
+
+    def run_layer_granular(self, layer: LayerSpec, activations: Any, device_weights: DeviceBuffer,
+                           backend: Any, stream: Any, fetch: Callable[[list[int]], None]) -> Any:
+        """``run_layer`` for a layer whose routed experts are copied on demand."""
+        x = np.asarray(activations, dtype=np.float32)
+        if self.attention is not None:
+            x = self.attention(x, layer, device_weights, backend, stream)
+        elif not self._moe_only(layer):
+            raise NotImplementedError(
+                "layer holds attention tensors; pass attention=... to run them")
+        return self.moe_block_granular(layer, x, device_weights, backend, stream, fetch)
+
     def run_layer(self, layer: LayerSpec, activations: Any, device_weights: DeviceBuffer,
                   backend: Any, stream: Any) -> Any:
         x = np.asarray(activations, dtype=np.float32)

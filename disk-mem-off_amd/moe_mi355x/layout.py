@@ -200,6 +200,28 @@ class MoeLayerLayout:
             rows.append((-1,) * 6)
         return rows
 
+    def routed_expert_ranges(self) -> list[tuple[int, int]]:
+        """Byte range [start, end) of each routed expert's tensors (weights and scales);
+        the loader's lexicographic packing keeps each expert's tensors adjacent."""
+        out = []
+        for e in range(self.n_experts):
+            ms = self._experts[e].values()
+            out.append((min(int(m["offset"]) for m in ms),
+                        max(int(m["offset"]) + int(m["nbytes"]) for m in ms)))
+        return out
+
+    def core_ranges(self, total: int) -> list[tuple[int, int]]:
+        """Byte ranges of [0, total) outside every routed expert: norms, router, bias,
+        shared expert(s), any other tensor of the layer, and padding."""
+        out, pos = [], 0
+        for a, b in sorted(self.routed_expert_ranges()):
+            if a > pos:
+                out.append((pos, a))
+            pos = max(pos, b)
+        if pos < total:
+            out.append((pos, total))
+        return out
+
     def expert_matrices(self) -> list[tuple[int, int, int]]:
         """(byte offset, rows, cols) of every expert weight matrix, shared expert last."""
         out = []

@@ -110,6 +110,7 @@ class MoeRunner:
         self._table_key: Any = None
         self._io: dict[str, DeviceBuffer] = {}
         self._pinned: dict[str, Any] = {}
+        self._split_tokens = 0
 
     # -- allocation (never called from forward_device) --
     def reserve(self, desc: _lib.MxMoeDesc, tokens: int) -> None:
@@ -191,6 +192,51 @@ class MoeRunner:
         self.backend.copy_d2h_ptr_async(addr_o, self._io["out"].handle, nb, stream)
         self.backend.synchronize_stream(stream)
         return np.frombuffer(po.view, dtype=np.float32, count=T * desc.hidden).reshape(T, -1).copy()
+
+    # -- split forward (router part, then the expert part after the experts are copied) --
+    def route_numpy(self, desc: _lib.MxMoeDesc, weights: _lib.MxMoeWeights, x: np.ndarray,
+                    stream: Any) -> list[int]:
+        """Upload x and run stages 0..3 (RMSNorm, router, top-k, dispatch); returns the
+        routed experts the batch uses, ascending (synchronises ``stream``)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        if x.ndim != 2 or x.shape[1] != desc.hidden:
+            raise ValueError(f"activations must be [T, {desc.hidden}], got {x.shape}")
+        T = x.shape[0]
+        self.reserve(desc, max(T, 1))
+        self._split_tokens = T
+        if T == 0:
+            return []
+        px = self._pinned["x"]
+        np.frombuffer(px.view, dtype=np.uint8, count=x.nbytes)[:] = x.view(np.uint8).ravel()
+        self.backend.copy_h2d_ptr_async(self._io["x"].handle,
+                                        ctypes.addressof(ctypes.c_char.from_buffer(px.view)),
+                                        x.nbytes, stream)
+        self._stages(desc, weights, T, 0, _lib.MX_STAGE_ROUTE_END, stream)
+        v = self.views(desc, T)
+        ng = int(read_device(self.backend, v.n_groups, np.int32, 1, stream)[0])
+        ge = read_device(self.backend, v.g_expert, np.int32, ng, stream)
+        return sorted(int(e) for e in ge if e < desc.n_experts)
+
+    def finish_numpy(self, desc: _lib.MxMoeDesc, weights: _lib.MxMoeWeights,
+                     stream: Any) -> np.ndarray:
+        """Stages 4..6 for the batch of the last ``route_numpy``; synchronises ``stream``."""
+        T = self._split_tokens
+        nb = T * desc.hidden * 4
+        if T == 0:
+            return np.zeros((0, desc.hidden), np.float32)
+        self._stages(desc, weights, T, _lib.MX_STAGE_ROUTE_END, _lib.MX_N_STAGES, stream)
+        po = self._pinned["out"]
+        addr_o = ctypes.addressof(ctypes.c_char.from_buffer(po.view))
+        self.backend.copy_d2h_ptr_async(addr_o, self._io["out"].handle, nb, stream)
+        self.backend.synchronize_stream(stream)
+        return np.frombuffer(po.view, dtype=np.float32, count=T * desc.hidden).reshape(T, -1).copy()
+
+    def _stages(self, desc, weights, T: int, begin: int, end: int, stream: Any) -> None:
+        ws = self._ws
+        _lib.check(self.lib.mx_moe_forward_stages(ctypes.byref(desc), ctypes.byref(weights),
+                                                  self._io["x"].handle, self._io["out"].handle,
+                                                  T, ws.handle, ws.nbytes, begin, end, stream),
+                   "mx_moe_forward_stages")
 
     # -- inspection --
     def views(self, desc: _lib.MxMoeDesc, tokens: int) -> _lib.MxMoeViews:

@@ -101,6 +101,8 @@ class _Inflight:
     copied: Any  # event recorded after the copy on the transfer stream
     t_start: Any = None  # timing events (GPU backends)
     t_end: Any = None
+    granular: bool = False  # routed experts are copied on demand
+    extra_copies: list = field(default_factory=list)  # timing events of on-demand copies
 
 
 class OffloadRuntime:
@@ -115,6 +117,7 @@ class OffloadRuntime:
         use_pinned_staging: bool = False,
         dequantizer: Any | None = None,
         transfer_lookahead: int | None = None,
+        expert_granular: bool = False,
     ) -> None:
         self.layers = {layer.layer_id: layer for layer in layers}
         self.backend = backend
@@ -135,6 +138,17 @@ class OffloadRuntime:
         self.transfer_lookahead = transfer_lookahead
         self._timing = hasattr(backend, "create_timing_event")
         self._deferred_free: list[tuple[DeviceBuffer, Any]] = []
+        # Expert-granular transfer: ahead of compute only the bytes outside the routed
+        # experts are copied; after the layer's router has run, the executor asks for the
+        # routed experts it needs (run_layer_granular + fetch).
+        self.expert_granular = bool(expert_granular)
+        if self.expert_granular:
+            if not hasattr(executor, "run_layer_granular"):
+                raise ValueError("expert_granular needs an executor with run_layer_granular")
+            if not hasattr(backend, "copy_h2d_ptr_async"):
+                raise ValueError("expert_granular needs a backend with pointer copies")
+            if dequantizer is not None:
+                raise ValueError("expert_granular copies raw layer bytes; no host dequantizer")
 
     def __enter__(self) -> "OffloadRuntime":
         return self
@@ -215,14 +229,19 @@ class OffloadRuntime:
             lm.compressed_nbytes = compressed
             metrics.compressed_bytes += compressed
         nbytes = host.nbytes
-        staged = self._stage_pinned(host)
+        granular = self.expert_granular and layer.metadata.get("is_moe", True)
+        staged = host if granular else self._stage_pinned(host)
         device = self._alloc_device(nbytes)
         t0 = time.perf_counter()
         t_start = t_end = None
         if self._timing:
             t_start = self.backend.create_timing_event()
             self.backend.record(t_start, self.transfer_stream)
-        self.backend.copy_h2d_async(device, staged, self.transfer_stream)
+        if granular:
+            core, _ = self.executor.expert_ranges(layer)
+            nbytes = self._copy_ranges(device, staged, core)
+        else:
+            self.backend.copy_h2d_async(device, staged, self.transfer_stream)
         if self._timing:
             t_end = self.backend.create_timing_event()
             self.backend.record(t_end, self.transfer_stream)
@@ -232,7 +251,47 @@ class OffloadRuntime:
         lm.nbytes = nbytes
         metrics.transfer_seconds += elapsed
         metrics.transferred_bytes += nbytes
-        return _Inflight(index, layer, lm, host, staged, device, copied, t_start, t_end)
+        return _Inflight(index, layer, lm, host, staged, device, copied, t_start, t_end,
+                         granular)
+
+    def _copy_ranges(self, device: DeviceBuffer, host: HostBuffer,
+                     ranges: list[tuple[int, int]]) -> int:
+        """H2D of byte ranges of a layer into the same offsets of its device buffer, on
+        the transfer stream; returns the bytes enqueued."""
+        import numpy as np
+
+        base = int(np.frombuffer(host.view, dtype=np.uint8).ctypes.data)
+        total = 0
+        for a, b in ranges:
+            if b > a:
+                self.backend.copy_h2d_ptr_async(int(device.handle) + a, base + a, b - a,
+                                                self.transfer_stream)
+                total += b - a
+        return total
+
+    def _fetch_experts(self, rec: "_Inflight", ids: list[int], metrics: RuntimeMetrics) -> None:
+        """Copy the routed experts ``ids`` of an in-flight layer and make the compute
+        stream wait for them."""
+        _, per_expert = self.executor.expert_ranges(rec.layer)
+        t0 = time.perf_counter()
+        ev_a = ev_b = None
+        if self._timing:
+            ev_a = self.backend.create_timing_event()
+            self.backend.record(ev_a, self.transfer_stream)
+        n = self._copy_ranges(rec.device, rec.staged, [per_expert[e] for e in ids])
+        if self._timing:
+            ev_b = self.backend.create_timing_event()
+            self.backend.record(ev_b, self.transfer_stream)
+        done = self.backend.record_event(self.transfer_stream)
+        self.backend.wait_event(self.compute_stream, done)
+        self.backend.destroy_event(done)
+        elapsed = time.perf_counter() - t0
+        rec.lm.h2d_ms += elapsed * 1000
+        rec.lm.nbytes += n
+        metrics.transfer_seconds += elapsed
+        metrics.transferred_bytes += n
+        if ev_a is not None:
+            rec.extra_copies.append((ev_a, ev_b))
 
     def run_inference(self, ordered_layer_ids: list[int], inputs: Any) -> tuple[Any, RuntimeMetrics]:
         unknown = [lid for lid in ordered_layer_ids if lid not in self.layers]
@@ -262,13 +321,23 @@ class OffloadRuntime:
                     c_start = self.backend.create_timing_event()
                     self.backend.record(c_start, self.compute_stream)
                 t1 = time.perf_counter()
-                activations = self.executor.run_layer(
-                    layer=rec.layer,
-                    activations=activations,
-                    device_weights=rec.device,
-                    backend=self.backend,
-                    stream=self.compute_stream,
-                )
+                if rec.granular:
+                    activations = self.executor.run_layer_granular(
+                        layer=rec.layer,
+                        activations=activations,
+                        device_weights=rec.device,
+                        backend=self.backend,
+                        stream=self.compute_stream,
+                        fetch=lambda ids, rec=rec: self._fetch_experts(rec, ids, metrics),
+                    )
+                else:
+                    activations = self.executor.run_layer(
+                        layer=rec.layer,
+                        activations=activations,
+                        device_weights=rec.device,
+                        backend=self.backend,
+                        stream=self.compute_stream,
+                    )
                 compute_elapsed = time.perf_counter() - t1
                 if self._timing:
                     c_end = self.backend.create_timing_event()
@@ -283,7 +352,8 @@ class OffloadRuntime:
                     self._wait_copy(rec)
                     self._pinned_pool.release(rec.staged)
                 self.backend.destroy_event(rec.copied)
-                timings.append((rec.lm, rec.t_start, rec.t_end, c_start, c_end))
+                timings.append((rec.lm, rec.t_start, rec.t_end, c_start, c_end,
+                                rec.extra_copies))
                 metrics.layer_metrics.append(rec.lm)
                 self._flush_deferred()
 
@@ -305,14 +375,15 @@ class OffloadRuntime:
         metrics.end_to_end_seconds = time.perf_counter() - wall_start
         if self._timing and timings:
             first = None
-            for lm, hs, he, cs, ce in timings:
-                lm.h2d_gpu_ms = self.backend.elapsed_ms(hs, he)
+            for lm, hs, he, cs, ce, extra in timings:
+                lm.h2d_gpu_ms = self.backend.elapsed_ms(hs, he) + \
+                    sum(self.backend.elapsed_ms(a, b) for a, b in extra)
                 lm.compute_gpu_ms = self.backend.elapsed_ms(cs, ce)
                 metrics.transfer_gpu_seconds += lm.h2d_gpu_ms / 1000
                 metrics.compute_gpu_seconds += lm.compute_gpu_ms / 1000
                 first = hs if first is None else first
             metrics.device_seconds = self.backend.elapsed_ms(first, timings[-1][4]) / 1000
-            for _, hs, he, cs, ce in timings:
-                for ev in (hs, he, cs, ce):
+            for _, hs, he, cs, ce, extra in timings:
+                for ev in (hs, he, cs, ce, *[x for pair in extra for x in pair]):
                     self.backend.destroy_event(ev)
         return activations, metrics

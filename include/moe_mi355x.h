@@ -190,6 +190,15 @@ int mx_moe_forward(const MxMoeDesc* desc, const MxMoeWeights* weights, const flo
  * Stages: 0 rmsnorm, 1 router logits, 2 router top-k, 3 dispatch, 4 expert gate/up,
  * 5 expert down, 6 combine.                                                           */
 #define MX_N_STAGES 7
+/* Stages [stage_begin, stage_end) of mx_moe_forward on the same workspace: the router part
+ * (0..3) and the expert part (4..6) can run as two calls, with the routed experts' weights
+ * copied in between.  Splits the reference's _moe_mlp_block (glm4_moe.py:176-240) at the
+ * point where the active expert set (glm4_moe.py:206, set(topk_indices)) is known, which
+ * the expert-granular transfer of an offloaded layer needs.                            */
+#define MX_STAGE_ROUTE_END 4
+int mx_moe_forward_stages(const MxMoeDesc* desc, const MxMoeWeights* weights, const float* x,
+                          float* out, int32_t tokens, void* workspace, size_t workspace_bytes,
+                          int32_t stage_begin, int32_t stage_end, void* stream);
 int mx_moe_forward_profiled(const MxMoeDesc* desc, const MxMoeWeights* weights,
                             const float* x, float* out, int32_t tokens, void* workspace,
                             size_t workspace_bytes, void* stream, void* const* events,

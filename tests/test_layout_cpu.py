@@ -134,3 +134,30 @@ def test_layout_constants_match_header():
     hdr = (Path(__file__).resolve().parents[1] / "include" / "moe_mi355x.h").read_text()
     assert "#define MX_LAYOUT_ROWS 0" in hdr and "#define MX_LAYOUT_FRAG16 1" in hdr
     assert _lib.MX_LAYOUT_ROWS == 0 and _lib.MX_LAYOUT_FRAG16 == 1
+
+
+# ---- byte ranges for expert-granular transfer ---------------------------------------------
+
+def test_expert_and_core_ranges_partition_the_layer():
+    shape = syn.MoeShape(syn.GLM, 64, 12, 2, 32, 32, 2.5, 1e-5)
+    t = quantize_moe_tensors(syn.make_tensors(shape, 5))
+    raw, meta = pack_tensors(t)
+    lay = MoeLayerLayout.from_meta(meta)
+    ranges = lay.routed_expert_ranges()
+    core = lay.core_ranges(len(raw))
+    assert len(ranges) == 12
+    # every routed tensor (weights and scales) lies in its expert's range, nothing else does
+    for m in meta:
+        a, b = m["offset"], m["offset"] + m["nbytes"]
+        if m["name"].startswith("mlp.experts."):
+            e = int(m["name"].split(".")[2])
+            assert ranges[e][0] <= a and b <= ranges[e][1]
+        else:
+            assert any(ca <= a and b <= cb for ca, cb in core), m["name"]
+    # the pieces tile [0, nbytes) without overlap
+    pieces = sorted(ranges + core)
+    pos = 0
+    for a, b in pieces:
+        assert a == pos and b > a
+        pos = b
+    assert pos == len(raw)

@@ -160,3 +160,28 @@ def test_transfers_issued_ahead_of_compute():
     rt = runtime(4, 2, backend=Spy(), executor=Ex())
     rt.run_inference([0, 1, 2, 3], inputs=0)
     assert events == ["copy0", "copy1", "copy2", "run0", "copy3", "run1", "run2", "run3"]
+
+
+def test_expert_granular_needs_capable_executor_and_backend():
+    from moe_mi355x.backends import NullBackend
+    from moe_mi355x.runtime import OffloadRuntime
+    from moe_mi355x.scheduler import LookaheadScheduler
+    from moe_mi355x.storage import InMemoryStorage
+
+    class Plain:
+        def run_layer(self, layer, activations, device_weights, backend, stream):
+            return activations
+
+    class Granular(Plain):
+        def run_layer_granular(self, layer, activations, device_weights, backend, stream, fetch):
+            return activations
+
+        def expert_ranges(self, layer):
+            return [], []
+
+    with pytest.raises(ValueError, match="run_layer_granular"):
+        OffloadRuntime([], NullBackend(), InMemoryStorage({}), LookaheadScheduler(1), Plain(),
+                       expert_granular=True)
+    with pytest.raises(ValueError, match="pointer copies"):
+        OffloadRuntime([], NullBackend(), InMemoryStorage({}), LookaheadScheduler(1), Granular(),
+                       expert_granular=True)
