@@ -45,11 +45,15 @@ __device__ __forceinline__ int4_t mx_ld16(mx_rsrc_t r, uint32_t off) {
 // probe; the decode block: 1.07 -> 0.96 ms).  The prefill kernel keeps the default
 // policy: the sibling m-tiles of a hot expert re-read its weights and find part of them
 // in L2 (with nt the 2048-token prefill slowed from 2.19 to 2.58 ms).
+// Exception: the int8 gate/up launch of single-m-frag tiles without a K split (a decode
+// step touching few experts) streams faster with the default policy (GLM-4.7 int8,
+// 1 token: 25 vs 30 µs).
 #ifndef MX_W_NT
 #define MX_W_NT 1
 #endif
+template <bool NT>
 __device__ __forceinline__ int4_t mx_ldw16(mx_rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, MX_W_NT ? 2 : 0);
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, (MX_W_NT && NT) ? 2 : 0);
 }
 
 template <int WF>
@@ -116,7 +120,7 @@ __device__ __forceinline__ uint32_t mx_bfrag_base(bool tiled, int n16, int j, in
                : (uint32_t)(n16 + j) * (uint32_t)K * ESZ + (uint32_t)q * EPL * ESZ;
 }
 
-template <int WF, int MT, int NBI, bool GU, int UK, int KS>
+template <int WF, int MT, int NBI, bool GU, int UK, int KS, bool NT>
 __global__ __launch_bounds__(256) void k_expert(const ExpertParams p) {
   using Tr = WTr<WF>;
   constexpr int EPL = Tr::EPL, ESZ = Tr::ESZ, AESZ = Tr::AESZ, AV = Tr::AV;
@@ -188,7 +192,7 @@ __global__ __launch_bounds__(256) void k_expert(const ExpertParams p) {
     for (int f = 0; f < NF; ++f) {
       const int fi = GU ? (f % NBI) : f;
       const uint32_t o = kin ? boff[fi] + kb : MX_OOB;
-      b[f] = mx_ldw16((GU && f >= NBI) ? rb1 : rb0, o);
+      b[f] = mx_ldw16<NT>((GU && f >= NBI) ? rb1 : rb0, o);
     }
 #pragma unroll
     for (int mi = 0; mi < MT; ++mi)
@@ -679,9 +683,10 @@ static void launch_expert_ks(const ExpertParams& p, int mt_max, int nmax, hipStr
   constexpr int NBI = GU ? MX_DEC_NBI_GU : MX_DEC_NBI_DN;
   constexpr int UK = (WF == MX_DT_I8) ? (MT >= 4 ? 1 : MX_DEC_UK / 2)
                                       : (MT >= 4 ? 2 : MX_DEC_UK);
+  constexpr bool NT = !(WF == MX_DT_I8 && GU && MT == 1 && KS == 1);
   const dim3 grid(mt_max, mx_ceil_div(nmax, (4 / KS) * 16 * NBI));
   mx_clear_error();
-  hipLaunchKernelGGL((k_expert<WF, MT, NBI, GU, UK, KS>), grid, dim3(256), 0, s, p);
+  hipLaunchKernelGGL((k_expert<WF, MT, NBI, GU, UK, KS, NT>), grid, dim3(256), 0, s, p);
 }
 
 template <int WF, int MT, bool GU>
