@@ -51,9 +51,12 @@ __device__ __forceinline__ int4_t mx_ld16(mx_rsrc_t r, uint32_t off) {
 #ifndef MX_W_NT
 #define MX_W_NT 1
 #endif
+#ifndef MX_W_AUX
+#define MX_W_AUX 2  // cache-policy bits of the hinted loads (nt)
+#endif
 template <bool NT>
 __device__ __forceinline__ int4_t mx_ldw16(mx_rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, (MX_W_NT && NT) ? 2 : 0);
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, (MX_W_NT && NT) ? MX_W_AUX : 0);
 }
 
 template <int WF>
