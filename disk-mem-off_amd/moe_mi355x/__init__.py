@@ -5,7 +5,7 @@ this package is the host side: backend, pools, runtime, layer layout and executo
 """
 from .backends import DeviceBackend, MI355XBackend, NullBackend, ROCmBackend, detect_backend
 from .buffer_pool import DeviceBufferPool, PinnedHostBufferPool
-from .executors import GLM4MoeExecutor, Qwen3NextExecutor
+from .executors import GLM4MoeExecutor, Qwen3NextExecutor, host_attention, read_layer_tensors
 from .layout import MoeLayerLayout, make_layer_spec, pack_tensors, unpack_host
 from .moe import ROUTER_MODES, MoeConfig, MoeRunner
 from .quantize import (CompositeDequantizer, Float16Dequantizer, Int8Dequantizer,
@@ -22,6 +22,6 @@ __all__ = [
     "MI355XBackend", "MoeConfig", "MoeLayerLayout", "MoeRunner", "NullBackend",
     "OffloadRuntime", "PinnedHostBufferPool", "PrefetchScheduler", "Qwen3NextExecutor",
     "ROCmBackend", "ROUTER_MODES", "RuntimeMetrics", "dequantize_rows_int8", "detect_backend",
-    "make_layer_spec", "pack_tensors", "quantize_moe_tensors", "quantize_rows_int8",
-    "unpack_host",
+    "host_attention", "make_layer_spec", "pack_tensors", "quantize_moe_tensors",
+    "quantize_rows_int8", "read_layer_tensors", "unpack_host",
 ]

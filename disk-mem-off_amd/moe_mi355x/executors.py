@@ -8,10 +8,12 @@ step ``_moe_mlp_block`` is replaced: it consumes the layer's ``DeviceBuffer`` in
 ``layer.metadata["tensors"]`` offsets.
 
 Attention is not part of this package.  ``run_layer`` runs layers that hold only the MoE
-block tensors directly; for full transformer layers pass ``attention=callable`` (for
-example the reference executor's own ``_attention_block`` over read-back attention
-tensors), which receives ``(x, layer, device_weights, backend, stream)`` and returns the
-post-attention activations.
+block tensors directly; for full transformer layers pass ``attention=callable``, which
+receives ``(x, layer, device_weights, backend, stream)`` and returns the post-attention
+activations.  ``host_attention(fn)`` builds one from a host function ``fn(x, tensors)`` (for
+example the reference executor's own ``_attention_block``): it copies back only the
+layer's non-MLP tensors (``read_layer_tensors``) where the reference reads back the whole
+layer (glm4_moe.py:96-97, _common.py:20-34).
 
 Before ``run_layer`` returns, the compute stream is synchronised: the runtime frees or
 re-pools ``device_weights`` right after the call (runtime.py:180).
@@ -25,7 +27,7 @@ import numpy as np
 from . import _lib
 from .layout import NORM, MoeLayerLayout
 from .moe import MoeConfig, MoeRunner
-from .types import DeviceBuffer, LayerSpec
+from .types import DeviceBuffer, HostBuffer, LayerSpec
 
 AttentionFn = Callable[[np.ndarray, LayerSpec, DeviceBuffer, Any, Any], np.ndarray]
 
@@ -33,6 +35,71 @@ AttentionFn = Callable[[np.ndarray, LayerSpec, DeviceBuffer, Any, Any], np.ndarr
 def _rms_norm_np(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
     rms = np.sqrt(np.mean(x ** 2, axis=-1, keepdims=True) + eps)
     return w * (x / rms)
+
+
+def _merge_ranges(ranges: list[tuple[int, int]], gap: int) -> list[tuple[int, int]]:
+    """Sorted, merged byte ranges; ranges less than ``gap`` bytes apart are joined."""
+    out: list[tuple[int, int]] = []
+    for a, b in sorted(ranges):
+        if out and a - out[-1][1] < gap:
+            out[-1] = (out[-1][0], max(out[-1][1], b))
+        else:
+            out.append((a, b))
+    return out
+
+
+def read_layer_tensors(layer: LayerSpec, device_weights: DeviceBuffer, backend: Any,
+                       stream: Any, keep: Callable[[str], bool] | None = None,
+                       gap: int = 1 << 16) -> dict[str, np.ndarray]:
+    """Copy the tensors ``keep`` selects (by default every tensor outside the MoE block:
+    the attention weights and ``input_layernorm``) back to the host and return them by name.
+
+    Only the selected byte ranges travel (neighbours closer than ``gap`` bytes share one
+    copy); backends without pointer copies read the whole layer back, as
+    _common.py:20-34 does.  The stream is synchronised before returning.
+    """
+    keep = keep or (lambda n: not n.startswith("mlp.") and n != NORM)
+    metas = [m for m in layer.metadata["tensors"] if keep(m["name"])]
+    out: dict[str, np.ndarray] = {}
+    if not metas:
+        return out
+
+    def view(chunk: np.ndarray, base: int, m: dict[str, Any]) -> np.ndarray:
+        dt = np.dtype(m["dtype"])
+        a = m["offset"] - base
+        return chunk[a:a + m["nbytes"]].view(dt).reshape(m["shape"])
+
+    if not hasattr(backend, "copy_d2h_ptr_async"):
+        buf = np.empty(device_weights.nbytes, np.uint8)
+        backend.copy_d2h_async(HostBuffer(view=memoryview(buf)), device_weights, stream)
+        backend.synchronize_stream(stream)
+        return {m["name"]: view(buf, 0, m) for m in metas}
+    spans = _merge_ranges([(m["offset"], m["offset"] + m["nbytes"]) for m in metas], gap)
+    chunks = []
+    for a, b in spans:
+        chunk = np.empty(b - a, np.uint8)
+        backend.copy_d2h_ptr_async(int(chunk.ctypes.data), int(device_weights.handle) + a,
+                                   b - a, stream)
+        chunks.append((a, b, chunk))
+    backend.synchronize_stream(stream)
+    for m in metas:
+        a, _, chunk = next(c for c in chunks if c[0] <= m["offset"] < c[1] or
+                           (m["nbytes"] == 0 and c[0] <= m["offset"] <= c[1]))
+        out[m["name"]] = view(chunk, a, m)
+    return out
+
+
+def host_attention(fn: Callable[[np.ndarray, dict[str, np.ndarray]], np.ndarray],
+                   keep: Callable[[str], bool] | None = None) -> AttentionFn:
+    """An ``attention=`` hook that runs ``fn(x, tensors)`` on the host over the layer's
+    non-MLP tensors, copied back by ``read_layer_tensors``."""
+
+    def run(x: np.ndarray, layer: LayerSpec, device_weights: DeviceBuffer, backend: Any,
+            stream: Any) -> np.ndarray:
+        t = read_layer_tensors(layer, device_weights, backend, stream, keep)
+        return np.asarray(fn(x, t), dtype=np.float32)
+
+    return run
 
 
 class _MoeExecutorBase:

@@ -79,3 +79,76 @@ def test_embed_and_lm_head():
     h = np.ones((1, 4), np.float32)
     logits = ex.lm_head(h, np.ones(4, np.float32), np.eye(4, dtype=np.float32))
     np.testing.assert_allclose(logits, np.ones((1, 4)), rtol=1e-5)
+
+
+def _attention_layer(seed=5):
+    rng = np.random.default_rng(seed)
+    shape = syn.MoeShape(syn.GLM, 32, 4, 2, 16, 16, 2.5, 1e-5)
+    t = syn.make_tensors(shape, 1)
+    t["input_layernorm.weight"] = rng.standard_normal(32).astype(np.float32)
+    t["self_attn.q_proj.weight"] = rng.standard_normal((32, 32)).astype(np.float16)
+    t["self_attn.o_proj.weight"] = rng.standard_normal((32, 32)).astype(np.float32)
+    buf, meta = pack_tensors(t, align=16)
+    return t, buf, make_layer_spec(0, meta, len(buf))
+
+
+class _PtrBackend(NullBackend):
+    """NullBackend with pointer D2H copies over one numpy array; logs the byte counts."""
+
+    def __init__(self, data):
+        super().__init__()
+        self.data = np.frombuffer(bytes(data), np.uint8)
+        self.copied = []
+
+    def copy_d2h_ptr_async(self, dst_addr, src, nbytes, stream):
+        import ctypes
+        ctypes.memmove(dst_addr, self.data.ctypes.data + src, nbytes)
+        self.copied.append(nbytes)
+
+
+def test_read_layer_tensors_copies_only_non_mlp_ranges():
+    from moe_mi355x.executors import DeviceBuffer, read_layer_tensors
+
+    t, buf, layer = _attention_layer()
+    be = _PtrBackend(buf)
+    dev = DeviceBuffer(handle=0, nbytes=len(buf), backend="null")
+    got = read_layer_tensors(layer, dev, be, None, gap=1)
+    assert set(got) == {"input_layernorm.weight", "self_attn.q_proj.weight",
+                        "self_attn.o_proj.weight"}
+    for n, v in got.items():
+        assert v.dtype == t[n].dtype and np.array_equal(v, t[n])
+    want = sum(t[n].nbytes for n in got)
+    assert want <= sum(be.copied) < len(buf) // 4
+    # the whole-layer fallback of backends without pointer copies gives the same tensors
+    nb = NullBackend()
+    d2 = nb.alloc_device(len(buf))
+    from moe_mi355x.types import HostBuffer
+    nb.copy_h2d_async(d2, HostBuffer(view=memoryview(buf)), None)
+    got2 = read_layer_tensors(layer, d2, nb, None)
+    assert all(np.array_equal(got2[n], got[n]) for n in got)
+
+
+def test_merge_ranges():
+    from moe_mi355x.executors import _merge_ranges
+
+    assert _merge_ranges([(10, 20), (0, 5), (21, 30), (100, 110)], gap=2) == [
+        (0, 5), (10, 30), (100, 110)]
+    assert _merge_ranges([(0, 5), (3, 4)], gap=0) == [(0, 5)]
+
+
+def test_host_attention_hook_runs_before_the_moe_step():
+    from moe_mi355x.executors import DeviceBuffer, host_attention
+
+    t, buf, layer = _attention_layer()
+    seen = {}
+
+    def attn(x, tensors):
+        seen.update(tensors)
+        return x + tensors["input_layernorm.weight"]
+
+    hook = host_attention(attn)
+    be = _PtrBackend(buf)
+    x = np.zeros((3, 32), np.float32)
+    y = hook(x, layer, DeviceBuffer(handle=0, nbytes=len(buf), backend="null"), be, None)
+    assert np.array_equal(y, np.broadcast_to(t["input_layernorm.weight"], (3, 32)))
+    assert "self_attn.o_proj.weight" in seen and not any(n.startswith("mlp.") for n in seen)

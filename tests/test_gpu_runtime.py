@@ -145,3 +145,41 @@ def test_expert_granular_chain_matches_oracle(mi355x, arch, wdt, lookahead):
     if exact:  # no near-tie routing: the copied bytes are exactly core + the oracle's experts
         assert metrics.transferred_bytes == used
     assert all(lm.h2d_gpu_ms > 0 for lm in metrics.layer_metrics)
+
+
+def test_host_attention_layers_match_oracle(mi355x):
+    """Full layers (attention + MoE tensors in one packed buffer): the attention runs on the
+    host over only the copied-back attention tensors, the MoE step on the device."""
+    from moe_mi355x.executors import host_attention
+
+    say("[gpu] host attention + device MoE chain")
+    shape = syn.MoeShape(syn.GLM, 128, 8, 2, 64, 64, 2.5, 1e-5)
+    rng = np.random.default_rng(77)
+    tensors, layers, blobs = [], [], {}
+    for i in range(2):
+        t = syn.make_tensors(shape, 70 + i, weight_dtype=np.float16)
+        t["input_layernorm.weight"] = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+        t["self_attn.o_proj.weight"] = (0.05 * rng.standard_normal((128, 128))).astype(np.float16)
+        raw, meta = pack_tensors(t)
+        layers.append(make_layer_spec(i, meta, len(raw)))
+        blobs[i] = raw
+        tensors.append(t)
+
+    def attn(x, t):  # a stand-in attention: x + o_proj(rms_norm(x))
+        h = x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + 1e-5) * t["input_layernorm.weight"]
+        return x + h @ t["self_attn.o_proj.weight"].astype(np.float32).T
+
+    ex = GLM4MoeExecutor(shape.config(), attention=host_attention(attn))
+    x = syn.make_inputs(71, 5, shape.hidden)
+    rt = OffloadRuntime(layers, mi355x, InMemoryStorage(blobs), LookaheadScheduler(1), ex)
+    try:
+        out, _ = rt.run_inference([0, 1], x)
+    finally:
+        rt.close()
+        ex.close()
+    ref = x
+    for t in tensors:
+        ref = orc.moe_block(attn(ref, t), t, spec_for(shape))["out"]
+    err = normwise_err(out, ref)
+    say(f"    normwise err {err:.2e}")
+    assert err <= 5e-3
