@@ -99,3 +99,79 @@ def make_tensors(shape: MoeShape, seed: int, weight_dtype=np.float32, param_dtyp
 
 def make_inputs(seed: int, tokens: int, hidden: int) -> np.ndarray:
     return gen.normal(seed, stream_of("x"), (tokens, hidden), std=1.0)
+
+
+# ---- Qwen3-Next linear attention (Gated DeltaNet) layers -----------------------------
+
+@dataclass(frozen=True)
+class LinearAttnShape:
+    """A linear-attention block: ``n_heads`` key heads = value heads (the reference
+    reshapes q and k with the value-head count, qwen3_next.py:75-77, 255-258)."""
+
+    hidden: int
+    n_heads: int
+    head_dim_k: int
+    head_dim_v: int
+    conv_kernel: int = 4
+    eps: float = 1e-6
+
+    @property
+    def qkvz_rows(self) -> int:
+        return 2 * self.n_heads * (self.head_dim_k + self.head_dim_v)
+
+    @property
+    def conv_channels(self) -> int:
+        return self.n_heads * (2 * self.head_dim_k + self.head_dim_v)
+
+    @property
+    def ba_rows(self) -> int:
+        return self.n_heads * (self.head_dim_k + 1)
+
+    def config(self) -> dict:
+        """The Qwen3-Next config keys of qwen3_next.py:106-125 for this block."""
+        return {"architectures": ["Qwen3NextForCausalLM"], "hidden_size": self.hidden,
+                "rms_norm_eps": self.eps, "num_attention_heads": 1,
+                "linear_num_key_heads": self.n_heads, "linear_key_head_dim": self.head_dim_k,
+                "linear_num_value_heads": self.n_heads,
+                "linear_value_head_dim": self.head_dim_v,
+                "linear_conv_kernel_dim": self.conv_kernel}
+
+
+# Qwen3-Next-sized block with as many key heads as value heads (32 x 128).
+QWEN3_NEXT_LINEAR = LinearAttnShape(2048, 32, 128, 128, 4, 1e-6)
+
+
+def linear_attn_specs(shape: LinearAttnShape) -> list[tuple[str, tuple[int, ...], str, float, float]]:
+    """(name, shape, kind, std, mean) of every tensor of the block.  Projections
+    ~ N(0, 0.02); conv taps ~ N(0, 0.5) (so the conv keeps unit-scale signals);
+    A_log ~ N(0, 0.5) and dt_bias ~ N(-4, 0.5), which give per-token decays near 0.95
+    (memory of tens of tokens); norm weights 1 (+ noise)."""
+    H, n, dk, dv, K = (shape.hidden, shape.n_heads, shape.head_dim_k, shape.head_dim_v,
+                       shape.conv_kernel)
+    return [("input_layernorm.weight", (H,), "norm", 0.0, 0.0),
+            ("linear_attn.in_proj_qkvz.weight", (shape.qkvz_rows, H), "weight", 0.02, 0.0),
+            ("linear_attn.in_proj_ba.weight", (shape.ba_rows, H), "weight", 0.02, 0.0),
+            ("linear_attn.conv1d.weight", (shape.conv_channels, 1, K), "param", 0.5, 0.0),
+            ("linear_attn.A_log", (n,), "param", 0.5, 0.0),
+            ("linear_attn.dt_bias", (n,), "param", 0.5, -4.0),
+            ("linear_attn.norm.weight", (n * dv,), "norm", 0.0, 0.0),
+            ("linear_attn.out_proj.weight", (H, n * dv), "weight", 0.02, 0.0)]
+
+
+def make_linear_attn_tensors(shape: LinearAttnShape, seed: int, weight_dtype=np.float32,
+                             param_dtype=np.float32, norm_noise: float = 0.0
+                             ) -> dict[str, np.ndarray]:
+    """All tensors of one linear-attention block: projections in ``weight_dtype``, conv
+    taps, A_log, dt_bias and norm weights in ``param_dtype``."""
+    out = {}
+    for name, shp, kind, std, mean in linear_attn_specs(shape):
+        if kind == "norm":
+            v = np.ones(shp, dtype=np.float32)
+            if norm_noise:
+                v = v + gen.normal(seed, stream_of(name), shp, std=norm_noise)
+        else:
+            v = gen.normal(seed, stream_of(name), shp, std=std)
+            if mean:
+                v = v + np.float32(mean)
+        out[name] = v.astype(weight_dtype if kind == "weight" else param_dtype)
+    return out

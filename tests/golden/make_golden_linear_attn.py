@@ -1,0 +1,61 @@
+"""Write golden vectors of the reference linear-attention block (build container only).
+
+The composed output of ``Qwen3NextExecutor._linear_attn_block``
+(offload_runtime/executors/qwen3_next.py:207-269) — the split offsets of the fused
+projections, which half of ``in_proj_ba`` gates what, the conv/SiLU order, the gated
+output norm — is pinned by no test of the reference (its integration test checks shapes
+and finiteness, tests/test_integration_inference.py:509-535), so this script runs that
+method from a local checkout on seeded synthetic inputs and stores the outputs.  Inputs
+are regenerated from (shape, seed) by ``moe_mi355x.synthetic`` and checked against the
+stored SHA-256 digests.
+
+Usage:  python tests/golden/make_golden_linear_attn.py /path/to/disk-mem-off
+"""
+from __future__ import annotations
+
+import dataclasses
+import json
+import sys
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+sys.path.insert(0, str(HERE.parents[1] / "disk-mem-off_amd"))
+
+from moe_mi355x import synthetic as syn  # noqa: E402
+from make_golden import digest  # noqa: E402
+
+CASES = [
+    # name, shape, seed, tokens, dtype, norm noise
+    ("la_tiny_f32", syn.LinearAttnShape(8, 2, 4, 4, 4, 1e-6), 999, 3, "float32", 0.0),
+    ("la_small_f32", syn.LinearAttnShape(64, 4, 16, 8, 4, 1e-6), 31, 37, "float32", 0.1),
+    ("la_mid_f32", syn.LinearAttnShape(256, 8, 32, 32, 4, 1e-6), 32, 70, "float32", 0.1),
+    ("la_mid_f16", syn.LinearAttnShape(256, 8, 32, 32, 4, 1e-6), 33, 20, "float16", 0.0),
+    ("la_k2_f32", syn.LinearAttnShape(64, 2, 8, 16, 2, 1e-5), 34, 5, "float32", 0.0),
+]
+
+
+def main(ref_root: str) -> None:
+    sys.path.insert(0, ref_root)
+    from offload_runtime.executors.qwen3_next import Qwen3NextExecutor
+
+    index = {}
+    for name, shape, seed, tokens, dtype, noise in CASES:
+        dt = np.dtype(dtype)
+        t = syn.make_linear_attn_tensors(shape, seed, weight_dtype=dt, param_dtype=dt,
+                                         norm_noise=noise)
+        x = syn.make_inputs(seed, tokens, shape.hidden)
+        ex = Qwen3NextExecutor(shape.config())
+        out = np.asarray(ex._linear_attn_block(x, t), dtype=np.float32)
+        np.savez(HERE / f"{name}.npz", out=out)
+        index[name] = {"shape": dataclasses.asdict(shape), "seed": seed, "tokens": tokens,
+                       "dtype": dtype, "norm_noise": noise, "x_sha256": digest({"x": x}),
+                       "tensors_sha256": digest(t)}
+        print(f"{name}: out[0,:4]={out[0, :4]}")
+    (HERE / "linear_attn_index.json").write_text(
+        json.dumps(index, indent=1, sort_keys=True) + "\n")
+
+
+if __name__ == "__main__":
+    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
