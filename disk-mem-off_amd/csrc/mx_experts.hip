@@ -723,19 +723,18 @@ static int dispatch_expert(int wdt, int mt, const ExpertParams& p, int mt_max, i
 }
 
 // Direct-load kernel for m_blk 16/32/64; LDS-staged kernel for m_blk 128 (fp16/int8).
+// mt_max bounds the m-tile list (the kernels read the actual count from p.n_mtiles).
 template <bool GU>
-static int launch_grouped(const MxMoeDesc* d, const ExpertParams& p, int tokens, int m_blk,
-                          int nmax, hipStream_t s) {
-  const int has_shared = d->shared_inter > 0;
-  const int mt_max = mx_max_mtiles(tokens, d->top_k, d->n_experts, has_shared, m_blk);
+static int launch_grouped_mt(int wdt, const ExpertParams& p, int mt_max, int m_blk, int nmax,
+                             hipStream_t s) {
   if (m_blk == 128) {
-    if (d->weight_dtype == MX_DT_F32) return MX_ERR_INVALID;
+    if (wdt == MX_DT_F32) return MX_ERR_INVALID;
     const int cols = 4 * 16 * (GU ? 2 : 4);
     const int nblk = mx_ceil_div(nmax, cols);
     const long blocks = ((long)mt_max * nblk + 7) / 8 * 8;
     if (blocks > (1l << 31) - 1) return MX_ERR_UNSUPPORTED;
     mx_clear_error();
-    if (d->weight_dtype == MX_DT_F16)
+    if (wdt == MX_DT_F16)
       hipLaunchKernelGGL((k_expert_lds<MX_DT_F16, GU>), dim3((unsigned)blocks), dim3(256), 0, s,
                          p, mt_max, nblk);
     else
@@ -744,7 +743,60 @@ static int launch_grouped(const MxMoeDesc* d, const ExpertParams& p, int tokens,
     return mx_launch_status();
   }
   if (m_blk != 16 && m_blk != 32 && m_blk != 64) return MX_ERR_INVALID;
-  return dispatch_expert<GU>(d->weight_dtype, m_blk / 16, p, mt_max, nmax, s);
+  return dispatch_expert<GU>(wdt, m_blk / 16, p, mt_max, nmax, s);
+}
+
+template <bool GU>
+static int launch_grouped(const MxMoeDesc* d, const ExpertParams& p, int tokens, int m_blk,
+                          int nmax, hipStream_t s) {
+  const int has_shared = d->shared_inter > 0;
+  const int mt_max = mx_max_mtiles(tokens, d->top_k, d->n_experts, has_shared, m_blk);
+  return launch_grouped_mt<GU>(d->weight_dtype, p, mt_max, m_blk, nmax, s);
+}
+
+// Dense y[T, N] = a[T, K] W[N, K]^T (x the fp16 row scale of int8 weights) on the down-
+// projection kernels: one group of T rows, `entry` an expert table entry whose `down`
+// (and `down_scale`) is W, `tab` the single-group tables (g_* = {entry 0, row 0, T},
+// mt_group = 0, mt_row0 = i * m_blk, n_mtiles = ceil(T / m_blk)) and `ones` [T] of 1.0.
+int mx_dense_linear(int wdt, int tiled, const MxExpertPtrs* entry, const MxDenseTables& tab,
+                    int T, int N, int K, const void* a, float* y, hipStream_t s) {
+  int epl;
+  switch (wdt) {
+    case MX_DT_F32: epl = 4; break;
+    case MX_DT_F16: epl = 8; break;
+    case MX_DT_I8: epl = 16; break;
+    default: return MX_ERR_INVALID;
+  }
+  if (T <= 0 || N <= 0 || K <= 0 || !entry || !a || !y) return MX_ERR_INVALID;
+  if (K % epl) return MX_ERR_UNSUPPORTED;
+  if (tiled && (N % 16 || K % (4 * epl))) return MX_ERR_UNSUPPORTED;
+  const int esz = wdt == MX_DT_F32 ? 4 : (wdt == MX_DT_F16 ? 2 : 1);
+  const int aesz = wdt == MX_DT_F32 ? 4 : 2;
+  if ((long)N * K * esz >= (1l << 31) || (long)T * K * aesz >= (1l << 31))
+    return MX_ERR_UNSUPPORTED;
+  if (!mx_aligned16(a) || !mx_aligned16(y)) return MX_ERR_ALIGNMENT;
+  ExpertParams p;
+  p.experts = entry;
+  p.g_expert = tab.g_expert;
+  p.g_start = tab.g_start;
+  p.g_count = tab.g_count;
+  p.mt_group = tab.mt_group;
+  p.mt_row0 = tab.mt_row0;
+  p.n_mtiles = tab.n_mtiles;
+  p.sorted_tok = nullptr;
+  p.a = a;
+  p.a_bytes = (uint32_t)((long)T * K * aesz);
+  p.lda = K;
+  p.out = y;
+  p.ldo = N;
+  p.sorted_w = tab.ones;
+  p.E = 1;
+  p.N_r = N;
+  p.K_r = K;
+  p.N_s = N;
+  p.K_s = K;
+  p.tiled = tiled;
+  return launch_grouped_mt<false>(wdt, p, mx_ceil_div(T, tab.m_blk), tab.m_blk, N, s);
 }
 
 extern "C" int mx_expert_gate_up(const MxMoeDesc* desc, const MxExpertPtrs* experts,

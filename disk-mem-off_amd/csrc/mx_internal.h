@@ -28,3 +28,20 @@ int mx_router_decode_launch(const MxMoeDesc* d, const MxMoeWeights* w, int T, co
                             int* sorted_tok, float* sorted_w, int* pair_pos, int* g_expert,
                             int* g_start, int* g_count, int* n_groups, int* mt_group,
                             int* mt_row0, int* n_mtiles, hipStream_t s);
+
+// Single-group tables for dense products on the grouped-GEMM kernels (device pointers).
+struct MxDenseTables {
+  const int* g_expert;
+  const int* g_start;
+  const int* g_count;
+  const int* mt_group;
+  const int* mt_row0;
+  const int* n_mtiles;
+  const float* ones;
+  int m_blk;
+};
+
+// y[T, N] = a[T, K] W[N, K]^T through the down-projection kernels; W (and its int8 row
+// scales) is entry->down (->down_scale).  a is fp32 for MX_DT_F32 weights, else fp16.
+int mx_dense_linear(int wdt, int tiled, const MxExpertPtrs* entry, const MxDenseTables& tab,
+                    int T, int N, int K, const void* a, float* y, hipStream_t s);

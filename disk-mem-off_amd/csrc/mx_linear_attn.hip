@@ -1,0 +1,529 @@
+// Qwen3-Next linear-attention (Gated DeltaNet) block on the device:
+//   rmsnorm -> qkvz projection -> ba projection -> causal conv + SiLU + gates -> scan
+//   -> gated output norm -> out projection -> residual,
+// i.e. Qwen3NextExecutor._linear_attn_block (offload_runtime/executors/qwen3_next.py:207-269)
+// with _softplus (:27-28), _causal_conv1d (:35-53) and _gated_delta_rule_recurrence
+// (:56-95).  The three projections run on the grouped-GEMM kernels of the MoE experts as
+// single-group products (HBM-bound decode kernel for short inputs, LDS-staged MFMA kernel
+// for long ones).  Everything runs on the caller's stream out of the caller's workspace.
+#include <math.h>
+
+#include "mx_common.h"
+#include "mx_internal.h"
+
+namespace {
+
+struct LaDims {
+  int H, n, dk, dv, K;
+  int qd, vd;  // n dk, n dv
+  int C;       // conv channels: 2 qd + vd
+  int W1, W2;  // row widths of qkvz (2 qd + 2 vd) and ba (qd + n)
+};
+
+LaDims dims_of(const MxLinearAttnDesc* d) {
+  LaDims m;
+  m.H = d->hidden;
+  m.n = d->n_heads;
+  m.dk = d->head_dim_k;
+  m.dv = d->head_dim_v;
+  m.K = d->conv_kernel;
+  m.qd = m.n * m.dk;
+  m.vd = m.n * m.dv;
+  m.C = 2 * m.qd + m.vd;
+  m.W1 = 2 * m.qd + 2 * m.vd;
+  m.W2 = m.qd + m.n;
+  return m;
+}
+
+int check_desc(const MxLinearAttnDesc* d) {
+  if (!d) return MX_ERR_INVALID;
+  if (d->hidden <= 0 || d->n_heads <= 0 || d->head_dim_k <= 0 || d->head_dim_v <= 0 ||
+      d->conv_kernel <= 0)
+    return MX_ERR_INVALID;
+  if (d->param_dtype != MX_DT_F32 && d->param_dtype != MX_DT_F16) return MX_ERR_INVALID;
+  if (d->weight_dtype != MX_DT_F32 && d->weight_dtype != MX_DT_F16 && d->weight_dtype != MX_DT_I8)
+    return MX_ERR_INVALID;
+  if (d->conv_kernel > 16) return MX_ERR_UNSUPPORTED;
+  const int dk = d->head_dim_k;
+  if ((dk & (dk - 1)) || dk < 4 || dk > 512) return MX_ERR_UNSUPPORTED;
+  const long w1 = 2l * d->n_heads * (d->head_dim_k + d->head_dim_v);
+  if (w1 * d->hidden >= (1l << 31) || (long)d->hidden * d->n_heads * d->head_dim_v >= (1l << 31))
+    return MX_ERR_UNSUPPORTED;
+  return MX_OK;
+}
+
+struct Carve {
+  char* base;
+  size_t off = 0;
+  void* take(size_t n) {
+    off = mx_align_up(off, 256);
+    void* p = base ? base + off : nullptr;
+    off += n;
+    return p;
+  }
+};
+
+struct LaWork {
+  MxLinearAttnViews v;
+  MxExpertPtrs* entries;  // [3]: qkvz, ba, out
+  int* tabs;              // g_expert, g_start, g_count, n_mtiles (4 ints)
+  int* mt_group;
+  int* mt_row0;
+  float* ones;
+  int m_blk, n_mt;
+};
+
+int layout(const MxLinearAttnDesc* d, int T, void* ws, LaWork* w, size_t* total) {
+  MX_TRY(check_desc(d));
+  if (T < 0) return MX_ERR_INVALID;
+  const size_t Tn = T > 0 ? T : 1;
+  const LaDims m = dims_of(d);
+  const bool f32 = d->weight_dtype == MX_DT_F32;
+  const int m_blk = mx_m_blk_for((int)Tn, d->weight_dtype);
+  const int n_mt = mx_ceil_div((int)Tn, m_blk);
+  Carve c{(char*)ws};
+  LaWork t;
+  t.v.h32 = (float*)c.take(Tn * m.H * 4);
+  t.v.h16 = f32 ? nullptr : c.take(Tn * m.H * 2);
+  t.v.qkvz = (float*)c.take(Tn * m.W1 * 4);
+  t.v.ba = (float*)c.take(Tn * m.W2 * 4);
+  t.v.q = (float*)c.take(Tn * m.qd * 4);
+  t.v.kb = (float*)c.take(Tn * m.qd * 4);
+  t.v.v = (float*)c.take(Tn * m.vd * 4);
+  t.v.decay = (float*)c.take(Tn * m.n * 4);
+  t.v.o = (float*)c.take(Tn * m.vd * 4);
+  t.v.act = c.take(Tn * m.vd * (f32 ? 4 : 2));
+  t.v.y = (float*)c.take(Tn * m.H * 4);
+  t.entries = (MxExpertPtrs*)c.take(3 * sizeof(MxExpertPtrs));
+  t.tabs = (int*)c.take(4 * 4);
+  t.mt_group = (int*)c.take((size_t)n_mt * 4);
+  t.mt_row0 = (int*)c.take((size_t)n_mt * 4);
+  t.ones = (float*)c.take(Tn * 4);
+  t.m_blk = m_blk;
+  t.n_mt = n_mt;
+  if (w) *w = t;
+  if (total) *total = mx_align_up(c.off, 256);
+  return MX_OK;
+}
+
+// ------------------------------------------------------------------------------------
+// Kernels.
+// ------------------------------------------------------------------------------------
+
+// Expert-table entries of the three projections and the single-group m-tile tables.
+__global__ __launch_bounds__(256) void k_la_setup(int T, int m_blk, int n_mt,
+                                                  MxExpertPtrs* __restrict__ entries,
+                                                  MxExpertPtrs e0, MxExpertPtrs e1,
+                                                  MxExpertPtrs e2, int* __restrict__ tabs,
+                                                  int* __restrict__ mt_group,
+                                                  int* __restrict__ mt_row0,
+                                                  float* __restrict__ ones) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i == 0) {
+    entries[0] = e0;
+    entries[1] = e1;
+    entries[2] = e2;
+    tabs[0] = 0;  // g_expert
+    tabs[1] = 0;  // g_start
+    tabs[2] = T;  // g_count
+    tabs[3] = n_mt;
+  }
+  if (i < n_mt) {
+    mt_group[i] = 0;
+    mt_row0[i] = i * m_blk;
+  }
+  if (i < T) ones[i] = 1.f;
+}
+
+// Causal depthwise conv + SiLU on the q/k/v channels, beta * k, and the per-head decay.
+// Grid (ceil((C + n) / 256), T).  Thread c < C: out = sum_{j=0}^{K-1} x[t - j, c] w[c, j]
+// summed in j order from 0 (qwen3_next.py:49-52), then silu (:238); k channels times
+// sigmoid(b) (:244, :89).  Thread C + h: g = -exp(A_log) softplus(a + dt_bias) (:249),
+// decay = exp(g) (:84).  Products are rounded before each sum, as NumPy does.
+__global__ __launch_bounds__(256) void k_la_prep(const float* __restrict__ qkvz,
+                                                 const float* __restrict__ ba,
+                                                 const void* __restrict__ conv_w,
+                                                 const void* __restrict__ a_log,
+                                                 const void* __restrict__ dt_bias, int pdt,
+                                                 LaDims m, int T, float* __restrict__ q,
+                                                 float* __restrict__ kb, float* __restrict__ v,
+                                                 float* __restrict__ decay) {
+#pragma clang fp contract(off)
+  const int t = blockIdx.y;
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c < m.C) {
+    float acc = 0.f;
+    for (int j = 0; j < m.K && j <= t; ++j)
+      acc += qkvz[(size_t)(t - j) * m.W1 + c] * mx_load_param(conv_w, pdt, c * m.K + j);
+    const float s = mx_silu(acc);
+    if (c < m.qd) {
+      q[(size_t)t * m.qd + c] = s;
+    } else if (c < 2 * m.qd) {
+      const int ck = c - m.qd;
+      kb[(size_t)t * m.qd + ck] = mx_sigmoid(ba[(size_t)t * m.W2 + ck]) * s;
+    } else {
+      v[(size_t)t * m.vd + (c - 2 * m.qd)] = s;
+    }
+  } else if (c < m.C + m.n) {
+    const int h = c - m.C;
+    float ea = expf(mx_load_param(a_log, pdt, h));
+    if (pdt == MX_DT_F16) ea = (float)(half_t)ea;  // np.exp of an fp16 array stays fp16
+    const float a = ba[(size_t)t * m.W2 + m.qd + h] + mx_load_param(dt_bias, pdt, h);
+    const float sp = a > 20.f ? a : log1pf(expf(a));
+    decay[(size_t)t * m.n + h] = expf(-ea * sp);
+  }
+}
+
+// The recurrence.  Lane (row group rr, column group cg) of a wave holds CPL consecutive
+// state columns c0 = cg * CPL of one state row (head h, value index i):
+//   S[i, c] = S[i, c] * decay_t + v_t[i] * kb_t[c];   o_t[i] = sum_c S[i, c] q_t[c]
+// with the dot product finished across the L = dk / CPL lanes of the row (DPP inside a
+// 16-lane row, lane shuffles beyond).  A block of 4 waves holds RB = 4 * 64 / L rows of
+// one head; per chunk of TC tokens it stages that head's q, kb, its rows of v and the
+// decays in LDS (double-buffered, the next chunk's global loads in flight while the
+// current chunk runs), so every state element reads q and kb from LDS, not from L1.
+template <int CPL, int L>
+struct ScanShape {
+  static constexpr int DK = CPL * L;
+  static constexpr int RW = 64 / L;   // rows per wave
+  static constexpr int RB = 4 * RW;   // rows per block
+  static constexpr int TC = DK >= 512 ? 4 : (DK >= 256 ? 8 : 16);  // tokens per chunk
+  static constexpr int NQ = TC * DK;  // floats of q (and of kb) per chunk
+  static constexpr int NQ4 = NQ / 4;  // float4 pieces of q (and of kb) per chunk
+  static constexpr int QP = (NQ4 + 255) / 256;  // q (and kb) pieces per thread
+  static constexpr int NV = TC * RB;  // v values per chunk
+  static constexpr int VP = (NV + 255) / 256;
+  static constexpr int BUF = 2 * NQ + NV + TC;  // floats per LDS buffer
+  static_assert(DK % 4 == 0, "key head size must be a multiple of 4");
+};
+
+template <int L>
+__device__ __forceinline__ float la_row_sum(float v) {
+  if constexpr (L >= 2) v += mx_dpp<MX_DPP_XOR1>(v);
+  if constexpr (L >= 4) v += mx_dpp<MX_DPP_XOR2>(v);
+  if constexpr (L >= 8) v += mx_dpp<MX_DPP_HALF_MIRROR>(v);
+  if constexpr (L >= 16) v += mx_dpp<MX_DPP_MIRROR>(v);
+  if constexpr (L >= 32) v += __shfl_xor(v, 16);
+  if constexpr (L >= 64) v += __shfl_xor(v, 32);
+  return v;
+}
+
+template <int CPL, int L>
+__global__ __launch_bounds__(256) void k_la_scan(const float* __restrict__ q,
+                                                 const float* __restrict__ kb,
+                                                 const float* __restrict__ v,
+                                                 const float* __restrict__ decay, int T, int n,
+                                                 int dv, int bph, float* __restrict__ o) {
+  using Sh = ScanShape<CPL, L>;
+  constexpr int DK = Sh::DK, RB = Sh::RB, TC = Sh::TC, NQ = Sh::NQ, NQ4 = Sh::NQ4;
+  constexpr int QP = Sh::QP, NV = Sh::NV, VP = Sh::VP;
+  __shared__ __align__(16) float lds[2][Sh::BUF];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = blockIdx.x / bph;
+  const int rb0 = (blockIdx.x - h * bph) * RB;  // first value row of this block in head h
+  const int rr = lane / L, cg = lane % L;
+  const int rloc = wave * Sh::RW + rr;  // row within the block
+  const int row = rb0 + rloc;
+  const bool rvalid = row < dv;
+  const int c0 = cg * CPL;
+  const int qd = n * DK, vd = n * dv;
+
+  // Chunk staging (all offsets in elements; T * n * max(dk, dv) < 2^31 is checked by the
+  // launcher).  q and kb: float4 piece i = (token i / (DK / 4), columns 4 (i % (DK / 4))..)
+  // of head h; v: value i = (token i / RB, row rb0 + i % RB); decay: one per token.
+  struct Stage {
+    float4 qv[QP], kv[QP];
+    float vv[VP];
+    float dd;
+  };
+  auto load_chunk = [&](int t0, Stage& r) {
+#pragma unroll
+    for (int p = 0; p < QP; ++p) {
+      const int i = tid + 256 * p;
+      const int t = t0 + i / (DK / 4);
+      const bool ok = i < NQ4 && t < T;
+      const int off = t * qd + h * DK + 4 * (i % (DK / 4));
+      r.qv[p] = ok ? *(const float4*)(q + off) : make_float4(0.f, 0.f, 0.f, 0.f);
+      r.kv[p] = ok ? *(const float4*)(kb + off) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int p = 0; p < VP; ++p) {
+      const int i = tid + 256 * p;
+      const int t = t0 + i / RB, r2 = rb0 + i % RB;
+      r.vv[p] = (i < NV && t < T && r2 < dv) ? v[t * vd + h * dv + r2] : 0.f;
+    }
+    r.dd = (tid < TC && t0 + tid < T) ? decay[(t0 + tid) * n + h] : 0.f;
+  };
+  auto store_chunk = [&](int buf, const Stage& r) {
+    float* b = lds[buf];
+#pragma unroll
+    for (int p = 0; p < QP; ++p) {
+      const int i = tid + 256 * p;
+      if (i < NQ4) {
+        ((float4*)b)[i] = r.qv[p];
+        ((float4*)(b + NQ))[i] = r.kv[p];
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < VP; ++p) {
+      const int i = tid + 256 * p;
+      if (i < NV) b[2 * NQ + i] = r.vv[p];
+    }
+    if (tid < TC) b[2 * NQ + NV + tid] = r.dd;
+  };
+
+  float S[CPL];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) S[c] = 0.f;
+
+  Stage stage;
+  load_chunk(0, stage);
+  store_chunk(0, stage);
+  __syncthreads();
+  const int nchunk = (T + TC - 1) / TC;
+  for (int ch = 0; ch < nchunk; ++ch) {
+    const int t0 = ch * TC;
+    const int buf = ch & 1;
+    const bool more = ch + 1 < nchunk;
+    if (more) load_chunk(t0 + TC, stage);
+    const float* sq = lds[buf];
+    const float* sk = sq + NQ;
+    const float* sv = sk + NQ;
+    const float* sd = sv + NV;
+    const int nt = min(TC, T - t0);
+    for (int tt = 0; tt < nt; ++tt) {
+      float qv[CPL], kv[CPL];
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        qv[c] = sq[tt * DK + c0 + c];
+        kv[c] = sk[tt * DK + c0 + c];
+      }
+      const float vi = sv[tt * RB + rloc];
+      const float dd = sd[tt];
+      float part = 0.f;
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        S[c] = S[c] * dd + vi * kv[c];
+        part += S[c] * qv[c];
+      }
+      const float ov = la_row_sum<L>(part);
+      if (cg == 0 && rvalid) o[(t0 + tt) * vd + h * dv + row] = ov;
+    }
+    if (more) {
+      // The other buffer was last read in chunk ch - 1, before every wave passed the
+      // barrier that ended that chunk.
+      store_chunk(buf ^ 1, stage);
+      __syncthreads();
+    }
+  }
+}
+
+template <int CPL, int L>
+int launch_scan(const float* q, const float* kb, const float* v, const float* decay, int T,
+                int n, int dv, float* o, hipStream_t s) {
+  using Sh = ScanShape<CPL, L>;
+  const int bph = mx_ceil_div(dv, Sh::RB);
+  const long blocks = (long)n * bph;
+  const long dmax = Sh::DK > dv ? Sh::DK : dv;
+  if (blocks > (1l << 31) - 1 || (long)T * n * dmax >= (1l << 31)) return MX_ERR_UNSUPPORTED;
+  if (!mx_aligned16(q) || !mx_aligned16(kb)) return MX_ERR_ALIGNMENT;
+  mx_clear_error();
+  hipLaunchKernelGGL((k_la_scan<CPL, L>), dim3((unsigned)blocks), dim3(256), 0, s, q, kb, v,
+                     decay, T, n, dv, bph, o);
+  return mx_launch_status();
+}
+
+int scan_launch(const float* q, const float* kb, const float* v, const float* decay, int T,
+                int n, int dk, int dv, float* o, hipStream_t s) {
+  switch (dk) {
+    case 4: return launch_scan<4, 1>(q, kb, v, decay, T, n, dv, o, s);
+    case 8: return launch_scan<8, 1>(q, kb, v, decay, T, n, dv, o, s);
+    case 16: return launch_scan<8, 2>(q, kb, v, decay, T, n, dv, o, s);
+    case 32: return launch_scan<8, 4>(q, kb, v, decay, T, n, dv, o, s);
+    case 64: return launch_scan<8, 8>(q, kb, v, decay, T, n, dv, o, s);
+    case 128: return launch_scan<8, 16>(q, kb, v, decay, T, n, dv, o, s);
+    case 256: return launch_scan<8, 32>(q, kb, v, decay, T, n, dv, o, s);
+    case 512: return launch_scan<8, 64>(q, kb, v, decay, T, n, dv, o, s);
+    default: return MX_ERR_UNSUPPORTED;
+  }
+}
+
+// Gated output norm: act = (w * (o / rms(o))) * silu(z) per token row (qwen3_next.py:
+// 264-266, rms_norm of _common.py:73-75), written as fp16 (fp32 for fp32 weights).
+__global__ __launch_bounds__(256) void k_la_gated_norm(const float* __restrict__ o,
+                                                       const float* __restrict__ qkvz,
+                                                       const void* __restrict__ norm_w,
+                                                       int pdt, float eps, LaDims m,
+                                                       float* __restrict__ act32,
+                                                       half_t* __restrict__ act16) {
+#pragma clang fp contract(off)
+  const int t = blockIdx.x;
+  const float* orow = o + (size_t)t * m.vd;
+  const float* z = qkvz + (size_t)t * m.W1 + 2 * m.qd + m.vd;
+  float ss = 0.f;
+  for (int c = threadIdx.x; c < m.vd; c += 256) ss += orow[c] * orow[c];
+  __shared__ float red[4];
+  ss = mx_wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+  const float rms = sqrtf(tot / (float)m.vd + eps);
+  for (int c = threadIdx.x; c < m.vd; c += 256) {
+    const float y = mx_load_param(norm_w, pdt, c) * (orow[c] / rms);
+    const float a = y * mx_silu(z[c]);
+    if (act16)
+      act16[(size_t)t * m.vd + c] = (half_t)a;
+    else
+      act32[(size_t)t * m.vd + c] = a;
+  }
+}
+
+__global__ __launch_bounds__(256) void k_la_residual(const float* __restrict__ x,
+                                                     const float* __restrict__ y, long n4,
+                                                     float* __restrict__ out) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i < n4) {
+    const float4 a = ((const float4*)x)[i], b = ((const float4*)y)[i];
+    ((float4*)out)[i] = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+  }
+}
+
+int check_weights(const MxLinearAttnDesc* d, const MxLinearAttnWeights* w) {
+  if (!w || !w->norm_w || !w->qkvz_w || !w->ba_w || !w->conv_w || !w->a_log || !w->dt_bias ||
+      !w->out_norm_w || !w->out_w)
+    return MX_ERR_INVALID;
+  if (d->weight_dtype == MX_DT_I8 && (!w->qkvz_scale || !w->ba_scale || !w->out_scale))
+    return MX_ERR_INVALID;
+  if (!mx_aligned16(w->qkvz_w) || !mx_aligned16(w->ba_w) || !mx_aligned16(w->out_w))
+    return MX_ERR_ALIGNMENT;
+  return MX_OK;
+}
+
+int run_stage(int st, const MxLinearAttnDesc* d, const MxLinearAttnWeights* w, const float* x,
+              float* out, int T, const LaWork& k, hipStream_t s) {
+  const LaDims m = dims_of(d);
+  const int wdt = d->weight_dtype;
+  const bool f32 = wdt == MX_DT_F32;
+  MxDenseTables tab{k.tabs + 0, k.tabs + 1, k.tabs + 2, k.mt_group, k.mt_row0, k.tabs + 3,
+                    k.ones, k.m_blk};
+  const void* h = f32 ? (const void*)k.v.h32 : k.v.h16;
+  switch (st) {
+    case 0: {
+      MxExpertPtrs e[3] = {};
+      e[0].down = w->qkvz_w;
+      e[0].down_scale = w->qkvz_scale;
+      e[1].down = w->ba_w;
+      e[1].down_scale = w->ba_scale;
+      e[2].down = w->out_w;
+      e[2].down_scale = w->out_scale;
+      const int nth = T > k.n_mt ? T : k.n_mt;
+      mx_clear_error();
+      hipLaunchKernelGGL(k_la_setup, dim3(mx_ceil_div(nth, 256)), dim3(256), 0, s, T, k.m_blk,
+                         k.n_mt, k.entries, e[0], e[1], e[2], k.tabs, k.mt_group, k.mt_row0,
+                         k.ones);
+      MX_TRY(mx_launch_status());
+      return mx_rmsnorm_launch(x, w->norm_w, d->param_dtype, d->eps, T, m.H, k.v.h32, k.v.h16,
+                               s);
+    }
+    case 1:
+      return mx_dense_linear(wdt, 0, k.entries + 0, tab, T, m.W1, m.H, h, k.v.qkvz, s);
+    case 2:
+      return mx_dense_linear(wdt, 0, k.entries + 1, tab, T, m.W2, m.H, h, k.v.ba, s);
+    case 3:
+      mx_clear_error();
+      hipLaunchKernelGGL(k_la_prep, dim3(mx_ceil_div(m.C + m.n, 256), T), dim3(256), 0, s,
+                         k.v.qkvz, k.v.ba, w->conv_w, w->a_log, w->dt_bias, d->param_dtype, m,
+                         T, k.v.q, k.v.kb, k.v.v, k.v.decay);
+      return mx_launch_status();
+    case 4:
+      return scan_launch(k.v.q, k.v.kb, k.v.v, k.v.decay, T, m.n, m.dk, m.dv, k.v.o, s);
+    case 5:
+      mx_clear_error();
+      hipLaunchKernelGGL(k_la_gated_norm, dim3(T), dim3(256), 0, s, k.v.o, k.v.qkvz,
+                         w->out_norm_w, d->param_dtype, d->eps, m, (float*)k.v.act,
+                         f32 ? nullptr : (half_t*)k.v.act);
+      return mx_launch_status();
+    case 6:
+      return mx_dense_linear(wdt, 0, k.entries + 2, tab, T, m.H, m.vd, k.v.act, k.v.y, s);
+    case 7: {
+      const long n4 = (long)T * m.H / 4;
+      mx_clear_error();
+      hipLaunchKernelGGL(k_la_residual, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, x,
+                         k.v.y, n4, out);
+      return mx_launch_status();
+    }
+    default:
+      return MX_ERR_INVALID;
+  }
+}
+
+int forward(const MxLinearAttnDesc* d, const MxLinearAttnWeights* w, const float* x, float* out,
+            int T, void* ws, size_t ws_bytes, hipStream_t s, void* const* events) {
+  MX_TRY(check_desc(d));
+  MX_TRY(check_weights(d, w));
+  if (!x || !out || !ws || T < 0) return MX_ERR_INVALID;
+  if (d->hidden % 4) return MX_ERR_UNSUPPORTED;  // float4 residual
+  if (!mx_aligned16(x) || !mx_aligned16(out)) return MX_ERR_ALIGNMENT;
+  if (T == 0) return MX_OK;
+  LaWork k;
+  size_t need = 0;
+  MX_TRY(layout(d, T, ws, &k, &need));
+  if (ws_bytes < need) return MX_ERR_WORKSPACE;
+  for (int st = 0; st < MX_LA_N_STAGES; ++st) {
+    if (events) MX_TRY(mx_status(hipEventRecord((hipEvent_t)events[st], s)));
+    MX_TRY(run_stage(st, d, w, x, out, T, k, s));
+  }
+  if (events) MX_TRY(mx_status(hipEventRecord((hipEvent_t)events[MX_LA_N_STAGES], s)));
+  return MX_OK;
+}
+
+}  // namespace
+
+extern "C" int mx_linear_attn_workspace_size(const MxLinearAttnDesc* desc, int32_t tokens,
+                                             size_t* nbytes) {
+  if (!nbytes) return MX_ERR_INVALID;
+  return layout(desc, tokens, nullptr, nullptr, nbytes);
+}
+
+extern "C" int mx_linear_attn_views(const MxLinearAttnDesc* desc, int32_t tokens,
+                                    void* workspace, MxLinearAttnViews* views) {
+  if (!workspace || !views) return MX_ERR_INVALID;
+  LaWork k;
+  MX_TRY(layout(desc, tokens, workspace, &k, nullptr));
+  *views = k.v;
+  return MX_OK;
+}
+
+extern "C" int mx_linear_attn_forward(const MxLinearAttnDesc* desc,
+                                      const MxLinearAttnWeights* weights, const float* x,
+                                      float* out, int32_t tokens, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+  return forward(desc, weights, x, out, tokens, workspace, workspace_bytes, (hipStream_t)stream,
+                 nullptr);
+}
+
+extern "C" int mx_linear_attn_forward_profiled(const MxLinearAttnDesc* desc,
+                                               const MxLinearAttnWeights* weights,
+                                               const float* x, float* out, int32_t tokens,
+                                               void* workspace, size_t workspace_bytes,
+                                               void* stream, void* const* events,
+                                               int32_t n_events) {
+  if (!events || n_events != MX_LA_N_STAGES + 1) return MX_ERR_INVALID;
+  for (int i = 0; i < n_events; ++i)
+    if (!events[i]) return MX_ERR_INVALID;
+  return forward(desc, weights, x, out, tokens, workspace, workspace_bytes, (hipStream_t)stream,
+                 events);
+}
+
+extern "C" int mx_gated_delta_scan(const float* q, const float* kb, const float* v,
+                                   const float* decay, int32_t tokens, int32_t n_heads,
+                                   int32_t head_dim_k, int32_t head_dim_v, float* o,
+                                   void* stream) {
+  if (!q || !kb || !v || !decay || !o || tokens < 0 || n_heads <= 0 || head_dim_k <= 0 ||
+      head_dim_v <= 0)
+    return MX_ERR_INVALID;
+  if (tokens == 0) return MX_OK;
+  return scan_launch(q, kb, v, decay, tokens, n_heads, head_dim_k, head_dim_v, o,
+                     (hipStream_t)stream);
+}

@@ -76,6 +76,30 @@ class MxMoeViews(ctypes.Structure):
     ]
 
 
+MX_LA_N_STAGES = 8
+LA_STAGE_NAMES = ("rmsnorm", "qkvz_proj", "ba_proj", "conv_gates", "scan", "gated_norm",
+                  "out_proj", "residual")
+
+
+class MxLinearAttnDesc(ctypes.Structure):
+    _fields_ = [("hidden", c_int32), ("n_heads", c_int32), ("head_dim_k", c_int32),
+                ("head_dim_v", c_int32), ("conv_kernel", c_int32), ("weight_dtype", c_int32),
+                ("param_dtype", c_int32), ("eps", c_float)]
+
+
+class MxLinearAttnWeights(ctypes.Structure):
+    _fields_ = [("norm_w", c_void_p), ("qkvz_w", c_void_p), ("qkvz_scale", c_void_p),
+                ("ba_w", c_void_p), ("ba_scale", c_void_p), ("conv_w", c_void_p),
+                ("a_log", c_void_p), ("dt_bias", c_void_p), ("out_norm_w", c_void_p),
+                ("out_w", c_void_p), ("out_scale", c_void_p)]
+
+
+class MxLinearAttnViews(ctypes.Structure):
+    _fields_ = [("h32", c_void_p), ("h16", c_void_p), ("qkvz", c_void_p), ("ba", c_void_p),
+                ("q", c_void_p), ("kb", c_void_p), ("v", c_void_p), ("decay", c_void_p),
+                ("o", c_void_p), ("act", c_void_p), ("y", c_void_p)]
+
+
 class MxDeviceInfo(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char * 256), ("arch", ctypes.c_char * 64),
                 ("cu_count", c_int32), ("clock_khz", c_int32), ("mem_clock_khz", c_int32),
@@ -143,6 +167,19 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "mx_tile_weights": (ctypes.c_int, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p]),
     "mx_quantize_rows_i8": (ctypes.c_int, [c_void_p, c_int32, c_int32, c_int32, c_void_p,
                                            c_void_p, c_void_p]),
+    "mx_linear_attn_workspace_size": (ctypes.c_int, [P(MxLinearAttnDesc), c_int32,
+                                                     P(c_size_t)]),
+    "mx_linear_attn_views": (ctypes.c_int, [P(MxLinearAttnDesc), c_int32, c_void_p,
+                                            P(MxLinearAttnViews)]),
+    "mx_linear_attn_forward": (ctypes.c_int, [P(MxLinearAttnDesc), P(MxLinearAttnWeights),
+                                              c_void_p, c_void_p, c_int32, c_void_p, c_size_t,
+                                              c_void_p]),
+    "mx_linear_attn_forward_profiled": (ctypes.c_int, [P(MxLinearAttnDesc),
+                                                       P(MxLinearAttnWeights), c_void_p,
+                                                       c_void_p, c_int32, c_void_p, c_size_t,
+                                                       c_void_p, P(c_void_p), c_int32]),
+    "mx_gated_delta_scan": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32,
+                                           c_int32, c_int32, c_int32, c_void_p, c_void_p]),
 }
 
 _lock = threading.Lock()

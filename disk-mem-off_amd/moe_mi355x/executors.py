@@ -26,6 +26,7 @@ import numpy as np
 
 from . import _lib
 from .layout import NORM, MoeLayerLayout
+from .linear_attn import LinearAttnLayout, LinearAttnRunner, has_linear_attn
 from .moe import MoeConfig, MoeRunner
 from .types import DeviceBuffer, HostBuffer, LayerSpec
 
@@ -113,6 +114,8 @@ class _MoeExecutorBase:
         self.max_tokens = max_tokens
         self._runner: MoeRunner | None = None
         self._layouts: dict[int, tuple[list, MoeLayerLayout]] = {}
+        self._la_runner: LinearAttnRunner | None = None
+        self._la_layouts: dict[int, tuple[list, LinearAttnLayout]] = {}
 
     # values supplied by subclasses
     top_k: int
@@ -137,8 +140,10 @@ class _MoeExecutorBase:
                                      routed_scaling=self.routed_scaling, eps=self.rms_norm_eps)
 
     def moe_block(self, layer: LayerSpec, x: np.ndarray, device_weights: DeviceBuffer,
-                  backend: Any, stream: Any) -> np.ndarray:
-        """x + MoE(rms_norm(x)) on the device (the reference ``_moe_mlp_block``)."""
+                  backend: Any, stream: Any, pre: Callable[[int, int], None] | None = None
+                  ) -> np.ndarray:
+        """x + MoE(rms_norm(x)) on the device (the reference ``_moe_mlp_block``); ``pre``
+        rewrites the uploaded activations on the device first (the attention block)."""
         if device_weights.backend != "rocm":
             raise RuntimeError("the MoE step needs the MI355X backend; got "
                                f"{device_weights.backend!r} device buffers")
@@ -153,11 +158,11 @@ class _MoeExecutorBase:
         T = int(np.shape(x)[0])
         self._runner.reserve(desc, max(T, self.max_tokens, 1))
         weights = self._runner.bind(layout, int(device_weights.handle), stream)
-        return self._runner.forward_numpy(desc, weights, x, stream)
+        return self._runner.forward_numpy(desc, weights, x, stream, pre=pre)
 
     def moe_block_granular(self, layer: LayerSpec, x: np.ndarray, device_weights: DeviceBuffer,
-                           backend: Any, stream: Any,
-                           fetch: Callable[[list[int]], None]) -> np.ndarray:
+                           backend: Any, stream: Any, fetch: Callable[[list[int]], None],
+                           pre: Callable[[int, int], None] | None = None) -> np.ndarray:
         """The MoE step when only the layer's non-expert bytes are on the device yet: route
         on the device, ``fetch(expert_ids)`` (the caller copies those routed experts into
         ``device_weights`` and makes ``stream`` wait for the copies), then the experts."""
@@ -174,7 +179,7 @@ class _MoeExecutorBase:
         T = int(np.shape(x)[0])
         self._runner.reserve(desc, max(T, self.max_tokens, 1))
         weights = self._runner.bind(layout, int(device_weights.handle), stream)
-        active = self._runner.route_numpy(desc, weights, x, stream)
+        active = self._runner.route_numpy(desc, weights, x, stream, pre=pre)
         fetch(active)
         return self._runner.finish_numpy(desc, weights, stream)
 
@@ -183,28 +188,36 @@ class _MoeExecutorBase:
         lay = self._layout(layer)
         return lay.core_ranges(layer.nbytes), lay.routed_expert_ranges()
 
+    def _attention(self, layer: LayerSpec, x: np.ndarray, device_weights: DeviceBuffer,
+                   backend: Any, stream: Any) -> tuple[np.ndarray, Any]:
+        """Run (host hook) or schedule (device block, returned as a ``pre`` hook) the
+        layer's attention part."""
+        if self.attention is not None:
+            return self.attention(x, layer, device_weights, backend, stream), None
+        pre = self._device_attention(layer, device_weights, backend, stream)
+        if pre is None and not self._moe_only(layer):
+            raise NotImplementedError(
+                "layer holds attention tensors; pass attention=... to run them")
+        return x, pre
+
+    def _device_attention(self, layer: LayerSpec, device_weights: DeviceBuffer, backend: Any,
+                          stream: Any) -> Callable[[int, int], None] | None:
+        return None
+
     def run_layer_granular(self, layer: LayerSpec, activations: Any, device_weights: DeviceBuffer,
                            backend: Any, stream: Any, fetch: Callable[[list[int]], None]) -> Any:
         """``run_layer`` for a layer whose routed experts are copied on demand."""
-        x = np.asarray(activations, dtype=np.float32)
-        if self.attention is not None:
-            x = self.attention(x, layer, device_weights, backend, stream)
-        elif not self._moe_only(layer):
-            raise NotImplementedError(
-                "layer holds attention tensors; pass attention=... to run them")
-        return self.moe_block_granular(layer, x, device_weights, backend, stream, fetch)
+        x, pre = self._attention(layer, np.asarray(activations, dtype=np.float32),
+                                 device_weights, backend, stream)
+        return self.moe_block_granular(layer, x, device_weights, backend, stream, fetch, pre=pre)
 
     def run_layer(self, layer: LayerSpec, activations: Any, device_weights: DeviceBuffer,
                   backend: Any, stream: Any) -> Any:
-        x = np.asarray(activations, dtype=np.float32)
-        if self.attention is not None:
-            x = self.attention(x, layer, device_weights, backend, stream)
-        elif not self._moe_only(layer):
-            raise NotImplementedError(
-                "layer holds attention tensors; pass attention=... to run them")
+        x, pre = self._attention(layer, np.asarray(activations, dtype=np.float32),
+                                 device_weights, backend, stream)
         if not layer.metadata.get("is_moe", True):
             raise NotImplementedError("dense MLP layers are not handled by this executor")
-        return self.moe_block(layer, x, device_weights, backend, stream)
+        return self.moe_block(layer, x, device_weights, backend, stream, pre=pre)
 
     @staticmethod
     def _moe_only(layer: LayerSpec) -> bool:
@@ -223,6 +236,9 @@ class _MoeExecutorBase:
         if self._runner is not None:
             self._runner.close()
             self._runner = None
+        if self._la_runner is not None:
+            self._la_runner.close()
+            self._la_runner = None
 
 
 class GLM4MoeExecutor(_MoeExecutorBase):
@@ -245,15 +261,74 @@ class GLM4MoeExecutor(_MoeExecutorBase):
 
 class Qwen3NextExecutor(_MoeExecutorBase):
     """Qwen3-Next (Qwen3NextForCausalLM): softmax router, renormalised top-k, no scaling,
-    shared expert scaled by sigmoid(h . shared_expert_gate)."""
+    shared expert scaled by sigmoid(h . shared_expert_gate).
+
+    Linear-attention layers (``metadata["attn_type"]`` "linear", the default as in
+    qwen3_next.py:155) run their Gated DeltaNet block on the device ahead of the MoE
+    block, on the same uploaded activations; full-attention layers need ``attention=``."""
 
     _router_default = _lib.MX_ROUTER_SOFTMAX
 
     def __init__(self, config: dict[str, Any], **kw: Any) -> None:
         super().__init__(config, **kw)
         self.rms_norm_eps = float(config.get("rms_norm_eps", 1e-6))
+        # qwen3_next.py:120-125
+        self.linear_num_key_heads = int(config.get("linear_num_key_heads", 16))
+        self.linear_key_head_dim = int(config.get("linear_key_head_dim", 128))
+        self.linear_num_value_heads = int(config.get("linear_num_value_heads", 32))
+        self.linear_value_head_dim = int(config.get("linear_value_head_dim", 128))
+        self.linear_conv_kernel_dim = int(config.get("linear_conv_kernel_dim", 4))
         self.num_experts = int(config.get("num_experts", config.get("n_routed_experts", 512)))
         self.top_k = int(config.get("num_experts_per_tok", 10))
         self.norm_topk_prob = bool(config.get("norm_topk_prob", True))
         self.routed_scaling = 1.0
         self.num_experts_per_tok = self.top_k
+
+    def linear_attn_layout(self, layer: LayerSpec) -> LinearAttnLayout:
+        meta = layer.metadata["tensors"]
+        hit = self._la_layouts.get(layer.layer_id)
+        if hit is not None and hit[0] is meta:
+            return hit[1]
+        if self.linear_num_key_heads != self.linear_num_value_heads:
+            # qwen3_next.py:75-77 reshapes q/k [T, key heads * dk] with the value-head
+            # count, which fails unless the counts agree.
+            raise ValueError(
+                f"linear attention needs linear_num_key_heads == linear_num_value_heads "
+                f"(got {self.linear_num_key_heads} and {self.linear_num_value_heads})")
+        lay = LinearAttnLayout.from_meta(meta)
+        want = (self.hidden_size, self.linear_num_value_heads, self.linear_key_head_dim,
+                self.linear_value_head_dim, self.linear_conv_kernel_dim)
+        got = (lay.hidden, lay.n_heads, lay.head_dim_k, lay.head_dim_v, lay.conv_kernel)
+        if got != want:
+            raise ValueError(f"layer {layer.layer_id}: linear-attention tensors give "
+                             f"(hidden, heads, dk, dv, conv) = {got}, config says {want}")
+        self._la_layouts[layer.layer_id] = (meta, lay)
+        return lay
+
+    def _device_attention(self, layer: LayerSpec, device_weights: DeviceBuffer, backend: Any,
+                          stream: Any) -> Callable[[int, int], None] | None:
+        if layer.metadata.get("attn_type", "linear") != "linear" or \
+                not has_linear_attn(layer.metadata["tensors"]):
+            return None
+        if device_weights.backend != "rocm":
+            raise RuntimeError("the linear-attention block needs the MI355X backend; got "
+                               f"{device_weights.backend!r} device buffers")
+        lay = self.linear_attn_layout(layer)
+        desc = lay.desc(self.rms_norm_eps)
+        weights = lay.weights(int(device_weights.handle))
+        if self._la_runner is None:
+            self._la_runner = LinearAttnRunner(backend)
+        runner = self._la_runner
+
+        def pre(x_dev: int, tokens: int) -> None:
+            runner.reserve(desc, max(tokens, self.max_tokens, 1), io=False)
+            runner.forward_device(desc, weights, x_dev, x_dev, tokens, stream)
+
+        return pre
+
+    @staticmethod
+    def _moe_only(layer: LayerSpec) -> bool:
+        return all(m["name"] in (NORM, "input_layernorm.weight") or
+                   m["name"].startswith(("mlp.", "linear_attn."))
+                   for m in layer.metadata["tensors"]) and \
+            layer.metadata.get("attn_type", "linear") == "linear"

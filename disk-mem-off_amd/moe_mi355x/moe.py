@@ -10,7 +10,7 @@ from __future__ import annotations
 
 import ctypes
 from dataclasses import dataclass
-from typing import Any
+from typing import Any, Callable
 
 import numpy as np
 
@@ -173,8 +173,10 @@ class MoeRunner:
         _lib.check(rc, "mx_moe_forward")
 
     def forward_numpy(self, desc: _lib.MxMoeDesc, weights: _lib.MxMoeWeights, x: np.ndarray,
-                      stream: Any) -> np.ndarray:
-        """Host fp32 [T, H] in, host fp32 [T, H] out; synchronises ``stream``."""
+                      stream: Any, pre: Callable[[int, int], None] | None = None) -> np.ndarray:
+        """Host fp32 [T, H] in, host fp32 [T, H] out; synchronises ``stream``.  ``pre(x_dev,
+        T)``, when given, runs on ``stream`` after the upload and rewrites the device copy of
+        x in place (for example the layer's attention block) before the MoE block reads it."""
         x = np.ascontiguousarray(x, dtype=np.float32)
         if x.ndim != 2 or x.shape[1] != desc.hidden:
             raise ValueError(f"activations must be [T, {desc.hidden}], got {x.shape}")
@@ -188,6 +190,8 @@ class MoeRunner:
         addr_x = ctypes.addressof(ctypes.c_char.from_buffer(px.view))
         addr_o = ctypes.addressof(ctypes.c_char.from_buffer(po.view))
         self.backend.copy_h2d_ptr_async(self._io["x"].handle, addr_x, nb, stream)
+        if pre is not None:
+            pre(self._io["x"].handle, T)
         self.forward_device(desc, weights, self._io["x"].handle, self._io["out"].handle, T, stream)
         self.backend.copy_d2h_ptr_async(addr_o, self._io["out"].handle, nb, stream)
         self.backend.synchronize_stream(stream)
@@ -195,9 +199,10 @@ class MoeRunner:
 
     # -- split forward (router part, then the expert part after the experts are copied) --
     def route_numpy(self, desc: _lib.MxMoeDesc, weights: _lib.MxMoeWeights, x: np.ndarray,
-                    stream: Any) -> list[int]:
-        """Upload x and run stages 0..3 (RMSNorm, router, top-k, dispatch); returns the
-        routed experts the batch uses, ascending (synchronises ``stream``)."""
+                    stream: Any, pre: Callable[[int, int], None] | None = None) -> list[int]:
+        """Upload x (then ``pre`` as in ``forward_numpy``) and run stages 0..3 (RMSNorm,
+        router, top-k, dispatch); returns the routed experts the batch uses, ascending
+        (synchronises ``stream``)."""
         x = np.ascontiguousarray(x, dtype=np.float32)
         if x.ndim != 2 or x.shape[1] != desc.hidden:
             raise ValueError(f"activations must be [T, {desc.hidden}], got {x.shape}")
@@ -211,6 +216,8 @@ class MoeRunner:
         self.backend.copy_h2d_ptr_async(self._io["x"].handle,
                                         ctypes.addressof(ctypes.c_char.from_buffer(px.view)),
                                         x.nbytes, stream)
+        if pre is not None:
+            pre(self._io["x"].handle, T)
         self._stages(desc, weights, T, 0, _lib.MX_STAGE_ROUTE_END, stream)
         v = self.views(desc, T)
         ng = int(read_device(self.backend, v.n_groups, np.int32, 1, stream)[0])

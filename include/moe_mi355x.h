@@ -291,6 +291,80 @@ int mx_quantize_rows_i8(const void* w, int32_t w_dtype, int32_t rows, int32_t co
 int mx_tile_weights(void* dst, const void* src, int32_t rows, int32_t cols,
                     int32_t weight_dtype, void* stream);
 
+/* =================================================================================== *
+ * Qwen3-Next linear-attention (Gated DeltaNet) block: Qwen3NextExecutor._linear_attn_block
+ * (offload_runtime/executors/qwen3_next.py:207-269) with its helpers _softplus (:27-28),
+ * _causal_conv1d (:35-53) and _gated_delta_rule_recurrence (:56-95):
+ *   h = rms_norm(x);  [q|k|v|z] = h W_qkvz^T;  [q|k|v] = silu(causal_conv1d([q|k|v]))
+ *   [b|a] = h W_ba^T;  beta = sigmoid(b);  g = -exp(A_log) softplus(a + dt_bias)
+ *   per head: S_t = exp(g_t) S_{t-1} + v_t (beta_t k_t)^T,  o_t = S_t q_t  (S_0 = 0)
+ *   out = x + (rms_norm(o) * silu(z)) W_out^T
+ * The reference reshapes q and k with the value-head count, so it runs only with as
+ * many key heads as value heads; n_heads is that count.  The state starts at zero on
+ * every call (the reference keeps no recurrent state between calls).
+ * =================================================================================== */
+typedef struct MxLinearAttnDesc {
+  int32_t hidden;       /* H                                                            */
+  int32_t n_heads;      /* linear_num_key_heads == linear_num_value_heads               */
+  int32_t head_dim_k;   /* linear_key_head_dim: a power of two, 4..512                  */
+  int32_t head_dim_v;   /* linear_value_head_dim                                        */
+  int32_t conv_kernel;  /* linear_conv_kernel_dim, 1..16                                */
+  int32_t weight_dtype; /* in_proj_qkvz / in_proj_ba / out_proj: F32 / F16 / I8 (+ scales) */
+  int32_t param_dtype;  /* norms, conv1d, A_log, dt_bias: F32 / F16                     */
+  float eps;            /* rms_norm_eps                                                 */
+} MxLinearAttnDesc;
+
+typedef struct MxLinearAttnWeights {
+  const void* norm_w;     /* input_layernorm.weight [H]                                 */
+  const void* qkvz_w;     /* linear_attn.in_proj_qkvz.weight [2 n dk + 2 n dv, H]       */
+  const void* qkvz_scale; /* fp16 per row for MX_DT_I8, else NULL                       */
+  const void* ba_w;       /* linear_attn.in_proj_ba.weight [n dk + n, H]                */
+  const void* ba_scale;
+  const void* conv_w;     /* linear_attn.conv1d.weight [2 n dk + n dv, (1,) K]          */
+  const void* a_log;      /* linear_attn.A_log [n]                                      */
+  const void* dt_bias;    /* linear_attn.dt_bias [n]                                    */
+  const void* out_norm_w; /* linear_attn.norm.weight [n dv]                             */
+  const void* out_w;      /* linear_attn.out_proj.weight [H, n dv]                      */
+  const void* out_scale;
+} MxLinearAttnWeights;
+
+/* Views into a linear-attention workspace (device pointers), for inspection.          */
+typedef struct MxLinearAttnViews {
+  float* h32;    /* [T, H] rms_norm(x)                                                  */
+  void* h16;     /* [T, H] fp16 copy (NULL for F32 weights)                             */
+  float* qkvz;   /* [T, 2 n dk + 2 n dv] h W_qkvz^T                                     */
+  float* ba;     /* [T, n dk + n] h W_ba^T                                              */
+  float* q;      /* [T, n dk] silu(conv(q))                                             */
+  float* kb;     /* [T, n dk] sigmoid(b) * silu(conv(k))                                */
+  float* v;      /* [T, n dv] silu(conv(v))                                             */
+  float* decay;  /* [T, n] exp(g)                                                       */
+  float* o;      /* [T, n dv] recurrence output                                         */
+  void* act;     /* [T, n dv] rms_norm(o) * silu(z), fp16 (fp32 for F32 weights)        */
+  float* y;      /* [T, H] act W_out^T                                                  */
+} MxLinearAttnViews;
+
+#define MX_LA_N_STAGES 8 /* rmsnorm, qkvz, ba, conv+gates, scan, gated norm, out, residual */
+
+int mx_linear_attn_workspace_size(const MxLinearAttnDesc* desc, int32_t tokens,
+                                  size_t* nbytes);
+int mx_linear_attn_views(const MxLinearAttnDesc* desc, int32_t tokens, void* workspace,
+                         MxLinearAttnViews* views);
+/* out may alias x (the block reads x first, then writes out element by element). */
+int mx_linear_attn_forward(const MxLinearAttnDesc* desc, const MxLinearAttnWeights* weights,
+                           const float* x, float* out, int32_t tokens, void* workspace,
+                           size_t workspace_bytes, void* stream);
+/* Same, with an event recorded before each of the MX_LA_N_STAGES stages and at the end. */
+int mx_linear_attn_forward_profiled(const MxLinearAttnDesc* desc,
+                                    const MxLinearAttnWeights* weights, const float* x,
+                                    float* out, int32_t tokens, void* workspace,
+                                    size_t workspace_bytes, void* stream, void* const* events,
+                                    int32_t n_events);
+/* The recurrence alone (qwen3_next.py:56-95 with beta * k formed): q, kb [T, n dk],
+ * v, o [T, n dv], decay [T, n] = exp(g), all fp32 on the device.                      */
+int mx_gated_delta_scan(const float* q, const float* kb, const float* v, const float* decay,
+                        int32_t tokens, int32_t n_heads, int32_t head_dim_k,
+                        int32_t head_dim_v, float* o, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

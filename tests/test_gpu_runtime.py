@@ -183,3 +183,46 @@ def test_host_attention_layers_match_oracle(mi355x):
     err = normwise_err(out, ref)
     say(f"    normwise err {err:.2e}")
     assert err <= 5e-3
+
+
+@pytest.mark.parametrize("granular", [False, True])
+def test_qwen_linear_attention_layers_match_oracle(mi355x, granular):
+    """Full Qwen3-Next linear-attention layers (Gated DeltaNet + MoE tensors in one packed
+    buffer, attn_type "linear"): both blocks on the device, chained by the runtime."""
+    from oracle import linear_attn_oracle as la
+
+    say(f"[gpu] Qwen3-Next linear-attention layers, expert_granular={granular}")
+    shape = syn.MoeShape(syn.QWEN, 256, 32, 6, 64, 64, 1.0, 1e-6, has_bias=False,
+                         has_shared_gate=True)
+    lshape = syn.LinearAttnShape(256, 4, 32, 32, 4, 1e-6)
+    tensors, layers, blobs = [], [], {}
+    for i in range(3):
+        t = syn.make_tensors(shape, 90 + i, weight_dtype=np.float16)
+        t.update(syn.make_linear_attn_tensors(lshape, 90 + i, weight_dtype=np.float16,
+                                              param_dtype=np.float32))
+        raw, meta = pack_tensors(t)  # loader packing: contiguous, lexicographic
+        layers.append(make_layer_spec(i, meta, len(raw), attn_type="linear"))
+        pin = mi355x.alloc_pinned_host(len(raw))
+        np.frombuffer(pin.view, dtype=np.uint8)[:] = np.frombuffer(raw, dtype=np.uint8)
+        blobs[i] = pin
+        tensors.append(t)
+    cfg = shape.config()
+    cfg.update(lshape.config())
+    ex = Qwen3NextExecutor(cfg)
+    x = syn.make_inputs(91, 9, shape.hidden)
+    rt = OffloadRuntime(layers, mi355x, InMemoryStorage(blobs), LookaheadScheduler(1), ex,
+                        expert_granular=granular)
+    try:
+        out, _ = rt.run_inference([0, 1, 2], x)
+    finally:
+        rt.close()
+        ex.close()
+        for pin in blobs.values():
+            mi355x.free_pinned_host(pin)
+    ref = x
+    lspec = la.LinearAttnSpec(lshape.n_heads, lshape.head_dim_k, lshape.head_dim_v, lshape.eps)
+    for t in tensors:
+        ref = orc.moe_block(la.linear_attn_block(ref, t, lspec)["out"], t, spec_for(shape))["out"]
+    err = normwise_err(out, ref)
+    say(f"    normwise err {err:.2e}")
+    assert err <= 5e-3
