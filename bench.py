@@ -15,7 +15,9 @@ in the reference's loop structure on the same full-size layer (routed experts co
 the host), timed on the host cores.  Other BASELINE workloads (decode T=1/8, Zipf
 prefill T=2048, Qwen3-Next T=1/4096, per-row int8 decode T=1/16, and 8 per-row int8
 layers streamed from pinned host memory through the lookahead-2 runtime at T=1/16) are
-reported under "sweep".  Prints ONE JSON line.
+reported under "sweep", with the Qwen3-Next linear-attention (Gated DeltaNet) block at
+T=1/4096 (32 key = value heads of 128, hidden 2048, fp16 projections).  Prints ONE JSON
+line.
 """
 from __future__ import annotations
 
@@ -200,6 +202,79 @@ def cpu_baseline(layer: DeviceMoeLayer, shape: syn.MoeShape, x: np.ndarray, budg
                        f"{len(os.sched_getaffinity(0))} host cores visible, {cpu_model}, "
                        f"numpy {np.__version__}")}
     return base, out, ids
+
+
+def linear_attn_case(backend, stream, shape: syn.LinearAttnShape, tokens: tuple[int, ...],
+                     steps: int, warmup: int) -> dict[str, dict]:
+    """Qwen3-Next linear-attention (Gated DeltaNet) block: fp16 projections, fp32 conv /
+    gates / recurrence, timed like the MoE cases (events around K steps on the launch
+    stream, then a pass with an event between stages).  Roofline of the recurrence scan:
+    5 flops per state element per token (decay multiply, rank-1 update, dot product) on the
+    fp32 vector units; of the projections: weight bytes from HBM."""
+    from moe_mi355x.linear_attn import DeviceLinearAttnLayer
+
+    t = syn.make_linear_attn_tensors(shape, SEED, weight_dtype=np.float16,
+                                     param_dtype=np.float32)
+    layer = DeviceLinearAttnLayer.from_host(backend, t, stream)
+    n, dk, dv, H = shape.n_heads, shape.head_dim_k, shape.head_dim_v, shape.hidden
+    w_bytes = 2 * H * (shape.qkvz_rows + shape.ba_rows + n * dv)
+    out: dict[str, dict] = {}
+    b = backend
+    try:
+        desc, w = layer.desc(shape.eps), layer.weights()
+        r = layer.runner
+        for T in tokens:
+            name = f"qwen3next_linattn_fp16_t{T}"
+            r.reserve(desc, T)
+            x = syn.make_inputs(SEED + T, T, H)
+            b.copy_h2d_ptr_async(r._io["x"].handle, x.ctypes.data, x.nbytes, stream)
+            b.synchronize_stream(stream)
+            k = min(steps, 20)
+
+            def step(ev=None):
+                r.forward_device(desc, w, r._io["x"].handle, r._io["out"].handle, T, stream, ev)
+
+            for _ in range(warmup):
+                step()
+            b.synchronize_stream(stream)
+            e0, e1 = b.create_timing_event(), b.create_timing_event()
+            b.record(e0, stream)
+            for _ in range(k):
+                step()
+            b.record(e1, stream)
+            b.event_synchronize(e1)
+            ms = b.elapsed_ms(e0, e1) / k
+            ev = [[b.create_timing_event() for _ in range(_lib.MX_LA_N_STAGES + 1)]
+                  for _ in range(k)]
+            for i in range(k):
+                step(ev[i])
+            b.event_synchronize(ev[-1][-1])
+            st = np.array([[b.elapsed_ms(e[j], e[j + 1]) for j in range(_lib.MX_LA_N_STAGES)]
+                           for e in ev]).mean(axis=0)
+            for e in ev + [[e0, e1]]:
+                for x_ in e:
+                    b.destroy_event(x_)
+            scan_s = st[4] / 1e3
+            scan_flops = 5.0 * T * n * dk * dv
+            scan_bytes = 4.0 * T * (2 * n * dk + 2 * n * dv + n)
+            proj_s = (st[1] + st[2] + st[6]) / 1e3
+            out[name] = {
+                "workload": name, "tokens_per_s": round(T / (ms / 1e3), 1),
+                "ms_per_step": round(ms, 4),
+                "stage_ms": {nm: round(float(v), 4) for nm, v in zip(_lib.LA_STAGE_NAMES, st)},
+                "scan": {"ms": round(st[4], 4), "flops": scan_flops, "bytes": scan_bytes,
+                         "TFLOPs": round(scan_flops / scan_s / 1e12, 2),
+                         "frac_fp32_peak": round(scan_flops / scan_s / MFMA_F32_PEAK, 4),
+                         "GBps": round(scan_bytes / scan_s / 1e9, 1)},
+                "projections": {"ms": round(proj_s * 1e3, 4), "weight_bytes": w_bytes,
+                                "hbm_frac": round(w_bytes / proj_s / HBM_PEAK, 4),
+                                "mfma_frac": round(2.0 * T * w_bytes / 2 / proj_s /
+                                                   MFMA_F16_PEAK, 4)},
+            }
+            log(f"{name}: {out[name]['tokens_per_s']} tok/s, {ms:.3f} ms, scan {st[4]:.3f} ms")
+    finally:
+        layer.close()
+    return out
 
 
 def stream_case(backend, shape: syn.MoeShape, tokens: tuple[int, ...], n_layers: int = 8,
@@ -403,7 +478,7 @@ def main() -> int:
         layer.close()
 
     # ---- Qwen3-Next fp16 layer ---------------------------------------------------------------
-    if not args.no_sweep and (only is None or only.startswith("qwen3next")):
+    if not args.no_sweep and (only is None or only.startswith("qwen3next_fp16")):
         Q = syn.QWEN3_NEXT
         layer = DeviceMoeLayer.synthetic(backend, Q, SEED, stream, weight_dtype="float16",
                                          param_dtype="float32")
@@ -419,6 +494,12 @@ def main() -> int:
             sweep[name] = summarize(r, name, "float16")
             log(f"{name}: {sweep[name]['tokens_per_s']} tok/s")
         layer.close()
+
+    # ---- Qwen3-Next linear-attention (Gated DeltaNet) block -------------------------------------
+    if not args.no_sweep and (only is None or only.startswith("qwen3next_linattn")):
+        toks = (1, 4096) if only is None else (int(only.rsplit("_t", 1)[1]),)
+        sweep.update(linear_attn_case(backend, stream, syn.QWEN3_NEXT_LINEAR, toks, args.steps,
+                                      3))
 
     # ---- 8 int8 GLM-4.7 layers streamed from pinned host memory -------------------------------
     if not args.no_sweep and (only is None or only.startswith("glm47_int8_stream")):

@@ -45,3 +45,10 @@ struct MxDenseTables {
 // scales) is entry->down (->down_scale).  a is fp32 for MX_DT_F32 weights, else fp16.
 int mx_dense_linear(int wdt, int tiled, const MxExpertPtrs* entry, const MxDenseTables& tab,
                     int T, int N, int K, const void* a, float* y, hipStream_t s);
+
+// Dense y[T, N] (fp32) = a[T, K] W[N, K]^T on hipBLASLt (dtype MX_DT_F16: fp16 a and W,
+// MX_DT_F32: fp32), fp32 accumulation; ws of ws_bytes (mx_gemm_workspace_bytes()) is the
+// library's workspace.  MX_ERR_UNSUPPORTED when the library has no algorithm for the shape.
+size_t mx_gemm_workspace_bytes();
+int mx_gemm_wt(int dtype, const void* a, const void* w, float* y, int T, int N, int K, void* ws,
+               size_t ws_bytes, hipStream_t s);

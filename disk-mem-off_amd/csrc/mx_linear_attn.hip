@@ -63,8 +63,18 @@ struct Carve {
   }
 };
 
+// Inputs longer than this run the projections on hipBLASLt (fp16 / fp32 weights); shorter
+// ones, and int8 weights, on the HBM-streaming expert kernels.
+#define LA_BLAS_MIN_TOKENS 65
+
+bool use_blas(const MxLinearAttnDesc* d, int T) {
+  return T >= LA_BLAS_MIN_TOKENS && d->weight_dtype != MX_DT_I8;
+}
+
 struct LaWork {
   MxLinearAttnViews v;
+  void* blas_ws;          // hipBLASLt workspace (long inputs), else NULL
+  size_t blas_ws_bytes;
   MxExpertPtrs* entries;  // [3]: qkvz, ba, out
   int* tabs;              // g_expert, g_start, g_count, n_mtiles (4 ints)
   int* mt_group;
@@ -99,6 +109,8 @@ int layout(const MxLinearAttnDesc* d, int T, void* ws, LaWork* w, size_t* total)
   t.mt_group = (int*)c.take((size_t)n_mt * 4);
   t.mt_row0 = (int*)c.take((size_t)n_mt * 4);
   t.ones = (float*)c.take(Tn * 4);
+  t.blas_ws_bytes = use_blas(d, (int)Tn) ? mx_gemm_workspace_bytes() : 0;
+  t.blas_ws = t.blas_ws_bytes ? c.take(t.blas_ws_bytes) : nullptr;
   t.m_blk = m_blk;
   t.n_mt = n_mt;
   if (w) *w = t;
@@ -136,10 +148,15 @@ __global__ __launch_bounds__(256) void k_la_setup(int T, int m_blk, int n_mt,
 }
 
 // Causal depthwise conv + SiLU on the q/k/v channels, beta * k, and the per-head decay.
-// Grid (ceil((C + n) / 256), T).  Thread c < C: out = sum_{j=0}^{K-1} x[t - j, c] w[c, j]
-// summed in j order from 0 (qwen3_next.py:49-52), then silu (:238); k channels times
-// sigmoid(b) (:244, :89).  Thread C + h: g = -exp(A_log) softplus(a + dt_bias) (:249),
-// decay = exp(g) (:84).  Products are rounded before each sum, as NumPy does.
+// Grid (ceil((C + n) / 256), ceil(T / LA_TT)); a thread walks LA_TT consecutive tokens of
+// one channel with the last K - 1 inputs in registers (KC = K known at compile time, 0 =
+// any K up to 16, re-read from memory).  Channel c < C: out = sum_{j=0}^{K-1} x[t - j, c]
+// w[c, j], summed in j order from 0 (qwen3_next.py:49-52), then silu (:238); k channels
+// times sigmoid(b) (:244, :89).  Thread C + h: g = -exp(A_log) softplus(a + dt_bias)
+// (:249), decay = exp(g) (:84).  Products are rounded before each sum, as NumPy does.
+#define LA_TT 16
+
+template <int KC>
 __global__ __launch_bounds__(256) void k_la_prep(const float* __restrict__ qkvz,
                                                  const float* __restrict__ ba,
                                                  const void* __restrict__ conv_w,
@@ -149,44 +166,99 @@ __global__ __launch_bounds__(256) void k_la_prep(const float* __restrict__ qkvz,
                                                  float* __restrict__ kb, float* __restrict__ v,
                                                  float* __restrict__ decay) {
 #pragma clang fp contract(off)
-  const int t = blockIdx.y;
+  const int t0 = blockIdx.y * LA_TT;
+  const int t1 = min(T, t0 + LA_TT);
   const int c = blockIdx.x * 256 + threadIdx.x;
   if (c < m.C) {
-    float acc = 0.f;
-    for (int j = 0; j < m.K && j <= t; ++j)
-      acc += qkvz[(size_t)(t - j) * m.W1 + c] * mx_load_param(conv_w, pdt, c * m.K + j);
-    const float s = mx_silu(acc);
+    float* dst;
+    int ld;
+    const float* gate = nullptr;
     if (c < m.qd) {
-      q[(size_t)t * m.qd + c] = s;
+      dst = q + c;
+      ld = m.qd;
     } else if (c < 2 * m.qd) {
-      const int ck = c - m.qd;
-      kb[(size_t)t * m.qd + ck] = mx_sigmoid(ba[(size_t)t * m.W2 + ck]) * s;
+      dst = kb + (c - m.qd);
+      ld = m.qd;
+      gate = ba + (c - m.qd);
     } else {
-      v[(size_t)t * m.vd + (c - 2 * m.qd)] = s;
+      dst = v + (c - 2 * m.qd);
+      ld = m.vd;
+    }
+    const float* x = qkvz + c;
+    if constexpr (KC > 0) {
+      // Before token t's shift win[j] = x[t - 1 - j]; after it win[j] = x[t - j].
+      float w[KC], win[KC];
+#pragma unroll
+      for (int j = 0; j < KC; ++j) {
+        w[j] = mx_load_param(conv_w, pdt, c * KC + j);
+        win[j] = (t0 - 1 - j >= 0) ? x[(size_t)(t0 - 1 - j) * m.W1] : 0.f;
+      }
+      // All of the thread's inputs first (independent loads in flight together).
+      float xs[LA_TT], gs[LA_TT];
+#pragma unroll
+      for (int i = 0; i < LA_TT; ++i) {
+        const int t = min(t0 + i, T - 1);
+        xs[i] = x[(size_t)t * m.W1];
+        gs[i] = gate ? gate[(size_t)t * m.W2] : 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < LA_TT; ++i) {
+#pragma unroll
+        for (int j = KC - 1; j > 0; --j) win[j] = win[j - 1];
+        win[0] = xs[i];
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < KC; ++j) acc += win[j] * w[j];
+        float s = mx_silu(acc);
+        if (gate) s = mx_sigmoid(gs[i]) * s;
+        if (t0 + i < t1) dst[(size_t)(t0 + i) * ld] = s;
+      }
+    } else {
+      for (int t = t0; t < t1; ++t) {
+        float acc = 0.f;
+        for (int j = 0; j < m.K && j <= t; ++j)
+          acc += x[(size_t)(t - j) * m.W1] * mx_load_param(conv_w, pdt, c * m.K + j);
+        float s = mx_silu(acc);
+        if (gate) s = mx_sigmoid(gate[(size_t)t * m.W2]) * s;
+        dst[(size_t)t * ld] = s;
+      }
     }
   } else if (c < m.C + m.n) {
     const int h = c - m.C;
     float ea = expf(mx_load_param(a_log, pdt, h));
     if (pdt == MX_DT_F16) ea = (float)(half_t)ea;  // np.exp of an fp16 array stays fp16
-    const float a = ba[(size_t)t * m.W2 + m.qd + h] + mx_load_param(dt_bias, pdt, h);
-    const float sp = a > 20.f ? a : log1pf(expf(a));
-    decay[(size_t)t * m.n + h] = expf(-ea * sp);
+    const float bias = mx_load_param(dt_bias, pdt, h);
+    for (int t = t0; t < t1; ++t) {
+      const float a = ba[(size_t)t * m.W2 + m.qd + h] + bias;
+      const float sp = a > 20.f ? a : log1pf(expf(a));
+      decay[(size_t)t * m.n + h] = expf(-ea * sp);
+    }
   }
 }
 
-// The recurrence.  Lane (row group rr, column group cg) of a wave holds CPL consecutive
-// state columns c0 = cg * CPL of one state row (head h, value index i):
-//   S[i, c] = S[i, c] * decay_t + v_t[i] * kb_t[c];   o_t[i] = sum_c S[i, c] q_t[c]
-// with the dot product finished across the L = dk / CPL lanes of the row (DPP inside a
-// 16-lane row, lane shuffles beyond).  A block of 4 waves holds RB = 4 * 64 / L rows of
-// one head; per chunk of TC tokens it stages that head's q, kb, its rows of v and the
-// decays in LDS (double-buffered, the next chunk's global loads in flight while the
-// current chunk runs), so every state element reads q and kb from LDS, not from L1.
-template <int CPL, int L>
-struct ScanShape {
-  static constexpr int DK = CPL * L;
-  static constexpr int RW = 64 / L;   // rows per wave
-  static constexpr int RB = 4 * RW;   // rows per block
+// ------------------------------------------------------------------------------------
+// The recurrence:  S[i, c] = S[i, c] * decay_t + v_t[i] * kb_t[c];  o_t[i] = sum_c S[i, c] q_t[c]
+// per head (state rows i = value index, columns c = key index), from S = 0.
+//
+// A block of 4 waves holds RB state rows of one head.  Per chunk of TC tokens it stages
+// that head's q and kb, its rows of v and the decays in LDS (double-buffered: the next
+// chunk's global loads are in flight while the current chunk runs), so every state
+// element reads q and kb from LDS rather than L1.  Full chunks run unrolled and branch-
+// free with the (state-independent) LDS reads of later tokens issued ahead of the update
+// chain; each output is kept by one lane of its row and all are stored after the chunk.
+//
+// Two lane mappings:
+//  * k_la_scan_wide (dk >= 64): a wave holds 4 rows; lane l holds columns
+//    [l * CPL, (l + 1) * CPL) of all 4 (CPL = dk / 64), so the q and kb values a lane
+//    reads serve 4 rows.  The 4 dot products are reduce-scattered across the wave with
+//    the gfx950 lane swaps (v_permlane32_swap: halves, v_permlane16_swap: rows of 16)
+//    and finished by DPP inside each row of 16: 3 swaps + 3 adds + 4 DPP adds for 4 sums.
+//  * k_la_scan (dk <= 32): lane (row group, column group) holds CPL columns of one row,
+//    the dot product is finished across the L = dk / CPL lanes of the row with DPP.
+// ------------------------------------------------------------------------------------
+template <int DK_, int RB_>
+struct ScanStage {
+  static constexpr int DK = DK_, RB = RB_;
   static constexpr int TC = DK >= 512 ? 4 : (DK >= 256 ? 8 : 16);  // tokens per chunk
   static constexpr int NQ = TC * DK;  // floats of q (and of kb) per chunk
   static constexpr int NQ4 = NQ / 4;  // float4 pieces of q (and of kb) per chunk
@@ -195,7 +267,96 @@ struct ScanShape {
   static constexpr int VP = (NV + 255) / 256;
   static constexpr int BUF = 2 * NQ + NV + TC;  // floats per LDS buffer
   static_assert(DK % 4 == 0, "key head size must be a multiple of 4");
+
+  // Registers of one staged chunk.  Offsets are in elements (T * n * max(dk, dv) < 2^31
+  // is checked by the launcher).  q and kb: float4 piece i = (token i / (DK / 4), columns
+  // 4 (i % (DK / 4)) ..) of head h; v: value i = (token i / RB, row rb0 + i % RB); decay:
+  // one per token.
+  float4 qv[QP], kv[QP];
+  float vv[VP];
+  float dd;
+
+  __device__ __forceinline__ void load(const float* __restrict__ q,
+                                       const float* __restrict__ kb,
+                                       const float* __restrict__ v,
+                                       const float* __restrict__ decay, int t0, int T, int n,
+                                       int dv, int h, int rb0) {
+    const int tid = threadIdx.x;
+    const int qd = n * DK, vd = n * dv;
+#pragma unroll
+    for (int p = 0; p < QP; ++p) {
+      const int i = tid + 256 * p;
+      const int t = t0 + i / (DK / 4);
+      const bool ok = i < NQ4 && t < T;
+      const int off = t * qd + h * DK + 4 * (i % (DK / 4));
+      qv[p] = ok ? *(const float4*)(q + off) : make_float4(0.f, 0.f, 0.f, 0.f);
+      kv[p] = ok ? *(const float4*)(kb + off) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int p = 0; p < VP; ++p) {
+      const int i = tid + 256 * p;
+      const int t = t0 + i / RB, r2 = rb0 + i % RB;
+      vv[p] = (i < NV && t < T && r2 < dv) ? v[t * vd + h * dv + r2] : 0.f;
+    }
+    dd = (tid < TC && t0 + tid < T) ? decay[(t0 + tid) * n + h] : 0.f;
+  }
+
+  __device__ __forceinline__ void store(float* b) const {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int p = 0; p < QP; ++p) {
+      const int i = tid + 256 * p;
+      if (i < NQ4) {
+        ((float4*)b)[i] = qv[p];
+        ((float4*)(b + NQ))[i] = kv[p];
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < VP; ++p) {
+      const int i = tid + 256 * p;
+      if (i < NV) b[2 * NQ + i] = vv[p];
+    }
+    if (tid < TC) b[2 * NQ + NV + tid] = dd;
+  }
 };
+
+// Walks the chunks of [0, T): chunk c is computed from LDS buffer c % 2 while the global
+// loads of chunks c + 1 and c + 2 are in flight in two register stages, so every load has
+// at least one chunk of compute to arrive before it is written to LDS.  One barrier per
+// chunk: the buffer written after chunk c was last read in chunk c - 1, before every wave
+// passed the barrier that ended that chunk.  compute(buf, t0) runs one chunk.
+template <class St, class F>
+__device__ __forceinline__ void la_chunks(const float* __restrict__ q,
+                                          const float* __restrict__ kb,
+                                          const float* __restrict__ v,
+                                          const float* __restrict__ decay, int T, int n, int dv,
+                                          int h, int rb0, float (*lds)[St::BUF], F&& compute) {
+  constexpr int TC = St::TC;
+  const int nchunk = (T + TC - 1) / TC;
+  St sa, sb;
+  sa.load(q, kb, v, decay, 0, T, n, dv, h, rb0);
+  sa.store(lds[0]);
+  if (nchunk > 1) sa.load(q, kb, v, decay, TC, T, n, dv, h, rb0);
+  if (nchunk > 2) sb.load(q, kb, v, decay, 2 * TC, T, n, dv, h, rb0);
+  __syncthreads();
+  for (int ch = 0; ch < nchunk; ch += 2) {
+    compute(lds[0], ch * TC);  // sa: chunk ch + 1, sb: chunk ch + 2
+    if (ch + 1 >= nchunk) break;
+    sa.store(lds[1]);
+    __syncthreads();
+    if (ch + 3 < nchunk) sa.load(q, kb, v, decay, (ch + 3) * TC, T, n, dv, h, rb0);
+    compute(lds[1], (ch + 1) * TC);  // sb: chunk ch + 2, sa: chunk ch + 3
+    if (ch + 2 >= nchunk) break;
+    sb.store(lds[0]);
+    __syncthreads();
+    if (ch + 4 < nchunk) sb.load(q, kb, v, decay, (ch + 4) * TC, T, n, dv, h, rb0);
+  }
+}
+
+// Tokens of LDS reads in flight ahead of the recurrence update (full chunks).
+#ifndef LA_SCAN_PD
+#define LA_SCAN_PD 2
+#endif
 
 template <int L>
 __device__ __forceinline__ float la_row_sum(float v) {
@@ -208,129 +369,217 @@ __device__ __forceinline__ float la_row_sum(float v) {
   return v;
 }
 
+// Sums of p[0..3] over the 64 lanes; row j (lanes 16 j .. 16 j + 15) returns the sum of
+// p[j].  permlane32_swap(a, b) gives (lanes < 32: a[l], a[l + 32]; lanes >= 32: b[l - 32],
+// b[l]), permlane16_swap(a, b) the same between the rows of 16 of each half.  Both
+// elements of a swap's result are copied to integers before conversion: this compiler
+// folds __builtin_bit_cast(float, r[1]) of the result vector into r[0].
+__device__ __forceinline__ float la_swap_sum32(float a, float b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false,
+                                                  false);
+  const unsigned x0 = r[0], x1 = r[1];
+  return __uint_as_float(x0) + __uint_as_float(x1);
+}
+
+__device__ __forceinline__ float la_swap_sum16(float a, float b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false,
+                                                  false);
+  const unsigned x0 = r[0], x1 = r[1];
+  return __uint_as_float(x0) + __uint_as_float(x1);
+}
+
+__device__ __forceinline__ float la_wave_sum4(const float (&p)[4]) {
+  const float u0 = la_swap_sum32(p[0], p[2]);
+  const float u1 = la_swap_sum32(p[1], p[3]);
+  return la_row_sum<16>(la_swap_sum16(u0, u1));
+}
+
+template <int CPL>
+__global__ __launch_bounds__(256) void k_la_scan_wide(const float* __restrict__ q,
+                                                      const float* __restrict__ kb,
+                                                      const float* __restrict__ v,
+                                                      const float* __restrict__ decay, int T,
+                                                      int n, int dv, int bph,
+                                                      float* __restrict__ o) {
+  constexpr int DK = 64 * CPL, RB = 16;
+  using St = ScanStage<DK, RB>;
+  constexpr int TC = St::TC, NQ = St::NQ, NV = St::NV;
+  __shared__ __align__(16) float lds[2][St::BUF];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int h = blockIdx.x / bph;
+  const int rb0 = (blockIdx.x - h * bph) * RB;  // first value row of this block in head h
+  const int r0 = wave * 4;                      // first row of this wave in the block
+  const int c0 = lane * CPL;
+  const int j = lane >> 4, tl = lane & 15;      // this lane's row (of 4) and token slot
+  const int row = rb0 + r0 + j;
+  const bool rvalid = row < dv;
+  const int vd = n * dv;
+
+  float S[4][CPL];
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) S[m][c] = 0.f;
+
+  la_chunks<St>(q, kb, v, decay, T, n, dv, h, rb0, lds, [&](const float* sq, int t0) {
+    const float* sk = sq + NQ;
+    const float* sv = sk + NQ;
+    const float* sd = sv + NV;
+    auto token = [&](int tt, const float (&qv)[CPL], const float (&kv)[CPL],
+                     const float4& vr, float dd) {
+      const float vv[4] = {vr.x, vr.y, vr.z, vr.w};
+      float part[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        part[m] = 0.f;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+          S[m][c] = S[m][c] * dd + vv[m] * kv[c];
+          part[m] += S[m][c] * qv[c];
+        }
+      }
+      return la_wave_sum4(part);
+    };
+    auto fetch = [&](int tt, float (&qv)[CPL], float (&kv)[CPL], float4& vr, float& dd) {
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        qv[c] = sq[tt * DK + c0 + c];
+        kv[c] = sk[tt * DK + c0 + c];
+      }
+      vr = *(const float4*)(sv + tt * RB + r0);
+      dd = sd[tt];
+    };
+    if (t0 + TC <= T) {
+      constexpr int PD = LA_SCAN_PD;
+      float rq[PD + 1][CPL], rk[PD + 1][CPL], rd[PD + 1];
+      float4 rv[PD + 1];
+      float keep = 0.f;
+#pragma unroll
+      for (int tt = 0; tt < PD && tt < TC; ++tt) fetch(tt, rq[tt], rk[tt], rv[tt], rd[tt]);
+#pragma unroll
+      for (int tt = 0; tt < TC; ++tt) {
+        if (tt + PD < TC) {
+          const int b = (tt + PD) % (PD + 1);
+          fetch(tt + PD, rq[b], rk[b], rv[b], rd[b]);
+        }
+        const int b = tt % (PD + 1);
+        const float ov = token(tt, rq[b], rk[b], rv[b], rd[b]);
+        keep = tl == tt ? ov : keep;
+      }
+      if (tl < TC && rvalid) o[(t0 + tl) * vd + h * dv + row] = keep;
+    } else {
+      for (int tt = 0; tt < T - t0; ++tt) {
+        float qv[CPL], kv[CPL], dd;
+        float4 vr;
+        fetch(tt, qv, kv, vr, dd);
+        const float ov = token(tt, qv, kv, vr, dd);
+        if (tl == 0 && rvalid) o[(t0 + tt) * vd + h * dv + row] = ov;
+      }
+    }
+  });
+}
+
 template <int CPL, int L>
 __global__ __launch_bounds__(256) void k_la_scan(const float* __restrict__ q,
                                                  const float* __restrict__ kb,
                                                  const float* __restrict__ v,
                                                  const float* __restrict__ decay, int T, int n,
                                                  int dv, int bph, float* __restrict__ o) {
-  using Sh = ScanShape<CPL, L>;
-  constexpr int DK = Sh::DK, RB = Sh::RB, TC = Sh::TC, NQ = Sh::NQ, NQ4 = Sh::NQ4;
-  constexpr int QP = Sh::QP, NV = Sh::NV, VP = Sh::VP;
-  __shared__ __align__(16) float lds[2][Sh::BUF];
+  constexpr int DK = CPL * L, RW = 64 / L, RB = 4 * RW;
+  using St = ScanStage<DK, RB>;
+  constexpr int TC = St::TC, NQ = St::NQ, NV = St::NV;
+  __shared__ __align__(16) float lds[2][St::BUF];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int h = blockIdx.x / bph;
   const int rb0 = (blockIdx.x - h * bph) * RB;  // first value row of this block in head h
   const int rr = lane / L, cg = lane % L;
-  const int rloc = wave * Sh::RW + rr;  // row within the block
+  const int rloc = wave * RW + rr;  // row within the block
   const int row = rb0 + rloc;
   const bool rvalid = row < dv;
   const int c0 = cg * CPL;
-  const int qd = n * DK, vd = n * dv;
-
-  // Chunk staging (all offsets in elements; T * n * max(dk, dv) < 2^31 is checked by the
-  // launcher).  q and kb: float4 piece i = (token i / (DK / 4), columns 4 (i % (DK / 4))..)
-  // of head h; v: value i = (token i / RB, row rb0 + i % RB); decay: one per token.
-  struct Stage {
-    float4 qv[QP], kv[QP];
-    float vv[VP];
-    float dd;
-  };
-  auto load_chunk = [&](int t0, Stage& r) {
-#pragma unroll
-    for (int p = 0; p < QP; ++p) {
-      const int i = tid + 256 * p;
-      const int t = t0 + i / (DK / 4);
-      const bool ok = i < NQ4 && t < T;
-      const int off = t * qd + h * DK + 4 * (i % (DK / 4));
-      r.qv[p] = ok ? *(const float4*)(q + off) : make_float4(0.f, 0.f, 0.f, 0.f);
-      r.kv[p] = ok ? *(const float4*)(kb + off) : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-#pragma unroll
-    for (int p = 0; p < VP; ++p) {
-      const int i = tid + 256 * p;
-      const int t = t0 + i / RB, r2 = rb0 + i % RB;
-      r.vv[p] = (i < NV && t < T && r2 < dv) ? v[t * vd + h * dv + r2] : 0.f;
-    }
-    r.dd = (tid < TC && t0 + tid < T) ? decay[(t0 + tid) * n + h] : 0.f;
-  };
-  auto store_chunk = [&](int buf, const Stage& r) {
-    float* b = lds[buf];
-#pragma unroll
-    for (int p = 0; p < QP; ++p) {
-      const int i = tid + 256 * p;
-      if (i < NQ4) {
-        ((float4*)b)[i] = r.qv[p];
-        ((float4*)(b + NQ))[i] = r.kv[p];
-      }
-    }
-#pragma unroll
-    for (int p = 0; p < VP; ++p) {
-      const int i = tid + 256 * p;
-      if (i < NV) b[2 * NQ + i] = r.vv[p];
-    }
-    if (tid < TC) b[2 * NQ + NV + tid] = r.dd;
-  };
+  const int vd = n * dv;
 
   float S[CPL];
 #pragma unroll
   for (int c = 0; c < CPL; ++c) S[c] = 0.f;
 
-  Stage stage;
-  load_chunk(0, stage);
-  store_chunk(0, stage);
-  __syncthreads();
-  const int nchunk = (T + TC - 1) / TC;
-  for (int ch = 0; ch < nchunk; ++ch) {
-    const int t0 = ch * TC;
-    const int buf = ch & 1;
-    const bool more = ch + 1 < nchunk;
-    if (more) load_chunk(t0 + TC, stage);
-    const float* sq = lds[buf];
+  la_chunks<St>(q, kb, v, decay, T, n, dv, h, rb0, lds, [&](const float* sq, int t0) {
     const float* sk = sq + NQ;
     const float* sv = sk + NQ;
     const float* sd = sv + NV;
-    const int nt = min(TC, T - t0);
-    for (int tt = 0; tt < nt; ++tt) {
-      float qv[CPL], kv[CPL];
+    auto fetch = [&](int tt, float (&qv)[CPL], float (&kv)[CPL], float& vi, float& dd) {
 #pragma unroll
       for (int c = 0; c < CPL; ++c) {
         qv[c] = sq[tt * DK + c0 + c];
         kv[c] = sk[tt * DK + c0 + c];
       }
-      const float vi = sv[tt * RB + rloc];
-      const float dd = sd[tt];
+      vi = sv[tt * RB + rloc];
+      dd = sd[tt];
+    };
+    auto token = [&](const float (&qv)[CPL], const float (&kv)[CPL], float vi, float dd) {
       float part = 0.f;
 #pragma unroll
       for (int c = 0; c < CPL; ++c) {
         S[c] = S[c] * dd + vi * kv[c];
         part += S[c] * qv[c];
       }
-      const float ov = la_row_sum<L>(part);
-      if (cg == 0 && rvalid) o[(t0 + tt) * vd + h * dv + row] = ov;
+      return la_row_sum<L>(part);
+    };
+    if (t0 + TC <= T) {
+      // Lane cg of a row keeps the outputs of tokens cg, cg + L, ...
+      constexpr int NK = (TC + L - 1) / L;
+      constexpr int PD = LA_SCAN_PD;
+      float keep[NK];
+#pragma unroll
+      for (int i = 0; i < NK; ++i) keep[i] = 0.f;
+      float rq[PD + 1][CPL], rk[PD + 1][CPL], rv[PD + 1], rd[PD + 1];
+#pragma unroll
+      for (int tt = 0; tt < PD && tt < TC; ++tt) fetch(tt, rq[tt], rk[tt], rv[tt], rd[tt]);
+#pragma unroll
+      for (int tt = 0; tt < TC; ++tt) {
+        if (tt + PD < TC) {
+          const int b = (tt + PD) % (PD + 1);
+          fetch(tt + PD, rq[b], rk[b], rv[b], rd[b]);
+        }
+        const int b = tt % (PD + 1);
+        const float ov = token(rq[b], rk[b], rv[b], rd[b]);
+        keep[tt / L] = cg == tt % L ? ov : keep[tt / L];
+      }
+#pragma unroll
+      for (int i = 0; i < NK; ++i) {
+        const int tt = i * L + cg;
+        if (tt < TC && rvalid) o[(t0 + tt) * vd + h * dv + row] = keep[i];
+      }
+    } else {
+      for (int tt = 0; tt < T - t0; ++tt) {
+        float qv[CPL], kv[CPL], vi, dd;
+        fetch(tt, qv, kv, vi, dd);
+        const float ov = token(qv, kv, vi, dd);
+        if (cg == 0 && rvalid) o[(t0 + tt) * vd + h * dv + row] = ov;
+      }
     }
-    if (more) {
-      // The other buffer was last read in chunk ch - 1, before every wave passed the
-      // barrier that ended that chunk.
-      store_chunk(buf ^ 1, stage);
-      __syncthreads();
-    }
-  }
+  });
 }
 
 template <int CPL, int L>
 int launch_scan(const float* q, const float* kb, const float* v, const float* decay, int T,
                 int n, int dv, float* o, hipStream_t s) {
-  using Sh = ScanShape<CPL, L>;
-  const int bph = mx_ceil_div(dv, Sh::RB);
+  constexpr bool wide = L == 64;
+  constexpr int RB = wide ? 16 : 4 * (64 / L);
+  const int bph = mx_ceil_div(dv, RB);
   const long blocks = (long)n * bph;
-  const long dmax = Sh::DK > dv ? Sh::DK : dv;
+  const long dmax = CPL * L > dv ? CPL * L : dv;
   if (blocks > (1l << 31) - 1 || (long)T * n * dmax >= (1l << 31)) return MX_ERR_UNSUPPORTED;
   if (!mx_aligned16(q) || !mx_aligned16(kb)) return MX_ERR_ALIGNMENT;
   mx_clear_error();
-  hipLaunchKernelGGL((k_la_scan<CPL, L>), dim3((unsigned)blocks), dim3(256), 0, s, q, kb, v,
-                     decay, T, n, dv, bph, o);
+  if constexpr (wide)
+    hipLaunchKernelGGL((k_la_scan_wide<CPL>), dim3((unsigned)blocks), dim3(256), 0, s, q, kb,
+                       v, decay, T, n, dv, bph, o);
+  else
+    hipLaunchKernelGGL((k_la_scan<CPL, L>), dim3((unsigned)blocks), dim3(256), 0, s, q, kb, v,
+                       decay, T, n, dv, bph, o);
   return mx_launch_status();
 }
 
@@ -341,9 +590,9 @@ int scan_launch(const float* q, const float* kb, const float* v, const float* de
     case 8: return launch_scan<8, 1>(q, kb, v, decay, T, n, dv, o, s);
     case 16: return launch_scan<8, 2>(q, kb, v, decay, T, n, dv, o, s);
     case 32: return launch_scan<8, 4>(q, kb, v, decay, T, n, dv, o, s);
-    case 64: return launch_scan<8, 8>(q, kb, v, decay, T, n, dv, o, s);
-    case 128: return launch_scan<8, 16>(q, kb, v, decay, T, n, dv, o, s);
-    case 256: return launch_scan<8, 32>(q, kb, v, decay, T, n, dv, o, s);
+    case 64: return launch_scan<1, 64>(q, kb, v, decay, T, n, dv, o, s);
+    case 128: return launch_scan<2, 64>(q, kb, v, decay, T, n, dv, o, s);
+    case 256: return launch_scan<4, 64>(q, kb, v, decay, T, n, dv, o, s);
     case 512: return launch_scan<8, 64>(q, kb, v, decay, T, n, dv, o, s);
     default: return MX_ERR_UNSUPPORTED;
   }
@@ -400,6 +649,19 @@ int check_weights(const MxLinearAttnDesc* d, const MxLinearAttnWeights* w) {
   return MX_OK;
 }
 
+// One projection y[T, N] = a[T, K] W^T: hipBLASLt for long inputs (falling back to the
+// expert kernels when the library has no algorithm for the shape), else the single-group
+// down-projection kernels with the table entry of this stage.
+int linear(int st, const MxLinearAttnDesc* d, const LaWork& k, const MxDenseTables& tab,
+           const void* wmat, int T, int N, int K, const void* a, float* y, hipStream_t s) {
+  if (k.blas_ws) {
+    const int rc = mx_gemm_wt(d->weight_dtype, a, wmat, y, T, N, K, k.blas_ws, k.blas_ws_bytes, s);
+    if (rc != MX_ERR_UNSUPPORTED) return rc;
+  }
+  const MxExpertPtrs* entry = k.entries + (st == 1 ? 0 : (st == 2 ? 1 : 2));
+  return mx_dense_linear(d->weight_dtype, 0, entry, tab, T, N, K, a, y, s);
+}
+
 int run_stage(int st, const MxLinearAttnDesc* d, const MxLinearAttnWeights* w, const float* x,
               float* out, int T, const LaWork& k, hipStream_t s) {
   const LaDims m = dims_of(d);
@@ -427,15 +689,22 @@ int run_stage(int st, const MxLinearAttnDesc* d, const MxLinearAttnWeights* w, c
                                s);
     }
     case 1:
-      return mx_dense_linear(wdt, 0, k.entries + 0, tab, T, m.W1, m.H, h, k.v.qkvz, s);
+      return linear(1, d, k, tab, w->qkvz_w, T, m.W1, m.H, h, k.v.qkvz, s);
     case 2:
-      return mx_dense_linear(wdt, 0, k.entries + 1, tab, T, m.W2, m.H, h, k.v.ba, s);
-    case 3:
+      return linear(2, d, k, tab, w->ba_w, T, m.W2, m.H, h, k.v.ba, s);
+    case 3: {
+      const dim3 grid(mx_ceil_div(m.C + m.n, 256), mx_ceil_div(T, LA_TT));
       mx_clear_error();
-      hipLaunchKernelGGL(k_la_prep, dim3(mx_ceil_div(m.C + m.n, 256), T), dim3(256), 0, s,
-                         k.v.qkvz, k.v.ba, w->conv_w, w->a_log, w->dt_bias, d->param_dtype, m,
-                         T, k.v.q, k.v.kb, k.v.v, k.v.decay);
+      if (m.K == 4)
+        hipLaunchKernelGGL(k_la_prep<4>, grid, dim3(256), 0, s, k.v.qkvz, k.v.ba, w->conv_w,
+                           w->a_log, w->dt_bias, d->param_dtype, m, T, k.v.q, k.v.kb, k.v.v,
+                           k.v.decay);
+      else
+        hipLaunchKernelGGL(k_la_prep<0>, grid, dim3(256), 0, s, k.v.qkvz, k.v.ba, w->conv_w,
+                           w->a_log, w->dt_bias, d->param_dtype, m, T, k.v.q, k.v.kb, k.v.v,
+                           k.v.decay);
       return mx_launch_status();
+    }
     case 4:
       return scan_launch(k.v.q, k.v.kb, k.v.v, k.v.decay, T, m.n, m.dk, m.dv, k.v.o, s);
     case 5:
@@ -445,7 +714,7 @@ int run_stage(int st, const MxLinearAttnDesc* d, const MxLinearAttnWeights* w, c
                          f32 ? nullptr : (half_t*)k.v.act);
       return mx_launch_status();
     case 6:
-      return mx_dense_linear(wdt, 0, k.entries + 2, tab, T, m.H, m.vd, k.v.act, k.v.y, s);
+      return linear(6, d, k, tab, w->out_w, T, m.H, m.vd, k.v.act, k.v.y, s);
     case 7: {
       const long n4 = (long)T * m.H / 4;
       mx_clear_error();

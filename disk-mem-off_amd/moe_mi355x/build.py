@@ -35,6 +35,10 @@ HIP_FLAGS = [
 ]
 
 
+# hipBLASLt: the plain dense GEMMs of long linear-attention inputs.
+LINK_LIBS = ["-lhipblaslt"]
+
+
 def _hipcc() -> str:
     path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not Path(path).exists():
@@ -66,7 +70,8 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
         objs = list(pool.map(lambda s: _compile(s, hipcc), srcs))
     tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = [hipcc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objs), "-o", str(tmp)]
+    cmd = [hipcc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objs), *LINK_LIBS,
+           "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")
