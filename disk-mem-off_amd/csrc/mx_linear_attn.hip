@@ -600,6 +600,7 @@ int scan_launch(const float* q, const float* kb, const float* v, const float* de
 
 // Gated output norm: act = (w * (o / rms(o))) * silu(z) per token row (qwen3_next.py:
 // 264-266, rms_norm of _common.py:73-75), written as fp16 (fp32 for fp32 weights).
+template <int RV>
 __global__ __launch_bounds__(256) void k_la_gated_norm(const float* __restrict__ o,
                                                        const float* __restrict__ qkvz,
                                                        const void* __restrict__ norm_w,
@@ -610,21 +611,51 @@ __global__ __launch_bounds__(256) void k_la_gated_norm(const float* __restrict__
   const int t = blockIdx.x;
   const float* orow = o + (size_t)t * m.vd;
   const float* z = qkvz + (size_t)t * m.W1 + 2 * m.qd + m.vd;
-  float ss = 0.f;
-  for (int c = threadIdx.x; c < m.vd; c += 256) ss += orow[c] * orow[c];
   __shared__ float red[4];
-  ss = mx_wave_sum(ss);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
-  __syncthreads();
-  const float tot = (red[0] + red[1]) + (red[2] + red[3]);
-  const float rms = sqrtf(tot / (float)m.vd + eps);
-  for (int c = threadIdx.x; c < m.vd; c += 256) {
-    const float y = mx_load_param(norm_w, pdt, c) * (orow[c] / rms);
-    const float a = y * mx_silu(z[c]);
-    if (act16)
-      act16[(size_t)t * m.vd + c] = (half_t)a;
-    else
-      act32[(size_t)t * m.vd + c] = a;
+  if constexpr (RV > 0) {
+    // The row fits the register tile (vd <= 256 RV): every load is issued up front.
+    float ov[RV], zv[RV], wv[RV];
+#pragma unroll
+    for (int i = 0; i < RV; ++i) {
+      const int c = min((int)threadIdx.x + 256 * i, m.vd - 1);
+      ov[i] = orow[c];
+      zv[i] = z[c];
+      wv[i] = mx_load_param(norm_w, pdt, c);
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < RV; ++i)
+      if ((int)threadIdx.x + 256 * i < m.vd) ss += ov[i] * ov[i];
+    ss = mx_wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+    const float rms = sqrtf(tot / (float)m.vd + eps);
+#pragma unroll
+    for (int i = 0; i < RV; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      if (c >= m.vd) break;
+      const float a = (wv[i] * (ov[i] / rms)) * mx_silu(zv[i]);
+      if (act16)
+        act16[(size_t)t * m.vd + c] = (half_t)a;
+      else
+        act32[(size_t)t * m.vd + c] = a;
+    }
+  } else {
+    float ss = 0.f;
+    for (int c = threadIdx.x; c < m.vd; c += 256) ss += orow[c] * orow[c];
+    ss = mx_wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+    const float rms = sqrtf(tot / (float)m.vd + eps);
+    for (int c = threadIdx.x; c < m.vd; c += 256) {
+      const float a = (mx_load_param(norm_w, pdt, c) * (orow[c] / rms)) * mx_silu(z[c]);
+      if (act16)
+        act16[(size_t)t * m.vd + c] = (half_t)a;
+      else
+        act32[(size_t)t * m.vd + c] = a;
+    }
   }
 }
 
@@ -709,9 +740,18 @@ int run_stage(int st, const MxLinearAttnDesc* d, const MxLinearAttnWeights* w, c
       return scan_launch(k.v.q, k.v.kb, k.v.v, k.v.decay, T, m.n, m.dk, m.dv, k.v.o, s);
     case 5:
       mx_clear_error();
-      hipLaunchKernelGGL(k_la_gated_norm, dim3(T), dim3(256), 0, s, k.v.o, k.v.qkvz,
-                         w->out_norm_w, d->param_dtype, d->eps, m, (float*)k.v.act,
-                         f32 ? nullptr : (half_t*)k.v.act);
+      if (m.vd <= 256 * 4)
+        hipLaunchKernelGGL(k_la_gated_norm<4>, dim3(T), dim3(256), 0, s, k.v.o, k.v.qkvz,
+                           w->out_norm_w, d->param_dtype, d->eps, m, (float*)k.v.act,
+                           f32 ? nullptr : (half_t*)k.v.act);
+      else if (m.vd <= 256 * 16)
+        hipLaunchKernelGGL(k_la_gated_norm<16>, dim3(T), dim3(256), 0, s, k.v.o, k.v.qkvz,
+                           w->out_norm_w, d->param_dtype, d->eps, m, (float*)k.v.act,
+                           f32 ? nullptr : (half_t*)k.v.act);
+      else
+        hipLaunchKernelGGL(k_la_gated_norm<0>, dim3(T), dim3(256), 0, s, k.v.o, k.v.qkvz,
+                           w->out_norm_w, d->param_dtype, d->eps, m, (float*)k.v.act,
+                           f32 ? nullptr : (half_t*)k.v.act);
       return mx_launch_status();
     case 6:
       return linear(6, d, k, tab, w->out_w, T, m.H, m.vd, k.v.act, k.v.y, s);
