@@ -175,3 +175,66 @@ def make_linear_attn_tensors(shape: LinearAttnShape, seed: int, weight_dtype=np.
                 v = v + np.float32(mean)
         out[name] = v.astype(weight_dtype if kind == "weight" else param_dtype)
     return out
+
+
+# ---- Qwen3-Next gated full-attention layers --------------------------------------------
+
+@dataclass(frozen=True)
+class FullAttnShape:
+    """A gated full-attention block (qwen3_next.py:161-205)."""
+
+    hidden: int
+    n_heads: int
+    n_kv_heads: int
+    head_dim: int
+    partial_rotary_factor: float = 0.25
+    rope_theta: float = 5000000.0
+    eps: float = 1e-6
+    qk_norm: bool = True
+
+    @property
+    def rotary_dim(self) -> int:
+        return int(self.head_dim * self.partial_rotary_factor)  # qwen3_next.py:118
+
+    def config(self) -> dict:
+        """The Qwen3-Next config keys of qwen3_next.py:106-118 for this block."""
+        return {"architectures": ["Qwen3NextForCausalLM"], "hidden_size": self.hidden,
+                "rms_norm_eps": self.eps, "num_attention_heads": self.n_heads,
+                "num_key_value_heads": self.n_kv_heads, "head_dim": self.head_dim,
+                "partial_rotary_factor": self.partial_rotary_factor,
+                "rope_theta": self.rope_theta}
+
+
+# Qwen3-Next's full-attention layers: 16 query heads, 2 key/value heads of 256, RoPE on 64.
+QWEN3_NEXT_FULL = FullAttnShape(2048, 16, 2, 256, 0.25, 5000000.0, 1e-6)
+
+
+def full_attn_specs(shape: FullAttnShape) -> list[tuple[str, tuple[int, ...], str, float]]:
+    """(name, shape, kind, std): projections ~ N(0, 0.02), norm weights 1 (+ noise)."""
+    H, nh, nkv, hd = shape.hidden, shape.n_heads, shape.n_kv_heads, shape.head_dim
+    specs = [("input_layernorm.weight", (H,), "norm", 0.0),
+             ("self_attn.q_proj.weight", (2 * nh * hd, H), "weight", 0.02),
+             ("self_attn.k_proj.weight", (nkv * hd, H), "weight", 0.02),
+             ("self_attn.v_proj.weight", (nkv * hd, H), "weight", 0.02),
+             ("self_attn.o_proj.weight", (H, nh * hd), "weight", 0.02)]
+    if shape.qk_norm:
+        specs += [("self_attn.q_norm.weight", (hd,), "norm", 0.0),
+                  ("self_attn.k_norm.weight", (hd,), "norm", 0.0)]
+    return specs
+
+
+def make_full_attn_tensors(shape: FullAttnShape, seed: int, weight_dtype=np.float32,
+                           param_dtype=np.float32, norm_noise: float = 0.0
+                           ) -> dict[str, np.ndarray]:
+    """All tensors of one gated full-attention block: projections in ``weight_dtype``,
+    norm weights in ``param_dtype``."""
+    out = {}
+    for name, shp, kind, std in full_attn_specs(shape):
+        if kind == "norm":
+            v = np.ones(shp, dtype=np.float32)
+            if norm_noise:
+                v = v + gen.normal(seed, stream_of(name), shp, std=norm_noise)
+        else:
+            v = gen.normal(seed, stream_of(name), shp, std=std)
+        out[name] = v.astype(weight_dtype if kind == "weight" else param_dtype)
+    return out
