@@ -1,0 +1,439 @@
+// Qwen3-Next gated full-attention block on the device:
+//   rmsnorm -> q (+gate) / k / v projections -> qk-norm + partial RoPE -> causal attention
+//   (fp32 MFMA, sigmoid gate fused) -> o projection -> residual,
+// i.e. Qwen3NextExecutor._full_attn_block (offload_runtime/executors/qwen3_next.py:161-205)
+// with rope / partial_rope / rms_norm_no_weight / repeat_kv of
+// offload_runtime/executors/_common.py:105-153.  Everything runs on the caller's stream out
+// of the caller's workspace.
+#include <math.h>
+
+#include "mx_common.h"
+#include "mx_internal.h"
+
+namespace {
+
+struct FaDims {
+  int H, nh, nkv, hd, rd;
+  int qw;  // q_proj rows: 2 nh hd ([q | gate] halves)
+  int kw;  // k / v rows: nkv hd
+  int od;  // attention output width: nh hd
+};
+
+FaDims dims_of(const MxFullAttnDesc* d) {
+  FaDims m;
+  m.H = d->hidden;
+  m.nh = d->n_heads;
+  m.nkv = d->n_kv_heads;
+  m.hd = d->head_dim;
+  m.rd = d->rotary_dim;
+  m.qw = 2 * m.nh * m.hd;
+  m.kw = m.nkv * m.hd;
+  m.od = m.nh * m.hd;
+  return m;
+}
+
+int check_desc(const MxFullAttnDesc* d) {
+  if (!d) return MX_ERR_INVALID;
+  if (d->hidden <= 0 || d->n_heads <= 0 || d->n_kv_heads <= 0 || d->head_dim <= 0 ||
+      d->rotary_dim < 0 || d->rotary_dim > d->head_dim || !(d->rope_theta > 0.0))
+    return MX_ERR_INVALID;
+  if (d->n_heads % d->n_kv_heads) return MX_ERR_INVALID;  // repeat_kv needs whole repeats
+  if (d->rotary_dim % 2) return MX_ERR_INVALID;           // rope splits the rotary dims in halves
+  if (d->param_dtype != MX_DT_F32 && d->param_dtype != MX_DT_F16) return MX_ERR_INVALID;
+  if (d->weight_dtype != MX_DT_F32 && d->weight_dtype != MX_DT_F16 && d->weight_dtype != MX_DT_I8)
+    return MX_ERR_INVALID;
+  if (d->head_dim % 4 || d->head_dim > 256) return MX_ERR_UNSUPPORTED;
+  const long qw = 2l * d->n_heads * d->head_dim;
+  if (qw * d->hidden >= (1l << 31)) return MX_ERR_UNSUPPORTED;
+  return MX_OK;
+}
+
+struct Carve {
+  char* base;
+  size_t off = 0;
+  void* take(size_t n) {
+    off = mx_align_up(off, 256);
+    void* p = base ? base + off : nullptr;
+    off += n;
+    return p;
+  }
+};
+
+struct FaWork {
+  MxFullAttnViews v;
+  MxDenseWork dw;  // projections: entry 0 q, 1 k, 2 v, 3 o
+};
+
+int layout(const MxFullAttnDesc* d, int T, void* ws, FaWork* w, size_t* total) {
+  MX_TRY(check_desc(d));
+  if (T < 0) return MX_ERR_INVALID;
+  const size_t Tn = T > 0 ? T : 1;
+  const FaDims m = dims_of(d);
+  const bool f32 = d->weight_dtype == MX_DT_F32;
+  Carve c{(char*)ws};
+  FaWork t;
+  t.v.h32 = (float*)c.take(Tn * m.H * 4);
+  t.v.h16 = f32 ? nullptr : c.take(Tn * m.H * 2);
+  t.v.qg = (float*)c.take(Tn * m.qw * 4);
+  t.v.k = (float*)c.take(Tn * m.kw * 4);
+  t.v.v = (float*)c.take(Tn * m.kw * 4);
+  t.v.act = c.take(Tn * m.od * (f32 ? 4 : 2));
+  t.v.y = (float*)c.take(Tn * m.H * 4);
+  char* dwb = (char*)c.take(mx_dense_work_bytes((int)Tn, d->weight_dtype, 4));
+  mx_dense_work_carve(dwb, (int)Tn, d->weight_dtype, 4, &t.dw);
+  if (w) *w = t;
+  if (total) *total = mx_align_up(c.off, 256);
+  return MX_OK;
+}
+
+// ------------------------------------------------------------------------------------
+// qk-norm + RoPE, in place on the q half of the q projection and on k.  One wave per
+// (token, head row); lane handles dims i = lane + 64 j.  y = (x / rms(x)) * w when the
+// norm weight is given (rms_norm_no_weight then the weight, _common.py:137-140), then on
+// the first rotary_dim dims the rotate-half RoPE of _common.py:105-127: with half =
+// rotary_dim / 2, freq_j = 1 / theta^(j / half) (fp64), angle = fp32(t * freq_j),
+// out_i = y_i cos - y_{i+half} sin (i < half), y_i cos + y_{i-half} sin (half <= i < rd).
+// Each lane recomputes its partner's normalised value from memory (same rms), so there is
+// no cross-lane exchange; all loads precede the reduction, all stores follow it.
+// ------------------------------------------------------------------------------------
+template <int EPT>
+__global__ __launch_bounds__(64) void k_fa_rope(float* __restrict__ qg, float* __restrict__ kk,
+                                                const void* __restrict__ qn_w,
+                                                const void* __restrict__ kn_w, int pdt,
+                                                FaDims m, double theta, float eps) {
+#pragma clang fp contract(off)
+  const int t = blockIdx.x, slot = blockIdx.y, lane = threadIdx.x;
+  const bool isq = slot < m.nh;
+  float* row = isq ? qg + (size_t)t * m.qw + (size_t)slot * m.hd
+                   : kk + (size_t)t * m.kw + (size_t)(slot - m.nh) * m.hd;
+  const void* nw = isq ? qn_w : kn_w;
+  const int half = m.rd / 2;
+  float x[EPT], xp[EPT], w[EPT], wp[EPT];
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int i = lane + 64 * j;
+    const bool valid = i < m.hd;
+    const int ic = valid ? i : 0;
+    const int p = ic < m.rd ? (ic < half ? ic + half : ic - half) : ic;
+    x[j] = valid ? row[ic] : 0.f;
+    xp[j] = valid ? row[p] : 0.f;
+    w[j] = nw ? mx_load_param(nw, pdt, ic) : 1.f;
+    wp[j] = nw ? mx_load_param(nw, pdt, p) : 1.f;
+  }
+  float rms = 1.f;
+  if (nw) {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) ss += x[j] * x[j];
+    ss = mx_wave_sum(ss);
+    rms = sqrtf(ss / (float)m.hd + eps);
+  }
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int i = lane + 64 * j;
+    if (i >= m.hd) break;
+    const float y = nw ? (x[j] / rms) * w[j] : x[j];
+    float out = y;
+    if (i < m.rd) {
+      const float yp = nw ? (xp[j] / rms) * wp[j] : xp[j];
+      const int jj = i < half ? i : i - half;
+      const double f = 1.0 / pow(theta, (double)jj / (double)half);
+      const float ang = (float)((double)t * f);
+      const float c = cosf(ang), s = sinf(ang);
+      out = i < half ? y * c - yp * s : y * c + yp * s;
+    }
+    row[i] = out;
+  }
+}
+
+// ------------------------------------------------------------------------------------
+// Causal attention on fp32 MFMA (v_mfma_f32_16x16x4_f32), flash-style.  Block = 4 waves,
+// one query head h, 64 queries (16 per wave); key tiles of 16 keys of the head's key/value
+// head (h / (n_heads / n_kv_heads), repeat_kv) staged in LDS: K row-major, V transposed.
+// Per tile each wave computes S^T = K Q^T (16 keys x 16 queries: lane l holds
+// S^T[4 (l / 16) + r][l % 16], so query l % 16 is lane-local) with Q held in registers, then
+// the online softmax per query (running max / sum; scores are (q.k) / sqrt(head_dim) with
+// keys after the query masked, qwen3_next.py:191-194), and O^T += V^T P, whose B operand is
+// exactly the lane's probabilities (the MFMA k-slot of lane l at step r is key 4 (l/16) + r,
+// the same key on both operands).  O^T keeps the query in the lane too, so the softmax
+// rescale needs no shuffle.  The epilogue divides by the row sum and multiplies by
+// sigmoid(gate) (qwen3_next.py:201-202), writing the o_proj input.  Head dims are padded to
+// a multiple of 16 with zeros.
+// ------------------------------------------------------------------------------------
+template <int NC>
+__global__ __launch_bounds__(256) void k_fa_attn(const float* __restrict__ qg,
+                                                 const float* __restrict__ kk,
+                                                 const float* __restrict__ vv, FaDims m, int T,
+                                                 float sqrt_hd, float* __restrict__ act32,
+                                                 half_t* __restrict__ act16) {
+  constexpr int DP = NC * 16;  // padded head dim
+  constexpr int KT = 16;       // keys per tile
+  constexpr int KS = DP + 4;   // LDS row stride of the K tile (floats)
+  constexpr int VS = KT + 4;   // LDS row stride of the transposed V tile
+  constexpr int NP = KT * DP / 4;  // float4 pieces of K (and of V) per tile
+  __shared__ __align__(16) float sk[KT * KS];
+  __shared__ __align__(16) float svt[DP * VS];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = blockIdx.y;
+  const int q0 = (gridDim.x - 1 - blockIdx.x) * 64;  // longest query blocks first
+  const int qw0 = q0 + wave * 16;
+  const int kvh = h / (m.nh / m.nkv);
+  const int ql = lane & 15, g = lane >> 4;
+  const int qi = qw0 + ql;
+  const int qc = min(qi, T - 1);
+
+  // Q fragment (B operand of S^T): qf[c] = Q[qi][16 c + 4 g .. + 3].
+  float4 qf[NC];
+  const float* qrow = qg + (size_t)qc * m.qw + (size_t)h * m.hd;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int d = 16 * c + 4 * g;
+    qf[c] = d < m.hd ? *(const float4*)(qrow + d) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  float4_t oacc[NC];
+#pragma unroll
+  for (int f = 0; f < NC; ++f) oacc[f] = (float4_t){0.f, 0.f, 0.f, 0.f};
+  float mrun = -INFINITY, lrun = 0.f;
+
+  const int kend = min(T, q0 + 64);
+  const int ntile = (kend + KT - 1) / KT;
+  const int wq_last = min(qw0 + 15, T - 1);  // last real query of this wave
+  const float* kbase = kk + (size_t)kvh * m.hd;
+  const float* vbase = vv + (size_t)kvh * m.hd;
+
+  for (int kt = 0; kt < ntile; ++kt) {
+    const int k0 = kt * KT;
+    __syncthreads();  // the previous tile's LDS reads are done
+    for (int p = tid; p < NP; p += 256) {
+      const int key = p / (DP / 4), d4 = (p % (DP / 4)) * 4;
+      const int s = k0 + key;
+      float4 k4 = make_float4(0.f, 0.f, 0.f, 0.f), v4 = k4;
+      if (s < T && d4 < m.hd) {
+        k4 = *(const float4*)(kbase + (size_t)s * m.kw + d4);
+        v4 = *(const float4*)(vbase + (size_t)s * m.kw + d4);
+      }
+      *(float4*)(sk + key * KS + d4) = k4;
+      svt[(d4 + 0) * VS + key] = v4.x;
+      svt[(d4 + 1) * VS + key] = v4.y;
+      svt[(d4 + 2) * VS + key] = v4.z;
+      svt[(d4 + 3) * VS + key] = v4.w;
+    }
+    __syncthreads();
+    if (k0 > wq_last) continue;  // every key of the tile is after every query of the wave
+
+    float4_t st = (float4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const float4 a = *(const float4*)(sk + ql * KS + 16 * c + 4 * g);
+      st = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, qf[c].x, st, 0, 0, 0);
+      st = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, qf[c].y, st, 0, 0, 0);
+      st = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, qf[c].z, st, 0, 0, 0);
+      st = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, qf[c].w, st, 0, 0, 0);
+    }
+    float sv[4];
+    float mt = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int key = k0 + 4 * g + r;
+      const bool masked = key > qi || key >= T;
+      sv[r] = masked ? -INFINITY : st[r] / sqrt_hd;
+      mt = fmaxf(mt, sv[r]);
+    }
+    mt = fmaxf(mt, __shfl_xor(mt, 16));
+    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    const float mnew = fmaxf(mrun, mt);
+    const float alpha = expf(mrun - mnew);  // 0 on the first tile (mrun = -inf)
+    float p[4];
+    float ps = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      p[r] = expf(sv[r] - mnew);
+      ps += p[r];
+    }
+    lrun = lrun * alpha + ps;
+    mrun = mnew;
+#pragma unroll
+    for (int f = 0; f < NC; ++f) {
+      oacc[f] *= alpha;
+      const float4 a = *(const float4*)(svt + (16 * f + ql) * VS + 4 * g);
+      oacc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, p[0], oacc[f], 0, 0, 0);
+      oacc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, p[1], oacc[f], 0, 0, 0);
+      oacc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, p[2], oacc[f], 0, 0, 0);
+      oacc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, p[3], oacc[f], 0, 0, 0);
+    }
+  }
+  float l = lrun + __shfl_xor(lrun, 16);
+  l = l + __shfl_xor(l, 32);
+  if (qi >= T) return;
+  const float* gate = qg + (size_t)qi * m.qw + (size_t)m.od + (size_t)h * m.hd;
+  const size_t orow = (size_t)qi * m.od + (size_t)h * m.hd;
+#pragma unroll
+  for (int f = 0; f < NC; ++f) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int d = 16 * f + 4 * g + r;
+      if (d < m.hd) {
+        const float a = (oacc[f][r] / l) * mx_sigmoid(gate[d]);
+        if (act16)
+          act16[orow + d] = (half_t)a;
+        else
+          act32[orow + d] = a;
+      }
+    }
+  }
+}
+
+template <int NC>
+int launch_attn(const float* qg, const float* kk, const float* vv, const FaDims& m, int T,
+                void* act, bool f16, hipStream_t s) {
+  const dim3 grid(mx_ceil_div(T, 64), m.nh);
+  const float sqrt_hd = (float)sqrt((double)m.hd);
+  mx_clear_error();
+  hipLaunchKernelGGL((k_fa_attn<NC>), grid, dim3(256), 0, s, qg, kk, vv, m, T, sqrt_hd,
+                     f16 ? nullptr : (float*)act, f16 ? (half_t*)act : nullptr);
+  return mx_launch_status();
+}
+
+int attn_launch(const float* qg, const float* kk, const float* vv, const FaDims& m, int T,
+                void* act, bool f16, hipStream_t s) {
+  if (m.hd <= 16) return launch_attn<1>(qg, kk, vv, m, T, act, f16, s);
+  if (m.hd <= 32) return launch_attn<2>(qg, kk, vv, m, T, act, f16, s);
+  if (m.hd <= 64) return launch_attn<4>(qg, kk, vv, m, T, act, f16, s);
+  if (m.hd <= 128) return launch_attn<8>(qg, kk, vv, m, T, act, f16, s);
+  if (m.hd <= 256) return launch_attn<16>(qg, kk, vv, m, T, act, f16, s);
+  return MX_ERR_UNSUPPORTED;
+}
+
+__global__ __launch_bounds__(256) void k_fa_residual(const float* __restrict__ x,
+                                                     const float* __restrict__ y, long n4,
+                                                     float* __restrict__ out) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i < n4) {
+    const float4 a = ((const float4*)x)[i], b = ((const float4*)y)[i];
+    ((float4*)out)[i] = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+  }
+}
+
+int check_weights(const MxFullAttnDesc* d, const MxFullAttnWeights* w) {
+  if (!w || !w->norm_w || !w->q_w || !w->k_w || !w->v_w || !w->o_w) return MX_ERR_INVALID;
+  if (d->weight_dtype == MX_DT_I8 && (!w->q_scale || !w->k_scale || !w->v_scale || !w->o_scale))
+    return MX_ERR_INVALID;
+  if (!mx_aligned16(w->q_w) || !mx_aligned16(w->k_w) || !mx_aligned16(w->v_w) ||
+      !mx_aligned16(w->o_w))
+    return MX_ERR_ALIGNMENT;
+  return MX_OK;
+}
+
+int run_stage(int st, const MxFullAttnDesc* d, const MxFullAttnWeights* w, const float* x,
+              float* out, int T, const FaWork& k, hipStream_t s) {
+  const FaDims m = dims_of(d);
+  const int wdt = d->weight_dtype;
+  const bool f32 = wdt == MX_DT_F32;
+  const void* h = f32 ? (const void*)k.v.h32 : k.v.h16;
+  switch (st) {
+    case 0: {
+      MxDenseEntries e = {};
+      e.e[0].down = w->q_w;
+      e.e[0].down_scale = w->q_scale;
+      e.e[1].down = w->k_w;
+      e.e[1].down_scale = w->k_scale;
+      e.e[2].down = w->v_w;
+      e.e[2].down_scale = w->v_scale;
+      e.e[3].down = w->o_w;
+      e.e[3].down_scale = w->o_scale;
+      MX_TRY(mx_dense_setup(k.dw, e, T, s));
+      return mx_rmsnorm_launch(x, w->norm_w, d->param_dtype, d->eps, T, m.H, k.v.h32, k.v.h16,
+                               s);
+    }
+    case 1:
+      return mx_project(k.dw, 0, wdt, w->q_w, T, m.qw, m.H, h, k.v.qg, s);
+    case 2:
+      return mx_project(k.dw, 1, wdt, w->k_w, T, m.kw, m.H, h, k.v.k, s);
+    case 3:
+      return mx_project(k.dw, 2, wdt, w->v_w, T, m.kw, m.H, h, k.v.v, s);
+    case 4: {
+      const dim3 grid(T, m.nh + m.nkv);
+      mx_clear_error();
+      if (m.hd <= 64)
+        hipLaunchKernelGGL(k_fa_rope<1>, grid, dim3(64), 0, s, k.v.qg, k.v.k, w->q_norm_w,
+                           w->k_norm_w, d->param_dtype, m, d->rope_theta, d->eps);
+      else if (m.hd <= 128)
+        hipLaunchKernelGGL(k_fa_rope<2>, grid, dim3(64), 0, s, k.v.qg, k.v.k, w->q_norm_w,
+                           w->k_norm_w, d->param_dtype, m, d->rope_theta, d->eps);
+      else
+        hipLaunchKernelGGL(k_fa_rope<4>, grid, dim3(64), 0, s, k.v.qg, k.v.k, w->q_norm_w,
+                           w->k_norm_w, d->param_dtype, m, d->rope_theta, d->eps);
+      return mx_launch_status();
+    }
+    case 5:
+      return attn_launch(k.v.qg, k.v.k, k.v.v, m, T, k.v.act, !f32, s);
+    case 6:
+      return mx_project(k.dw, 3, wdt, w->o_w, T, m.H, m.od, k.v.act, k.v.y, s);
+    case 7: {
+      const long n4 = (long)T * m.H / 4;
+      mx_clear_error();
+      hipLaunchKernelGGL(k_fa_residual, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, x,
+                         k.v.y, n4, out);
+      return mx_launch_status();
+    }
+    default:
+      return MX_ERR_INVALID;
+  }
+}
+
+int forward(const MxFullAttnDesc* d, const MxFullAttnWeights* w, const float* x, float* out,
+            int T, void* ws, size_t ws_bytes, hipStream_t s, void* const* events) {
+  MX_TRY(check_desc(d));
+  MX_TRY(check_weights(d, w));
+  if (!x || !out || !ws || T < 0) return MX_ERR_INVALID;
+  if (d->hidden % 4) return MX_ERR_UNSUPPORTED;  // float4 residual
+  if (!mx_aligned16(x) || !mx_aligned16(out)) return MX_ERR_ALIGNMENT;
+  if (T == 0) return MX_OK;
+  FaWork k;
+  size_t need = 0;
+  MX_TRY(layout(d, T, ws, &k, &need));
+  if (ws_bytes < need) return MX_ERR_WORKSPACE;
+  for (int st = 0; st < MX_FA_N_STAGES; ++st) {
+    if (events) MX_TRY(mx_status(hipEventRecord((hipEvent_t)events[st], s)));
+    MX_TRY(run_stage(st, d, w, x, out, T, k, s));
+  }
+  if (events) MX_TRY(mx_status(hipEventRecord((hipEvent_t)events[MX_FA_N_STAGES], s)));
+  return MX_OK;
+}
+
+}  // namespace
+
+extern "C" int mx_full_attn_workspace_size(const MxFullAttnDesc* desc, int32_t tokens,
+                                           size_t* nbytes) {
+  if (!nbytes) return MX_ERR_INVALID;
+  return layout(desc, tokens, nullptr, nullptr, nbytes);
+}
+
+extern "C" int mx_full_attn_views(const MxFullAttnDesc* desc, int32_t tokens, void* workspace,
+                                  MxFullAttnViews* views) {
+  if (!workspace || !views) return MX_ERR_INVALID;
+  FaWork k;
+  MX_TRY(layout(desc, tokens, workspace, &k, nullptr));
+  *views = k.v;
+  return MX_OK;
+}
+
+extern "C" int mx_full_attn_forward(const MxFullAttnDesc* desc, const MxFullAttnWeights* weights,
+                                    const float* x, float* out, int32_t tokens, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
+  return forward(desc, weights, x, out, tokens, workspace, workspace_bytes, (hipStream_t)stream,
+                 nullptr);
+}
+
+extern "C" int mx_full_attn_forward_profiled(const MxFullAttnDesc* desc,
+                                             const MxFullAttnWeights* weights, const float* x,
+                                             float* out, int32_t tokens, void* workspace,
+                                             size_t workspace_bytes, void* stream,
+                                             void* const* events, int32_t n_events) {
+  if (!events || n_events != MX_FA_N_STAGES + 1) return MX_ERR_INVALID;
+  for (int i = 0; i < n_events; ++i)
+    if (!events[i]) return MX_ERR_INVALID;
+  return forward(desc, weights, x, out, tokens, workspace, workspace_bytes, (hipStream_t)stream,
+                 events);
+}

@@ -52,3 +52,29 @@ int mx_dense_linear(int wdt, int tiled, const MxExpertPtrs* entry, const MxDense
 size_t mx_gemm_workspace_bytes();
 int mx_gemm_wt(int dtype, const void* a, const void* w, float* y, int T, int N, int K, void* ws,
                size_t ws_bytes, hipStream_t s);
+
+// Workspace pieces of the dense projections of an attention block (device pointers):
+// expert-table entries (one per projection), single-group m-tile tables, ones[T] and, for
+// long inputs with fp16 / fp32 weights, the hipBLASLt workspace.
+#define MX_DENSE_BLAS_MIN_TOKENS 65
+#define MX_DENSE_MAX_ENT 4
+struct MxDenseEntries {
+  MxExpertPtrs e[MX_DENSE_MAX_ENT];  // e[i].down / down_scale = projection i's weights
+};
+struct MxDenseWork {
+  MxExpertPtrs* entries;
+  int* tabs;  // g_expert, g_start, g_count, n_mtiles
+  int* mt_group;
+  int* mt_row0;
+  float* ones;
+  void* blas_ws;
+  size_t blas_ws_bytes;
+  int m_blk, n_mt, n_ent;
+};
+size_t mx_dense_work_bytes(int T, int weight_dtype, int n_ent);
+void mx_dense_work_carve(char* base, int T, int weight_dtype, int n_ent, MxDenseWork* w);
+// Writes the table entries and m-tile tables (one small launch per block call).
+int mx_dense_setup(const MxDenseWork& w, const MxDenseEntries& ents, int T, hipStream_t s);
+// y[T, N] = a[T, K] W^T with W = projection `ent` (wmat, its weights, for the library path).
+int mx_project(const MxDenseWork& w, int ent, int wdt, const void* wmat, int T, int N, int K,
+               const void* a, float* y, hipStream_t s);

@@ -63,24 +63,9 @@ struct Carve {
   }
 };
 
-// Inputs longer than this run the projections on hipBLASLt (fp16 / fp32 weights); shorter
-// ones, and int8 weights, on the HBM-streaming expert kernels.
-#define LA_BLAS_MIN_TOKENS 65
-
-bool use_blas(const MxLinearAttnDesc* d, int T) {
-  return T >= LA_BLAS_MIN_TOKENS && d->weight_dtype != MX_DT_I8;
-}
-
 struct LaWork {
   MxLinearAttnViews v;
-  void* blas_ws;          // hipBLASLt workspace (long inputs), else NULL
-  size_t blas_ws_bytes;
-  MxExpertPtrs* entries;  // [3]: qkvz, ba, out
-  int* tabs;              // g_expert, g_start, g_count, n_mtiles (4 ints)
-  int* mt_group;
-  int* mt_row0;
-  float* ones;
-  int m_blk, n_mt;
+  MxDenseWork dw;  // projections: entry 0 qkvz, 1 ba, 2 out
 };
 
 int layout(const MxLinearAttnDesc* d, int T, void* ws, LaWork* w, size_t* total) {
@@ -89,8 +74,6 @@ int layout(const MxLinearAttnDesc* d, int T, void* ws, LaWork* w, size_t* total)
   const size_t Tn = T > 0 ? T : 1;
   const LaDims m = dims_of(d);
   const bool f32 = d->weight_dtype == MX_DT_F32;
-  const int m_blk = mx_m_blk_for((int)Tn, d->weight_dtype);
-  const int n_mt = mx_ceil_div((int)Tn, m_blk);
   Carve c{(char*)ws};
   LaWork t;
   t.v.h32 = (float*)c.take(Tn * m.H * 4);
@@ -104,15 +87,8 @@ int layout(const MxLinearAttnDesc* d, int T, void* ws, LaWork* w, size_t* total)
   t.v.o = (float*)c.take(Tn * m.vd * 4);
   t.v.act = c.take(Tn * m.vd * (f32 ? 4 : 2));
   t.v.y = (float*)c.take(Tn * m.H * 4);
-  t.entries = (MxExpertPtrs*)c.take(3 * sizeof(MxExpertPtrs));
-  t.tabs = (int*)c.take(4 * 4);
-  t.mt_group = (int*)c.take((size_t)n_mt * 4);
-  t.mt_row0 = (int*)c.take((size_t)n_mt * 4);
-  t.ones = (float*)c.take(Tn * 4);
-  t.blas_ws_bytes = use_blas(d, (int)Tn) ? mx_gemm_workspace_bytes() : 0;
-  t.blas_ws = t.blas_ws_bytes ? c.take(t.blas_ws_bytes) : nullptr;
-  t.m_blk = m_blk;
-  t.n_mt = n_mt;
+  char* dwb = (char*)c.take(mx_dense_work_bytes((int)Tn, d->weight_dtype, 3));
+  mx_dense_work_carve(dwb, (int)Tn, d->weight_dtype, 3, &t.dw);
   if (w) *w = t;
   if (total) *total = mx_align_up(c.off, 256);
   return MX_OK;
@@ -121,31 +97,6 @@ int layout(const MxLinearAttnDesc* d, int T, void* ws, LaWork* w, size_t* total)
 // ------------------------------------------------------------------------------------
 // Kernels.
 // ------------------------------------------------------------------------------------
-
-// Expert-table entries of the three projections and the single-group m-tile tables.
-__global__ __launch_bounds__(256) void k_la_setup(int T, int m_blk, int n_mt,
-                                                  MxExpertPtrs* __restrict__ entries,
-                                                  MxExpertPtrs e0, MxExpertPtrs e1,
-                                                  MxExpertPtrs e2, int* __restrict__ tabs,
-                                                  int* __restrict__ mt_group,
-                                                  int* __restrict__ mt_row0,
-                                                  float* __restrict__ ones) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i == 0) {
-    entries[0] = e0;
-    entries[1] = e1;
-    entries[2] = e2;
-    tabs[0] = 0;  // g_expert
-    tabs[1] = 0;  // g_start
-    tabs[2] = T;  // g_count
-    tabs[3] = n_mt;
-  }
-  if (i < n_mt) {
-    mt_group[i] = 0;
-    mt_row0[i] = i * m_blk;
-  }
-  if (i < T) ones[i] = 1.f;
-}
 
 // Causal depthwise conv + SiLU on the q/k/v channels, beta * k, and the per-head decay.
 // Grid (ceil((C + n) / 256), ceil(T / LA_TT)); a thread walks LA_TT consecutive tokens of
@@ -680,49 +631,29 @@ int check_weights(const MxLinearAttnDesc* d, const MxLinearAttnWeights* w) {
   return MX_OK;
 }
 
-// One projection y[T, N] = a[T, K] W^T: hipBLASLt for long inputs (falling back to the
-// expert kernels when the library has no algorithm for the shape), else the single-group
-// down-projection kernels with the table entry of this stage.
-int linear(int st, const MxLinearAttnDesc* d, const LaWork& k, const MxDenseTables& tab,
-           const void* wmat, int T, int N, int K, const void* a, float* y, hipStream_t s) {
-  if (k.blas_ws) {
-    const int rc = mx_gemm_wt(d->weight_dtype, a, wmat, y, T, N, K, k.blas_ws, k.blas_ws_bytes, s);
-    if (rc != MX_ERR_UNSUPPORTED) return rc;
-  }
-  const MxExpertPtrs* entry = k.entries + (st == 1 ? 0 : (st == 2 ? 1 : 2));
-  return mx_dense_linear(d->weight_dtype, 0, entry, tab, T, N, K, a, y, s);
-}
-
 int run_stage(int st, const MxLinearAttnDesc* d, const MxLinearAttnWeights* w, const float* x,
               float* out, int T, const LaWork& k, hipStream_t s) {
   const LaDims m = dims_of(d);
   const int wdt = d->weight_dtype;
   const bool f32 = wdt == MX_DT_F32;
-  MxDenseTables tab{k.tabs + 0, k.tabs + 1, k.tabs + 2, k.mt_group, k.mt_row0, k.tabs + 3,
-                    k.ones, k.m_blk};
   const void* h = f32 ? (const void*)k.v.h32 : k.v.h16;
   switch (st) {
     case 0: {
-      MxExpertPtrs e[3] = {};
-      e[0].down = w->qkvz_w;
-      e[0].down_scale = w->qkvz_scale;
-      e[1].down = w->ba_w;
-      e[1].down_scale = w->ba_scale;
-      e[2].down = w->out_w;
-      e[2].down_scale = w->out_scale;
-      const int nth = T > k.n_mt ? T : k.n_mt;
-      mx_clear_error();
-      hipLaunchKernelGGL(k_la_setup, dim3(mx_ceil_div(nth, 256)), dim3(256), 0, s, T, k.m_blk,
-                         k.n_mt, k.entries, e[0], e[1], e[2], k.tabs, k.mt_group, k.mt_row0,
-                         k.ones);
-      MX_TRY(mx_launch_status());
+      MxDenseEntries e = {};
+      e.e[0].down = w->qkvz_w;
+      e.e[0].down_scale = w->qkvz_scale;
+      e.e[1].down = w->ba_w;
+      e.e[1].down_scale = w->ba_scale;
+      e.e[2].down = w->out_w;
+      e.e[2].down_scale = w->out_scale;
+      MX_TRY(mx_dense_setup(k.dw, e, T, s));
       return mx_rmsnorm_launch(x, w->norm_w, d->param_dtype, d->eps, T, m.H, k.v.h32, k.v.h16,
                                s);
     }
     case 1:
-      return linear(1, d, k, tab, w->qkvz_w, T, m.W1, m.H, h, k.v.qkvz, s);
+      return mx_project(k.dw, 0, wdt, w->qkvz_w, T, m.W1, m.H, h, k.v.qkvz, s);
     case 2:
-      return linear(2, d, k, tab, w->ba_w, T, m.W2, m.H, h, k.v.ba, s);
+      return mx_project(k.dw, 1, wdt, w->ba_w, T, m.W2, m.H, h, k.v.ba, s);
     case 3: {
       const dim3 grid(mx_ceil_div(m.C + m.n, 256), mx_ceil_div(T, LA_TT));
       mx_clear_error();
@@ -754,7 +685,7 @@ int run_stage(int st, const MxLinearAttnDesc* d, const MxLinearAttnWeights* w, c
                            f32 ? nullptr : (half_t*)k.v.act);
       return mx_launch_status();
     case 6:
-      return linear(6, d, k, tab, w->out_w, T, m.H, m.vd, k.v.act, k.v.y, s);
+      return mx_project(k.dw, 2, wdt, w->out_w, T, m.H, m.vd, k.v.act, k.v.y, s);
     case 7: {
       const long n4 = (long)T * m.H / 4;
       mx_clear_error();

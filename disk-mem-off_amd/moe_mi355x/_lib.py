@@ -100,6 +100,29 @@ class MxLinearAttnViews(ctypes.Structure):
                 ("o", c_void_p), ("act", c_void_p), ("y", c_void_p)]
 
 
+MX_FA_N_STAGES = 8
+FA_STAGE_NAMES = ("rmsnorm", "q_proj", "k_proj", "v_proj", "qk_rope", "attention", "o_proj",
+                  "residual")
+
+
+class MxFullAttnDesc(ctypes.Structure):
+    _fields_ = [("hidden", c_int32), ("n_heads", c_int32), ("n_kv_heads", c_int32),
+                ("head_dim", c_int32), ("rotary_dim", c_int32), ("weight_dtype", c_int32),
+                ("param_dtype", c_int32), ("rope_theta", ctypes.c_double), ("eps", c_float)]
+
+
+class MxFullAttnWeights(ctypes.Structure):
+    _fields_ = [("norm_w", c_void_p), ("q_w", c_void_p), ("q_scale", c_void_p),
+                ("k_w", c_void_p), ("k_scale", c_void_p), ("v_w", c_void_p),
+                ("v_scale", c_void_p), ("o_w", c_void_p), ("o_scale", c_void_p),
+                ("q_norm_w", c_void_p), ("k_norm_w", c_void_p)]
+
+
+class MxFullAttnViews(ctypes.Structure):
+    _fields_ = [("h32", c_void_p), ("h16", c_void_p), ("qg", c_void_p), ("k", c_void_p),
+                ("v", c_void_p), ("act", c_void_p), ("y", c_void_p)]
+
+
 class MxDeviceInfo(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char * 256), ("arch", ctypes.c_char * 64),
                 ("cu_count", c_int32), ("clock_khz", c_int32), ("mem_clock_khz", c_int32),
@@ -178,6 +201,14 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                                        P(MxLinearAttnWeights), c_void_p,
                                                        c_void_p, c_int32, c_void_p, c_size_t,
                                                        c_void_p, P(c_void_p), c_int32]),
+    "mx_full_attn_workspace_size": (ctypes.c_int, [P(MxFullAttnDesc), c_int32, P(c_size_t)]),
+    "mx_full_attn_views": (ctypes.c_int, [P(MxFullAttnDesc), c_int32, c_void_p,
+                                          P(MxFullAttnViews)]),
+    "mx_full_attn_forward": (ctypes.c_int, [P(MxFullAttnDesc), P(MxFullAttnWeights), c_void_p,
+                                            c_void_p, c_int32, c_void_p, c_size_t, c_void_p]),
+    "mx_full_attn_forward_profiled": (ctypes.c_int, [P(MxFullAttnDesc), P(MxFullAttnWeights),
+                                                     c_void_p, c_void_p, c_int32, c_void_p,
+                                                     c_size_t, c_void_p, P(c_void_p), c_int32]),
     "mx_gated_delta_scan": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32,
                                            c_int32, c_int32, c_int32, c_void_p, c_void_p]),
 }

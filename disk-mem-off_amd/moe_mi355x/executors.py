@@ -26,6 +26,7 @@ import numpy as np
 
 from . import _lib
 from .layout import NORM, MoeLayerLayout
+from .full_attn import FullAttnLayout, FullAttnRunner, has_full_attn
 from .linear_attn import LinearAttnLayout, LinearAttnRunner, has_linear_attn
 from .moe import MoeConfig, MoeRunner
 from .types import DeviceBuffer, HostBuffer, LayerSpec
@@ -116,6 +117,8 @@ class _MoeExecutorBase:
         self._layouts: dict[int, tuple[list, MoeLayerLayout]] = {}
         self._la_runner: LinearAttnRunner | None = None
         self._la_layouts: dict[int, tuple[list, LinearAttnLayout]] = {}
+        self._fa_runner: FullAttnRunner | None = None
+        self._fa_layouts: dict[int, tuple[list, FullAttnLayout]] = {}
 
     # values supplied by subclasses
     top_k: int
@@ -239,6 +242,9 @@ class _MoeExecutorBase:
         if self._la_runner is not None:
             self._la_runner.close()
             self._la_runner = None
+        if self._fa_runner is not None:
+            self._fa_runner.close()
+            self._fa_runner = None
 
 
 class GLM4MoeExecutor(_MoeExecutorBase):
@@ -263,9 +269,10 @@ class Qwen3NextExecutor(_MoeExecutorBase):
     """Qwen3-Next (Qwen3NextForCausalLM): softmax router, renormalised top-k, no scaling,
     shared expert scaled by sigmoid(h . shared_expert_gate).
 
-    Linear-attention layers (``metadata["attn_type"]`` "linear", the default as in
-    qwen3_next.py:155) run their Gated DeltaNet block on the device ahead of the MoE
-    block, on the same uploaded activations; full-attention layers need ``attention=``."""
+    Both attention kinds run on the device ahead of the MoE block, on the same uploaded
+    activations: linear-attention layers (``metadata["attn_type"]`` "linear", the default as
+    in qwen3_next.py:155) their Gated DeltaNet block, full-attention layers ("full") their
+    gated softmax attention (qwen3_next.py:161-205)."""
 
     _router_default = _lib.MX_ROUTER_SOFTMAX
 
@@ -278,6 +285,14 @@ class Qwen3NextExecutor(_MoeExecutorBase):
         self.linear_num_value_heads = int(config.get("linear_num_value_heads", 32))
         self.linear_value_head_dim = int(config.get("linear_value_head_dim", 128))
         self.linear_conv_kernel_dim = int(config.get("linear_conv_kernel_dim", 4))
+        # qwen3_next.py:109-118 (num_attention_heads is required there for full layers)
+        heads = config.get("num_attention_heads")
+        self.num_heads = int(heads) if heads is not None else None
+        self.num_kv_heads = int(config.get("num_key_value_heads", heads or 1))
+        self.head_dim = int(config.get("head_dim", self.hidden_size // (self.num_heads or 1)))
+        self.partial_rotary_factor = float(config.get("partial_rotary_factor", 0.25))
+        self.rotary_dim = int(self.head_dim * self.partial_rotary_factor)
+        self.rope_theta = float(config.get("rope_theta", 5000000.0))
         self.num_experts = int(config.get("num_experts", config.get("n_routed_experts", 512)))
         self.top_k = int(config.get("num_experts_per_tok", 10))
         self.norm_topk_prob = bool(config.get("norm_topk_prob", True))
@@ -305,10 +320,25 @@ class Qwen3NextExecutor(_MoeExecutorBase):
         self._la_layouts[layer.layer_id] = (meta, lay)
         return lay
 
+    def full_attn_layout(self, layer: LayerSpec) -> FullAttnLayout:
+        meta = layer.metadata["tensors"]
+        hit = self._fa_layouts.get(layer.layer_id)
+        if hit is not None and hit[0] is meta:
+            return hit[1]
+        if self.num_heads is None:
+            raise ValueError("full-attention layers need num_attention_heads in the config")
+        lay = FullAttnLayout.from_meta(meta, self.num_heads, self.num_kv_heads, self.head_dim,
+                                       self.rotary_dim, self.rope_theta)
+        self._fa_layouts[layer.layer_id] = (meta, lay)
+        return lay
+
     def _device_attention(self, layer: LayerSpec, device_weights: DeviceBuffer, backend: Any,
                           stream: Any) -> Callable[[int, int], None] | None:
-        if layer.metadata.get("attn_type", "linear") != "linear" or \
-                not has_linear_attn(layer.metadata["tensors"]):
+        kind = layer.metadata.get("attn_type", "linear")
+        meta = layer.metadata["tensors"]
+        if kind == "full" and has_full_attn(meta):
+            return self._device_full_attention(layer, device_weights, backend, stream)
+        if kind != "linear" or not has_linear_attn(meta):
             return None
         if device_weights.backend != "rocm":
             raise RuntimeError("the linear-attention block needs the MI355X backend; got "
@@ -319,6 +349,24 @@ class Qwen3NextExecutor(_MoeExecutorBase):
         if self._la_runner is None:
             self._la_runner = LinearAttnRunner(backend)
         runner = self._la_runner
+
+        def pre(x_dev: int, tokens: int) -> None:
+            runner.reserve(desc, max(tokens, self.max_tokens, 1), io=False)
+            runner.forward_device(desc, weights, x_dev, x_dev, tokens, stream)
+
+        return pre
+
+    def _device_full_attention(self, layer: LayerSpec, device_weights: DeviceBuffer,
+                               backend: Any, stream: Any) -> Callable[[int, int], None]:
+        if device_weights.backend != "rocm":
+            raise RuntimeError("the attention block needs the MI355X backend; got "
+                               f"{device_weights.backend!r} device buffers")
+        lay = self.full_attn_layout(layer)
+        desc = lay.desc(self.rms_norm_eps)
+        weights = lay.weights(int(device_weights.handle))
+        if self._fa_runner is None:
+            self._fa_runner = FullAttnRunner(backend)
+        runner = self._fa_runner
 
         def pre(x_dev: int, tokens: int) -> None:
             runner.reserve(desc, max(tokens, self.max_tokens, 1), io=False)

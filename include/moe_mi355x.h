@@ -359,6 +359,68 @@ int mx_linear_attn_forward_profiled(const MxLinearAttnDesc* desc,
                                     float* out, int32_t tokens, void* workspace,
                                     size_t workspace_bytes, void* stream, void* const* events,
                                     int32_t n_events);
+/* =================================================================================== *
+ * Qwen3-Next gated full-attention block: Qwen3NextExecutor._full_attn_block
+ * (offload_runtime/executors/qwen3_next.py:161-205) with rope / partial_rope /
+ * rms_norm_no_weight / repeat_kv (offload_runtime/executors/_common.py:105-153):
+ *   h = rms_norm(x);  [q | gate] = h W_q^T (halves);  k = h W_k^T;  v = h W_v^T
+ *   per head: q = rms_norm_no_weight(q) * q_norm (if given), k likewise; rotate-half RoPE
+ *   on the first rotary_dim dims at positions 0 .. T-1
+ *   attn = softmax((q k^T) / sqrt(head_dim) + causal mask) v   (k, v heads repeated)
+ *   out = x + (attn * sigmoid(gate)) W_o^T
+ * Attention runs in fp32 (MFMA 16x16x4 f32).  No KV cache: every call attends over its
+ * own T tokens, as in the reference.
+ * =================================================================================== */
+typedef struct MxFullAttnDesc {
+  int32_t hidden;       /* H                                                            */
+  int32_t n_heads;      /* num_attention_heads                                          */
+  int32_t n_kv_heads;   /* num_key_value_heads (divides n_heads)                        */
+  int32_t head_dim;     /* head_dim: a multiple of 4, <= 256                            */
+  int32_t rotary_dim;   /* int(head_dim * partial_rotary_factor), even, <= head_dim     */
+  int32_t weight_dtype; /* q / k / v / o projections: F32 / F16 / I8 (+ row scales)     */
+  int32_t param_dtype;  /* input_layernorm, q_norm, k_norm: F32 / F16                   */
+  double rope_theta;    /* rope_theta                                                   */
+  float eps;            /* rms_norm_eps                                                 */
+} MxFullAttnDesc;
+
+typedef struct MxFullAttnWeights {
+  const void* norm_w;   /* input_layernorm.weight [H]                                   */
+  const void* q_w;      /* self_attn.q_proj.weight [2 n_heads head_dim, H]              */
+  const void* q_scale;  /* fp16 per row for MX_DT_I8, else NULL                         */
+  const void* k_w;      /* self_attn.k_proj.weight [n_kv_heads head_dim, H]             */
+  const void* k_scale;
+  const void* v_w;      /* self_attn.v_proj.weight [n_kv_heads head_dim, H]             */
+  const void* v_scale;
+  const void* o_w;      /* self_attn.o_proj.weight [H, n_heads head_dim]                */
+  const void* o_scale;
+  const void* q_norm_w; /* self_attn.q_norm.weight [head_dim] or NULL (no qk norm)      */
+  const void* k_norm_w; /* self_attn.k_norm.weight [head_dim] or NULL                   */
+} MxFullAttnWeights;
+
+typedef struct MxFullAttnViews {
+  float* h32;  /* [T, H] rms_norm(x)                                                    */
+  void* h16;   /* [T, H] fp16 copy (NULL for F32 weights)                               */
+  float* qg;   /* [T, 2 n_heads head_dim] [q | gate]; q normalised and rotated in place */
+  float* k;    /* [T, n_kv_heads head_dim] k, normalised and rotated in place           */
+  float* v;    /* [T, n_kv_heads head_dim]                                              */
+  void* act;   /* [T, n_heads head_dim] attn * sigmoid(gate), fp16 (fp32 for F32 weights) */
+  float* y;    /* [T, H] act W_o^T                                                      */
+} MxFullAttnViews;
+
+#define MX_FA_N_STAGES 8 /* rmsnorm, q, k, v, qk-norm+rope, attention, o, residual */
+
+int mx_full_attn_workspace_size(const MxFullAttnDesc* desc, int32_t tokens, size_t* nbytes);
+int mx_full_attn_views(const MxFullAttnDesc* desc, int32_t tokens, void* workspace,
+                       MxFullAttnViews* views);
+/* out may alias x. */
+int mx_full_attn_forward(const MxFullAttnDesc* desc, const MxFullAttnWeights* weights,
+                         const float* x, float* out, int32_t tokens, void* workspace,
+                         size_t workspace_bytes, void* stream);
+int mx_full_attn_forward_profiled(const MxFullAttnDesc* desc, const MxFullAttnWeights* weights,
+                                  const float* x, float* out, int32_t tokens, void* workspace,
+                                  size_t workspace_bytes, void* stream, void* const* events,
+                                  int32_t n_events);
+
 /* The recurrence alone (qwen3_next.py:56-95 with beta * k formed): q, kb [T, n dk],
  * v, o [T, n dv], decay [T, n] = exp(g), all fp32 on the device.                      */
 int mx_gated_delta_scan(const float* q, const float* kb, const float* v, const float* decay,

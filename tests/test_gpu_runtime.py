@@ -226,3 +226,51 @@ def test_qwen_linear_attention_layers_match_oracle(mi355x, granular):
     err = normwise_err(out, ref)
     say(f"    normwise err {err:.2e}")
     assert err <= 5e-3
+
+
+def test_qwen_hybrid_layers_match_oracle(mi355x):
+    """A Qwen3-Next stack with both attention kinds (linear, linear, full) plus MoE in each
+    packed layer, every block on the device, chained by the runtime."""
+    from oracle import full_attn_oracle as fa
+    from oracle import linear_attn_oracle as la
+
+    say("[gpu] Qwen3-Next hybrid layers (linear, linear, full)")
+    shape = syn.MoeShape(syn.QWEN, 256, 32, 6, 64, 64, 1.0, 1e-6, has_bias=False,
+                         has_shared_gate=True)
+    lshape = syn.LinearAttnShape(256, 4, 32, 32, 4, 1e-6)
+    fshape = syn.FullAttnShape(256, 4, 2, 64, 0.25, 5000000.0, 1e-6)
+    tensors, layers, blobs, kinds = [], [], {}, ["linear", "linear", "full"]
+    for i, kind in enumerate(kinds):
+        t = syn.make_tensors(shape, 95 + i, weight_dtype=np.float16)
+        if kind == "linear":
+            t.update(syn.make_linear_attn_tensors(lshape, 95 + i, weight_dtype=np.float16))
+        else:
+            t.update(syn.make_full_attn_tensors(fshape, 95 + i, weight_dtype=np.float16))
+        raw, meta = pack_tensors(t)
+        layers.append(make_layer_spec(i, meta, len(raw), attn_type=kind))
+        blobs[i] = raw
+        tensors.append(t)
+    cfg = shape.config()
+    cfg.update(lshape.config())
+    cfg.update(fshape.config())
+    ex = Qwen3NextExecutor(cfg)
+    x = syn.make_inputs(96, 40, shape.hidden)
+    rt = OffloadRuntime(layers, mi355x, InMemoryStorage(blobs), LookaheadScheduler(1), ex)
+    try:
+        out, _ = rt.run_inference([0, 1, 2], x)
+    finally:
+        rt.close()
+        ex.close()
+    ref = x
+    lspec = la.LinearAttnSpec(lshape.n_heads, lshape.head_dim_k, lshape.head_dim_v, lshape.eps)
+    fspec = fa.FullAttnSpec(fshape.n_heads, fshape.n_kv_heads, fshape.head_dim,
+                            fshape.rotary_dim, fshape.rope_theta, fshape.eps)
+    for kind, t in zip(kinds, tensors):
+        if kind == "linear":
+            ref = la.linear_attn_block(ref, t, lspec)["out"]
+        else:
+            ref = fa.full_attn_block(ref, t, fspec)["out"]
+        ref = orc.moe_block(ref, t, spec_for(shape))["out"]
+    err = normwise_err(out, ref)
+    say(f"    normwise err {err:.2e}")
+    assert err <= 5e-3

@@ -87,16 +87,40 @@ def test_executor_defaults_and_head_check():
         Qwen3NextExecutor(cfg).linear_attn_layout(layer)
 
 
-def test_full_attention_layers_need_a_hook():
+def test_unknown_attention_layers_need_a_hook():
     from moe_mi355x.types import DeviceBuffer
 
     shape = syn.MoeShape(syn.QWEN, 32, 4, 2, 16, 16, 1.0, 1e-6, has_bias=False,
                          has_shared_gate=True)
     t = syn.make_tensors(shape, 1)
-    t["self_attn.q_proj.weight"] = np.zeros((8, 32), np.float32)
+    t["self_attn.c_attn.weight"] = np.zeros((8, 32), np.float32)
     raw, meta = pack_tensors(t)
     layer = make_layer_spec(0, meta, len(raw), attn_type="full")
     ex = Qwen3NextExecutor(shape.config())
     with pytest.raises(NotImplementedError, match="attention="):
         ex.run_layer(layer, np.zeros((1, 32), np.float32),
                      DeviceBuffer(handle=0, nbytes=len(raw), backend="rocm"), None, None)
+
+
+def test_full_attention_layout_and_config():
+    from moe_mi355x.full_attn import FullAttnLayout
+
+    fs = syn.FullAttnShape(64, 4, 2, 16, 0.25, 10000.0, 1e-6)
+    t = syn.make_full_attn_tensors(fs, 1, weight_dtype=np.float16)
+    raw, meta = pack_tensors(t)
+    lay = FullAttnLayout.from_meta(meta, 4, 2, 16, fs.rotary_dim, 10000.0)
+    d = lay.desc(1e-6)
+    assert (d.hidden, d.n_heads, d.n_kv_heads, d.head_dim, d.rotary_dim) == (64, 4, 2, 16, 4)
+    assert d.weight_dtype == _lib.MX_DT_F16 and d.rope_theta == 10000.0
+    assert ctypes.sizeof(_lib.MxFullAttnDesc) == 48 and ctypes.sizeof(_lib.MxFullAttnWeights) == 88
+    with pytest.raises(ValueError, match="expected"):
+        FullAttnLayout.from_meta(meta, 4, 4, 16, 4, 10000.0)
+    del t["self_attn.v_proj.weight"]
+    with pytest.raises(ValueError, match="lacks"):
+        FullAttnLayout.from_meta(pack_tensors(t)[1], 4, 2, 16, 4, 10000.0)
+    # executor config keys and defaults (qwen3_next.py:109-118)
+    ex = Qwen3NextExecutor(fs.config())
+    assert (ex.num_heads, ex.num_kv_heads, ex.head_dim, ex.rotary_dim, ex.rope_theta) == (
+        4, 2, 16, 4, 10000.0)
+    d = Qwen3NextExecutor({"hidden_size": 2048, "num_attention_heads": 16})
+    assert (d.num_kv_heads, d.head_dim, d.rotary_dim, d.rope_theta) == (16, 128, 32, 5000000.0)
