@@ -16,8 +16,9 @@ the host), timed on the host cores.  Other BASELINE workloads (decode T=1/8, Zip
 prefill T=2048, Qwen3-Next T=1/4096, per-row int8 decode T=1/16, and 8 per-row int8
 layers streamed from pinned host memory through the lookahead-2 runtime at T=1/16) are
 reported under "sweep", with the Qwen3-Next linear-attention (Gated DeltaNet) block at
-T=1/4096 (32 key = value heads of 128, hidden 2048, fp16 projections).  Prints ONE JSON
-line.
+T=1/4096 (32 key = value heads of 128, hidden 2048, fp16 projections) and the gated
+full-attention block at T=1/4096 (16 query / 2 key-value heads of 256, RoPE on 64 dims).
+Prints ONE JSON line.
 """
 from __future__ import annotations
 
@@ -277,6 +278,77 @@ def linear_attn_case(backend, stream, shape: syn.LinearAttnShape, tokens: tuple[
     return out
 
 
+def full_attn_case(backend, stream, shape: syn.FullAttnShape, tokens: tuple[int, ...],
+                   steps: int, warmup: int) -> dict[str, dict]:
+    """Qwen3-Next gated full-attention block: fp16 projections, fp32 qk-norm / RoPE /
+    attention (fp32 MFMA), timed like the other cases.  Roofline of the attention kernel:
+    4 * heads * head_dim * T (T + 1) / 2 flops (QK^T and PV over the causal triangle) on
+    fp32 MFMA; of the projections: weight bytes from HBM."""
+    from moe_mi355x.full_attn import DeviceFullAttnLayer
+
+    t = syn.make_full_attn_tensors(shape, SEED, weight_dtype=np.float16, param_dtype=np.float32)
+    layer = DeviceFullAttnLayer.from_host(backend, t, shape.n_heads, shape.n_kv_heads,
+                                          shape.head_dim, shape.rotary_dim, shape.rope_theta,
+                                          stream)
+    nh, nkv, hd, H = shape.n_heads, shape.n_kv_heads, shape.head_dim, shape.hidden
+    w_bytes = 2 * H * (2 * nh * hd + 2 * nkv * hd + nh * hd)
+    out: dict[str, dict] = {}
+    b = backend
+    try:
+        desc, w = layer.desc(shape.eps), layer.weights()
+        r = layer.runner
+        for T in tokens:
+            name = f"qwen3next_fullattn_fp16_t{T}"
+            r.reserve(desc, T)
+            x = syn.make_inputs(SEED + T, T, H)
+            b.copy_h2d_ptr_async(r._io["x"].handle, x.ctypes.data, x.nbytes, stream)
+            b.synchronize_stream(stream)
+            k = min(steps, 20)
+
+            def step(ev=None):
+                r.forward_device(desc, w, r._io["x"].handle, r._io["out"].handle, T, stream, ev)
+
+            for _ in range(warmup):
+                step()
+            b.synchronize_stream(stream)
+            e0, e1 = b.create_timing_event(), b.create_timing_event()
+            b.record(e0, stream)
+            for _ in range(k):
+                step()
+            b.record(e1, stream)
+            b.event_synchronize(e1)
+            ms = b.elapsed_ms(e0, e1) / k
+            ev = [[b.create_timing_event() for _ in range(_lib.MX_FA_N_STAGES + 1)]
+                  for _ in range(k)]
+            for i in range(k):
+                step(ev[i])
+            b.event_synchronize(ev[-1][-1])
+            st = np.array([[b.elapsed_ms(e[j], e[j + 1]) for j in range(_lib.MX_FA_N_STAGES)]
+                           for e in ev]).mean(axis=0)
+            for e in ev + [[e0, e1]]:
+                for x_ in e:
+                    b.destroy_event(x_)
+            att_s = st[5] / 1e3
+            att_flops = 4.0 * nh * hd * T * (T + 1) / 2
+            proj_s = (st[1] + st[2] + st[3] + st[6]) / 1e3
+            out[name] = {
+                "workload": name, "tokens_per_s": round(T / (ms / 1e3), 1),
+                "ms_per_step": round(ms, 4),
+                "stage_ms": {nm: round(float(v), 4) for nm, v in zip(_lib.FA_STAGE_NAMES, st)},
+                "attention": {"ms": round(st[5], 4), "flops": att_flops,
+                              "TFLOPs": round(att_flops / att_s / 1e12, 2),
+                              "frac_fp32_mfma_peak": round(att_flops / att_s / MFMA_F32_PEAK, 4)},
+                "projections": {"ms": round(proj_s * 1e3, 4), "weight_bytes": w_bytes,
+                                "hbm_frac": round(w_bytes / proj_s / HBM_PEAK, 4),
+                                "mfma_frac": round(T * w_bytes / proj_s / MFMA_F16_PEAK, 4)},
+            }
+            log(f"{name}: {out[name]['tokens_per_s']} tok/s, {ms:.3f} ms, attention "
+                f"{st[5]:.3f} ms")
+    finally:
+        layer.close()
+    return out
+
+
 def stream_case(backend, shape: syn.MoeShape, tokens: tuple[int, ...], n_layers: int = 8,
                  modes: tuple[tuple[str, int], ...] = (("layer", 2), ("layer", 0), ("experts", 2)),
                  runs: int = 2) -> dict:
@@ -500,6 +572,11 @@ def main() -> int:
         toks = (1, 4096) if only is None else (int(only.rsplit("_t", 1)[1]),)
         sweep.update(linear_attn_case(backend, stream, syn.QWEN3_NEXT_LINEAR, toks, args.steps,
                                       3))
+
+    # ---- Qwen3-Next gated full-attention block -------------------------------------------------
+    if not args.no_sweep and (only is None or only.startswith("qwen3next_fullattn")):
+        toks = (1, 4096) if only is None else (int(only.rsplit("_t", 1)[1]),)
+        sweep.update(full_attn_case(backend, stream, syn.QWEN3_NEXT_FULL, toks, args.steps, 3))
 
     # ---- 8 int8 GLM-4.7 layers streamed from pinned host memory -------------------------------
     if not args.no_sweep and (only is None or only.startswith("glm47_int8_stream")):

@@ -160,16 +160,25 @@ __global__ __launch_bounds__(64) void k_fa_rope(float* __restrict__ qg, float* _
 // sigmoid(gate) (qwen3_next.py:201-202), writing the o_proj input.  Head dims are padded to
 // a multiple of 16 with zeros.
 // ------------------------------------------------------------------------------------
+#ifndef FA_NS
+#define FA_NS 2  // 16-key sub-tiles per staged key tile
+#endif
+
+#ifndef FA_WPE
+#define FA_WPE 2  // waves per SIMD the register budget is sized for
+#endif
+
 template <int NC>
-__global__ __launch_bounds__(256) void k_fa_attn(const float* __restrict__ qg,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, FA_WPE))) void k_fa_attn(const float* __restrict__ qg,
                                                  const float* __restrict__ kk,
                                                  const float* __restrict__ vv, FaDims m, int T,
                                                  float sqrt_hd, float* __restrict__ act32,
                                                  half_t* __restrict__ act16) {
-  constexpr int DP = NC * 16;  // padded head dim
-  constexpr int KT = 16;       // keys per tile
-  constexpr int KS = DP + 4;   // LDS row stride of the K tile (floats)
-  constexpr int VS = KT + 4;   // LDS row stride of the transposed V tile
+  constexpr int DP = NC * 16;      // padded head dim
+  constexpr int NS = FA_NS;        // 16-key sub-tiles per tile
+  constexpr int KT = 16 * NS;      // keys per tile
+  constexpr int KS = DP + 4;       // LDS row stride of the K tile (floats)
+  constexpr int VS = KT + 4;       // LDS row stride of the transposed V tile
   constexpr int NP = KT * DP / 4;  // float4 pieces of K (and of V) per tile
   __shared__ __align__(16) float sk[KT * KS];
   __shared__ __align__(16) float svt[DP * VS];
@@ -202,11 +211,13 @@ __global__ __launch_bounds__(256) void k_fa_attn(const float* __restrict__ qg,
   const float* kbase = kk + (size_t)kvh * m.hd;
   const float* vbase = vv + (size_t)kvh * m.hd;
 
+  // Tile staging: piece p = (key p % KT, dims 4 (p / KT) .. + 3), so consecutive threads
+  // write consecutive keys (banks) of the transposed V tile.
   for (int kt = 0; kt < ntile; ++kt) {
     const int k0 = kt * KT;
     __syncthreads();  // the previous tile's LDS reads are done
     for (int p = tid; p < NP; p += 256) {
-      const int key = p / (DP / 4), d4 = (p % (DP / 4)) * 4;
+      const int key = p % KT, d4 = (p / KT) * 4;
       const int s = k0 + key;
       float4 k4 = make_float4(0.f, 0.f, 0.f, 0.f), v4 = k4;
       if (s < T && d4 < m.hd) {
@@ -222,45 +233,65 @@ __global__ __launch_bounds__(256) void k_fa_attn(const float* __restrict__ qg,
     __syncthreads();
     if (k0 > wq_last) continue;  // every key of the tile is after every query of the wave
 
-    float4_t st = (float4_t){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const float4 a = *(const float4*)(sk + ql * KS + 16 * c + 4 * g);
-      st = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, qf[c].x, st, 0, 0, 0);
-      st = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, qf[c].y, st, 0, 0, 0);
-      st = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, qf[c].z, st, 0, 0, 0);
-      st = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, qf[c].w, st, 0, 0, 0);
-    }
-    float sv[4];
+    // S^T per 16-key sub-tile j, four independent accumulation chains each (dims 4 e + 16 c
+    // go to chain e), summed in a fixed order.
+    float sv[NS][4];
     float mt = -INFINITY;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int key = k0 + 4 * g + r;
-      const bool masked = key > qi || key >= T;
-      sv[r] = masked ? -INFINITY : st[r] / sqrt_hd;
-      mt = fmaxf(mt, sv[r]);
+    for (int j = 0; j < NS; ++j) {
+      float4_t sc[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sc[e] = (float4_t){0.f, 0.f, 0.f, 0.f};
+      const float* krow = sk + (16 * j + ql) * KS + 4 * g;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const float4 a = *(const float4*)(krow + 16 * c);
+        sc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, qf[c].x, sc[0], 0, 0, 0);
+        sc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, qf[c].y, sc[1], 0, 0, 0);
+        sc[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, qf[c].z, sc[2], 0, 0, 0);
+        sc[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, qf[c].w, sc[3], 0, 0, 0);
+      }
+      const float4_t st = (sc[0] + sc[1]) + (sc[2] + sc[3]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = k0 + 16 * j + 4 * g + r;
+        const bool masked = key > qi || key >= T;
+        sv[j][r] = masked ? -INFINITY : st[r] / sqrt_hd;
+        mt = fmaxf(mt, sv[j][r]);
+      }
     }
     mt = fmaxf(mt, __shfl_xor(mt, 16));
     mt = fmaxf(mt, __shfl_xor(mt, 32));
     const float mnew = fmaxf(mrun, mt);
     const float alpha = expf(mrun - mnew);  // 0 on the first tile (mrun = -inf)
-    float p[4];
+    float p[NS][4];
     float ps = 0.f;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      p[r] = expf(sv[r] - mnew);
-      ps += p[r];
-    }
+    for (int j = 0; j < NS; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        p[j][r] = expf(sv[j][r] - mnew);
+        ps += p[j][r];
+      }
     lrun = lrun * alpha + ps;
+    // The accumulators are rescaled only when some query's running max moved (alpha < 1);
+    // once the maxima settle most tiles skip the rescale.
+    const bool grow = mnew > mrun;
     mrun = mnew;
+    if (__builtin_amdgcn_ballot_w64(grow)) {
+#pragma unroll
+      for (int f = 0; f < NC; ++f) oacc[f] *= alpha;
+    }
 #pragma unroll
     for (int f = 0; f < NC; ++f) {
-      oacc[f] *= alpha;
-      const float4 a = *(const float4*)(svt + (16 * f + ql) * VS + 4 * g);
-      oacc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, p[0], oacc[f], 0, 0, 0);
-      oacc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, p[1], oacc[f], 0, 0, 0);
-      oacc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, p[2], oacc[f], 0, 0, 0);
-      oacc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, p[3], oacc[f], 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < NS; ++j) {
+        const float4 a = *(const float4*)(svt + (16 * f + ql) * VS + 16 * j + 4 * g);
+        oacc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, p[j][0], oacc[f], 0, 0, 0);
+        oacc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, p[j][1], oacc[f], 0, 0, 0);
+        oacc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, p[j][2], oacc[f], 0, 0, 0);
+        oacc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, p[j][3], oacc[f], 0, 0, 0);
+      }
     }
   }
   float l = lrun + __shfl_xor(lrun, 16);
