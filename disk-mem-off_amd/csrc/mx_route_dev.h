@@ -159,3 +159,165 @@ __device__ __forceinline__ void mx_topk_token(
   }
 }
 
+// ------------------------------------------------------------------------------------
+// Top-k of small batches spread over several waves per token (the same selection and
+// weights as mx_topk_token).  Token t takes NP = ceil(E / 64) waves; wave `part` holds
+// experts 64 part .. 64 part + 63, one per lane, and keeps its k largest (key image,
+// then lower id) as candidates in LDS, in ascending expert id.  Every expert of the
+// token's top-k is among its wave's k, so one wave per token then selects the top-k of
+// the NP k candidates; the candidate order is the expert id order, which keeps the tie
+// rule.  Softmax weights use the per-wave maxima and sums: M = max_p m_p,
+// S = sum_p s_p exp(m_p - M) (parts in order).
+// ------------------------------------------------------------------------------------
+#define TKP_MAXC 512  // candidates per block: (tokens x parts) <= 16 waves, k <= 32
+
+struct MxTopkPar {
+  uint32_t u[TKP_MAXC];
+  int id[TKP_MAXC];
+  float w[TKP_MAXC];  // sigmoid score (sigmoid modes) or key (softmax modes)
+  float m[16], sm[16];
+};
+
+__device__ __forceinline__ uint32_t mx_key_image(float kv, bool valid) {
+  if (kv != kv) kv = -INFINITY;
+  if (kv == 0.f) kv = 0.f;
+  const uint32_t b = __builtin_bit_cast(uint32_t, kv);
+  return valid ? ((b & 0x80000000u) ? ~b : (b | 0x80000000u)) : 0u;
+}
+
+// Phase 1, by wave `wv` < T * NP of the block: candidates of token wv / NP.
+__device__ __forceinline__ void mx_topk_par_cand(MxTopkPar& sh, const float* __restrict__ logits,
+                                                 const void* __restrict__ bias, int pdt, int E,
+                                                 int E1, int k, int mode, int NP, int wv) {
+  const int lane = threadIdx.x & 63;
+  const int t = wv / NP, part = wv - t * NP;
+  const int e = part * 64 + lane;
+  const bool valid = e < E;
+  const int ec = min(e, E - 1);
+  const float l = logits[(size_t)t * E1 + ec];
+  float b = 0.f;
+  if (bias) b = pdt == MX_DT_F16 ? (float)((const half_t*)bias)[ec] : ((const float*)bias)[ec];
+  float key, wsrc;
+  if (mode == MX_ROUTER_SIGMOID_SELECT_BIAS) {
+    wsrc = mx_sigmoid(l);
+    key = valid ? wsrc + b : -INFINITY;
+  } else {
+    key = valid ? ((mode == MX_ROUTER_REF_SOFTMAX_BIAS) ? l + b : l) : -INFINITY;
+    wsrc = key;
+    const float m = mx_wave_max(key);
+    const float s = mx_wave_sum(valid ? expf(key - m) : 0.f);
+    if (lane == 0) {
+      sh.m[wv] = m;
+      sh.sm[wv] = s;
+    }
+  }
+  const uint32_t u = mx_key_image(key, valid);
+  uint32_t tau = 0;
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cand = tau | (1u << bit);
+    if (__popcll(__builtin_amdgcn_uicmp(u, cand, 35 /* uge */)) >= k) tau = cand;
+  }
+  const unsigned long long below = (1ull << lane) - 1ull;
+  const int ngt = __popcll(__ballot(u > tau));
+  const unsigned long long eq = __ballot(u == tau);
+  const bool sel = u > tau || (u == tau && __popcll(eq & below) < k - ngt);
+  if (sel) {
+    const int slot = t * NP * k + part * k + __popcll(__ballot(sel) & below);
+    sh.u[slot] = u;
+    sh.id[slot] = e;
+    sh.w[slot] = wsrc;
+  }
+}
+
+// Phase 2, by one wave per token (after a workgroup LDS sync): the token's top-k.
+template <int VC>
+__device__ __forceinline__ void mx_topk_par_final(
+    const MxTopkPar& sh, const float* __restrict__ logits, int t, int E, int E1, int k,
+    int mode, int norm, float scaling, int NP, int has_seg, int* __restrict__ ids,
+    float* __restrict__ tw, float* __restrict__ shared_w, int* lds_ids, float* lds_w,
+    float* lds_sw) {
+  const int lane = threadIdx.x & 63;
+  const int C = NP * k, c0 = t * C;
+  uint32_t u[VC];
+  int cid[VC];
+  float cw[VC];
+#pragma unroll
+  for (int i = 0; i < VC; ++i) {
+    const int s = lane + 64 * i;
+    const bool v = s < C;
+    u[i] = v ? sh.u[c0 + s] : 0u;
+    cid[i] = v ? sh.id[c0 + s] : 0;
+    cw[i] = v ? sh.w[c0 + s] : 0.f;
+  }
+  uint32_t tau = 0;
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cand = tau | (1u << bit);
+    int c = 0;
+#pragma unroll
+    for (int i = 0; i < VC; ++i) c += __popcll(__builtin_amdgcn_uicmp(u[i], cand, 35));
+    if (c >= k) tau = cand;
+  }
+  const unsigned long long below = (1ull << lane) - 1ull;
+  int ngt = 0;
+#pragma unroll
+  for (int i = 0; i < VC; ++i) ngt += __popcll(__ballot(u[i] > tau));
+  bool sel[VC];
+  int ties = 0;
+#pragma unroll
+  for (int i = 0; i < VC; ++i) {
+    const unsigned long long eq = __ballot(u[i] == tau);
+    sel[i] = u[i] > tau || (u[i] == tau && ties + __popcll(eq & below) < k - ngt);
+    ties += __popcll(eq);
+  }
+  // Slot = number of chosen candidates ahead (larger image, or equal and lower id).
+  int rank[VC];
+#pragma unroll
+  for (int i = 0; i < VC; ++i) rank[i] = 0;
+#pragma unroll
+  for (int iy = 0; iy < VC; ++iy) {
+    unsigned long long m = __ballot(sel[iy]);
+    while (m) {
+      const int ly = __builtin_ctzll(m);
+      m &= m - 1ull;
+      const uint32_t uy = (uint32_t)__builtin_amdgcn_readlane((int)u[iy], ly);
+      const int ey = __builtin_amdgcn_readlane(cid[iy], ly);
+#pragma unroll
+      for (int i = 0; i < VC; ++i) rank[i] += (uy > u[i] || (uy == u[i] && ey < cid[i])) ? 1 : 0;
+    }
+  }
+  float M = 0.f, S = 1.f;
+  if (mode != MX_ROUTER_SIGMOID_SELECT_BIAS) {
+    M = -INFINITY;
+    for (int p = 0; p < NP; ++p) M = fmaxf(M, sh.m[t * NP + p]);
+    S = 0.f;
+    for (int p = 0; p < NP; ++p) S += sh.sm[t * NP + p] * expf(sh.m[t * NP + p] - M);
+  }
+  __shared__ int s_id[16][TK_MAXK];
+  __shared__ float s_w[16][TK_MAXK];
+  const int wv = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = 0; i < VC; ++i) {
+    if (sel[i]) {
+      s_id[wv][rank[i]] = cid[i];
+      s_w[wv][rank[i]] =
+          mode == MX_ROUTER_SIGMOID_SELECT_BIAS ? cw[i] : expf(cw[i] - M) / S;
+    }
+  }
+  mx_lds_fence();
+  const int my_id = lane < k ? s_id[wv][lane] : 0;
+  const float my_w = lane < k ? s_w[wv][lane] : 0.f;
+  float sum = 0.f;  // sequential over the k slots, identical on every lane
+  for (int r = 0; r < k; ++r) sum += mx_readlane(my_w, r);
+  if (lane < k) {
+    const float w = (norm ? my_w / (sum + 1e-20f) : my_w) * scaling;
+    ids[(size_t)t * k + lane] = my_id;
+    tw[(size_t)t * k + lane] = w;
+    lds_ids[t * k + lane] = my_id;
+    lds_w[t * k + lane] = w;
+  }
+  if (lane == 0 && shared_w) {
+    const float g = has_seg ? mx_sigmoid(logits[(size_t)t * E1 + E]) : 1.f;
+    shared_w[t] = g;
+    lds_sw[t] = g;
+  }
+}

@@ -196,6 +196,50 @@ def test_qwen_structure(mi355x, stream, wdt):
         assert float(np.max(np.abs(out - ref["out"]))) <= LOWP_ABS
 
 
+# ---- many experts, 1-2 tokens: the top-k spread over several waves per token ---------------
+
+@pytest.mark.parametrize("E,k,mode,T", [(512, 10, orc.SOFTMAX, 1), (512, 10, orc.SOFTMAX, 2),
+                                        (400, 8, orc.SIGMOID_SELECT_BIAS, 1),
+                                        (512, 32, orc.REF_SOFTMAX_BIAS, 2),
+                                        (384, 6, orc.SOFTMAX, 2)])
+def test_many_experts_small_batch(mi355x, stream, E, k, mode, T):
+    say(f"[gpu] many experts E={E} k={k} mode={mode} T={T}")
+    qwen = mode == orc.SOFTMAX
+    shape = syn.MoeShape(syn.QWEN if qwen else syn.GLM, 256, E, k, 64, 64,
+                         1.0 if qwen else 2.5, 1e-6, has_bias=not qwen, has_shared_gate=qwen)
+    t = syn.make_tensors(shape, 77 + E + k)
+    x = syn.make_inputs(77 + T, T, shape.hidden)
+    spec = spec_for(shape, mode)
+    out, views = run_device(mi355x, stream, t, shape, spec, x)
+    ref = orc.moe_block(x, t, spec)
+    check_routing(views, ref, ref["logits"], t.get("mlp.gate.e_score_correction_bias"), spec,
+                  f"E{E}/k{k}/{mode}/T{T}")
+    if qwen:
+        np.testing.assert_allclose(views["shared_w"], ref["shared_w"], rtol=1e-5)
+    assert normwise_err(out, ref["out"]) <= FP32_REL
+
+
+def test_many_experts_ties_match_single_wave_selection(mi355x, stream):
+    """Exact key ties (router rows repeated in groups of 4) go to the lower expert id on both
+    selection paths: one token (several waves per token) against the same token repeated
+    eight times (one wave per token)."""
+    say("[gpu] many experts, tied keys")
+    shape = syn.MoeShape(syn.QWEN, 256, 512, 10, 64, 64, 1.0, 1e-6, has_bias=False,
+                         has_shared_gate=True)
+    t = syn.make_tensors(shape, 5)
+    w = t["mlp.gate.weight"]
+    t["mlp.gate.weight"] = np.ascontiguousarray(np.repeat(w[::4], 4, axis=0))
+    spec = spec_for(shape)
+    x1 = syn.make_inputs(9, 1, shape.hidden)
+    _, v1 = run_device(mi355x, stream, t, shape, spec, x1)
+    _, v8 = run_device(mi355x, stream, t, shape, spec, np.repeat(x1, 8, axis=0))
+    ids1 = v1["ids"][0]
+    assert np.all(ids1 % 4 == 0) or len(set(ids1 // 4)) < len(ids1), "no tied group selected"
+    for r in range(8):
+        assert np.array_equal(v8["ids"][r], ids1), f"row {r}: {v8['ids'][r]} vs {ids1}"
+        np.testing.assert_allclose(v8["w"][r], v1["w"][0], rtol=1e-6, atol=1e-7)
+
+
 # ---- error paths through the ABI ----------------------------------------------------------
 
 def test_forward_rejects_bad_arguments(mi355x, stream):
