@@ -62,7 +62,11 @@ struct Carve {
 struct FaWork {
   MxFullAttnViews v;
   MxDenseWork dw;  // projections: entry 0 q, 1 k, 2 v, 3 o
+  half_t* k16;     // fp16 path: keys [n_kv][Tp][DP] (Tp = T padded to 32 keys, DP = hd padded to 32)
+  half_t* v16t;    // fp16 path: values per 32-key tile, transposed [n_kv][Tp / 32][DP][32]
 };
+
+constexpr int FA_KT = 32;  // keys per attention tile (fp16 path)
 
 int layout(const MxFullAttnDesc* d, int T, void* ws, FaWork* w, size_t* total) {
   MX_TRY(check_desc(d));
@@ -81,6 +85,13 @@ int layout(const MxFullAttnDesc* d, int T, void* ws, FaWork* w, size_t* total) {
   t.v.y = (float*)c.take(Tn * m.H * 4);
   char* dwb = (char*)c.take(mx_dense_work_bytes((int)Tn, d->weight_dtype, 4));
   mx_dense_work_carve(dwb, (int)Tn, d->weight_dtype, 4, &t.dw);
+  if (!f32) {
+    const size_t tp = (Tn + FA_KT - 1) / FA_KT * FA_KT, dp = (size_t)(m.hd + 31) / 32 * 32;
+    t.k16 = (half_t*)c.take((size_t)m.nkv * tp * dp * 2);
+    t.v16t = (half_t*)c.take((size_t)m.nkv * tp * dp * 2);
+  } else {
+    t.k16 = t.v16t = nullptr;
+  }
   if (w) *w = t;
   if (total) *total = mx_align_up(c.off, 256);
   return MX_OK;
@@ -315,6 +326,218 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, FA_WPE))
   }
 }
 
+// ------------------------------------------------------------------------------------
+// The same causal attention for fp16 / int8 projections (the block's fp16 path, whose
+// output is rounded to fp16 anyway): q, k, v rounded to fp16 and both products on
+// v_mfma_f32_16x16x32_f16 with fp32 accumulation; softmax statistics stay fp32.
+//
+// k_fa_pack_kv first writes fp16 copies of the keys (after RoPE) and values: keys
+// row-major per key/value head, values transposed per 32-key tile with the keys of a
+// tile in k-slot order (below), so staging a tile is a straight 16-byte copy.
+//
+// k_fa_attn_h: block = NW waves, one query head, 16 NW queries (16 per wave); tiles of
+// 32 keys, the next tile's 16-byte pieces loaded into registers while a tile computes.
+//   S^T = K Q^T per 16-key sub-tile: A = K rows (16 keys x 32 dims from LDS), B = the
+//     wave's Q (registers, 8 fp16 dims per lane per 32-dim chunk); lane (j, g) gets
+//     S^T[4 g + r][j], so query j = lane % 16 is lane-local.
+//   O^T += V^T P per 16-dim slab: the MFMA k-slot (g, e) stands for key 4 g + e of
+//     sub-tile 0 (e < 4) and key 4 g + e - 4 of sub-tile 1 (e >= 4), so the B operand is
+//     exactly the lane's own 8 probabilities, and A is 16 bytes of a V^T row.
+// LDS rows are padded (K: +16 B, V^T: +16 B) so the 16-byte fragment reads of a quarter
+// wave hit distinct banks.
+// ------------------------------------------------------------------------------------
+__device__ __forceinline__ int fa_slot(int key) {  // key of a 32-key tile -> k-slot
+  return 8 * ((key & 15) >> 2) + (key & 3) + 4 * (key >> 4);
+}
+
+__global__ __launch_bounds__(256) void k_fa_pack_kv(const float* __restrict__ kk,
+                                                    const float* __restrict__ vv, FaDims m,
+                                                    int T, int Tp, int DP,
+                                                    half_t* __restrict__ k16,
+                                                    half_t* __restrict__ v16t) {
+  const int nc8 = DP / 8;
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  const long total = (long)m.nkv * Tp * nc8;
+  if (i >= total) return;
+  const int c8 = (int)(i % nc8);
+  const long r = i / nc8;
+  const int s = (int)(r % Tp), kvh = (int)(r / Tp);
+  half8_t kh, vh;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int d = 8 * c8 + e;
+    const bool ok = s < T && d < m.hd;
+    const size_t src = (size_t)s * m.kw + (size_t)kvh * m.hd + d;
+    kh[e] = (half_t)(ok ? kk[src] : 0.f);
+    vh[e] = (half_t)(ok ? vv[src] : 0.f);
+  }
+  *(half8_t*)(k16 + ((size_t)kvh * Tp + s) * DP + 8 * c8) = kh;
+  half_t* vt = v16t + ((size_t)kvh * (Tp / FA_KT) + s / FA_KT) * DP * FA_KT + fa_slot(s % FA_KT);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) vt[(size_t)(8 * c8 + e) * FA_KT] = vh[e];
+}
+
+template <int NC, int NW>
+__global__ __launch_bounds__(64 * NW) void k_fa_attn_h(const float* __restrict__ qg,
+                                                       const half_t* __restrict__ k16,
+                                                       const half_t* __restrict__ v16t,
+                                                       FaDims m, int T, int Tp, float sqrt_hd,
+                                                       half_t* __restrict__ act16) {
+  constexpr int DP = NC * 32;          // padded head dim
+  constexpr int KT = FA_KT;            // keys per tile
+  constexpr int KR = DP + 8;           // K tile row stride (halfs)
+  constexpr int VR = KT + 8;           // V^T tile row stride (halfs)
+  constexpr int NT = 64 * NW;          // threads
+  constexpr int KCH = KT * DP / 8;     // 16-byte pieces of a K tile (= of a V^T tile)
+  constexpr int PPT = (KCH + NT - 1) / NT;  // pieces of each per thread
+  __shared__ __align__(16) half_t sk[KT * KR];
+  __shared__ __align__(16) half_t svt[DP * VR];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = blockIdx.y;
+  const int QB = 16 * NW;
+  const int q0 = (gridDim.x - 1 - blockIdx.x) * QB;  // longest query blocks first
+  const int qw0 = q0 + wave * 16;
+  const int kvh = h / (m.nh / m.nkv);
+  const int ql = lane & 15, g = lane >> 4;
+  const int qi = qw0 + ql;
+  const int qc = min(qi, T - 1);
+
+  half8_t qf[NC];
+  const float* qrow = qg + (size_t)qc * m.qw + (size_t)h * m.hd;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int d = 32 * c + 8 * g + e;
+      qf[c][e] = (half_t)(d < m.hd ? qrow[d] : 0.f);
+    }
+  }
+  float4_t oacc[2 * NC];
+#pragma unroll
+  for (int f = 0; f < 2 * NC; ++f) oacc[f] = (float4_t){0.f, 0.f, 0.f, 0.f};
+  float mrun = -INFINITY, lrun = 0.f;
+
+  const int kend = min(T, q0 + QB);
+  const int ntile = (kend + KT - 1) / KT;
+  const int wq_last = min(qw0 + 15, T - 1);
+  const half_t* kb = k16 + (size_t)kvh * Tp * DP;
+  const half_t* vb = v16t + (size_t)kvh * Tp * DP;  // Tp / KT tiles of DP x KT
+  const float rs = 1.f / sqrt_hd;
+
+  // Staging pieces of this thread: K piece i -> row i / (DP / 8), V^T piece i -> row i / 4.
+  int4_t pk[PPT], pv[PPT];
+  auto fetch = [&](int kt) {
+    const int4_t* ks = (const int4_t*)(kb + (size_t)kt * KT * DP);
+    const int4_t* vs = (const int4_t*)(vb + (size_t)kt * KT * DP);
+#pragma unroll
+    for (int u = 0; u < PPT; ++u) {
+      const int i = tid + NT * u;
+      if (KCH % NT == 0 || i < KCH) {
+        pk[u] = ks[i];
+        pv[u] = vs[i];
+      }
+    }
+  };
+  auto stage = [&]() {
+#pragma unroll
+    for (int u = 0; u < PPT; ++u) {
+      const int i = tid + NT * u;
+      if (KCH % NT == 0 || i < KCH) {
+        *(int4_t*)(sk + (i / (DP / 8)) * KR + (i % (DP / 8)) * 8) = pk[u];
+        *(int4_t*)(svt + (i >> 2) * VR + (i & 3) * 8) = pv[u];
+      }
+    }
+  };
+
+  fetch(0);
+  for (int kt = 0; kt < ntile; ++kt) {
+    const int k0 = kt * KT;
+    __syncthreads();  // the previous tile's LDS reads are done
+    stage();
+    __syncthreads();
+    if (kt + 1 < ntile) fetch(kt + 1);
+    if (k0 > wq_last) continue;  // every key of the tile is after every query of the wave
+
+    float sv[2][4];
+    float mt = -INFINITY;
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      float4_t sc = (float4_t){0.f, 0.f, 0.f, 0.f};
+      const half_t* krow = sk + (16 * b + ql) * KR + 8 * g;
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+        sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const half8_t*)(krow + 32 * c), qf[c], sc,
+                                                    0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = k0 + 16 * b + 4 * g + r;
+        const bool masked = key > qi || key >= T;
+        sv[b][r] = masked ? -INFINITY : sc[r] * rs;
+        mt = fmaxf(mt, sv[b][r]);
+      }
+    }
+    mt = fmaxf(mt, __shfl_xor(mt, 16));
+    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    const float mnew = fmaxf(mrun, mt);
+    const float alpha = expf(mrun - mnew);  // 0 on the first tile (mrun = -inf)
+    half8_t pf;
+    float ps = 0.f;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float pv = expf(sv[b][r] - mnew);
+        ps += pv;
+        pf[4 * b + r] = (half_t)pv;
+      }
+    lrun = lrun * alpha + ps;
+    const bool grow = mnew > mrun;
+    mrun = mnew;
+    if (__builtin_amdgcn_ballot_w64(grow)) {
+#pragma unroll
+      for (int f = 0; f < 2 * NC; ++f) oacc[f] *= alpha;
+    }
+#pragma unroll
+    for (int f = 0; f < 2 * NC; ++f)
+      oacc[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+          *(const half8_t*)(svt + (16 * f + ql) * VR + 8 * g), pf, oacc[f], 0, 0, 0);
+  }
+  float l = lrun + __shfl_xor(lrun, 16);
+  l = l + __shfl_xor(l, 32);
+  if (qi >= T) return;
+  const float* gate = qg + (size_t)qi * m.qw + (size_t)m.od + (size_t)h * m.hd;
+  const size_t orow = (size_t)qi * m.od + (size_t)h * m.hd;
+#pragma unroll
+  for (int f = 0; f < 2 * NC; ++f) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int d = 16 * f + 4 * g + r;
+      if (d < m.hd) act16[orow + d] = (half_t)((oacc[f][r] / l) * mx_sigmoid(gate[d]));
+    }
+  }
+}
+
+#ifndef FA_H_NW
+#define FA_H_NW 8  // waves (16 queries each) per block of the fp16 attention
+#endif
+
+template <int NC>
+int launch_attn_h(const float* qg, const float* kk, const float* vv, const FaDims& m, int T,
+                  half_t* k16, half_t* v16t, void* act, hipStream_t s) {
+  const int Tp = (T + FA_KT - 1) / FA_KT * FA_KT, DP = NC * 32;
+  const long pieces = (long)m.nkv * Tp * (DP / 8);
+  mx_clear_error();
+  hipLaunchKernelGGL(k_fa_pack_kv, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, s, kk,
+                     vv, m, T, Tp, DP, k16, v16t);
+  MX_TRY(mx_launch_status());
+  const dim3 grid(mx_ceil_div(T, 16 * FA_H_NW), m.nh);
+  const float sqrt_hd = (float)sqrt((double)m.hd);
+  hipLaunchKernelGGL((k_fa_attn_h<NC, FA_H_NW>), grid, dim3(64 * FA_H_NW), 0, s, qg, k16, v16t,
+                     m, T, Tp, sqrt_hd, (half_t*)act);
+  return mx_launch_status();
+}
+
 template <int NC>
 int launch_attn(const float* qg, const float* kk, const float* vv, const FaDims& m, int T,
                 void* act, bool f16, hipStream_t s) {
@@ -327,7 +550,14 @@ int launch_attn(const float* qg, const float* kk, const float* vv, const FaDims&
 }
 
 int attn_launch(const float* qg, const float* kk, const float* vv, const FaDims& m, int T,
-                void* act, bool f16, hipStream_t s) {
+                void* act, bool f16, half_t* k16, half_t* v16t, hipStream_t s) {
+  if (f16) {
+    if (m.hd <= 32) return launch_attn_h<1>(qg, kk, vv, m, T, k16, v16t, act, s);
+    if (m.hd <= 64) return launch_attn_h<2>(qg, kk, vv, m, T, k16, v16t, act, s);
+    if (m.hd <= 128) return launch_attn_h<4>(qg, kk, vv, m, T, k16, v16t, act, s);
+    if (m.hd <= 256) return launch_attn_h<8>(qg, kk, vv, m, T, k16, v16t, act, s);
+    return MX_ERR_UNSUPPORTED;
+  }
   if (m.hd <= 16) return launch_attn<1>(qg, kk, vv, m, T, act, f16, s);
   if (m.hd <= 32) return launch_attn<2>(qg, kk, vv, m, T, act, f16, s);
   if (m.hd <= 64) return launch_attn<4>(qg, kk, vv, m, T, act, f16, s);
@@ -398,7 +628,7 @@ int run_stage(int st, const MxFullAttnDesc* d, const MxFullAttnWeights* w, const
       return mx_launch_status();
     }
     case 5:
-      return attn_launch(k.v.qg, k.v.k, k.v.v, m, T, k.v.act, !f32, s);
+      return attn_launch(k.v.qg, k.v.k, k.v.v, m, T, k.v.act, !f32, k.k16, k.v16t, s);
     case 6:
       return mx_project(k.dw, 3, wdt, w->o_w, T, m.H, m.od, k.v.act, k.v.y, s);
     case 7: {
