@@ -66,7 +66,11 @@ struct FaWork {
   half_t* v16t;    // fp16 path: values per 32-key tile, transposed [n_kv][Tp / 32][DP][32]
 };
 
-constexpr int FA_KT = 32;  // keys per attention tile (fp16 path)
+constexpr int FA_KT = 32;  // keys per transposed value block (fp16 path)
+#ifndef FA_H_S32
+#define FA_H_S32 2  // 32-key blocks per attention tile of the fp16 path
+#endif
+constexpr int FA_TPAD = FA_KT * FA_H_S32;  // keys are padded to whole tiles
 
 int layout(const MxFullAttnDesc* d, int T, void* ws, FaWork* w, size_t* total) {
   MX_TRY(check_desc(d));
@@ -86,7 +90,7 @@ int layout(const MxFullAttnDesc* d, int T, void* ws, FaWork* w, size_t* total) {
   char* dwb = (char*)c.take(mx_dense_work_bytes((int)Tn, d->weight_dtype, 4));
   mx_dense_work_carve(dwb, (int)Tn, d->weight_dtype, 4, &t.dw);
   if (!f32) {
-    const size_t tp = (Tn + FA_KT - 1) / FA_KT * FA_KT, dp = (size_t)(m.hd + 31) / 32 * 32;
+    const size_t tp = (Tn + FA_TPAD - 1) / FA_TPAD * FA_TPAD, dp = (size_t)(m.hd + 31) / 32 * 32;
     t.k16 = (half_t*)c.take((size_t)m.nkv * tp * dp * 2);
     t.v16t = (half_t*)c.take((size_t)m.nkv * tp * dp * 2);
   } else {
@@ -377,21 +381,21 @@ __global__ __launch_bounds__(256) void k_fa_pack_kv(const float* __restrict__ kk
   for (int e = 0; e < 8; ++e) vt[(size_t)(8 * c8 + e) * FA_KT] = vh[e];
 }
 
-template <int NC, int NW>
+template <int NC, int NW, int S32>
 __global__ __launch_bounds__(64 * NW) void k_fa_attn_h(const float* __restrict__ qg,
                                                        const half_t* __restrict__ k16,
                                                        const half_t* __restrict__ v16t,
                                                        FaDims m, int T, int Tp, float sqrt_hd,
                                                        half_t* __restrict__ act16) {
   constexpr int DP = NC * 32;          // padded head dim
-  constexpr int KT = FA_KT;            // keys per tile
+  constexpr int KT = 32 * S32;         // keys per tile
   constexpr int KR = DP + 8;           // K tile row stride (halfs)
   constexpr int VR = KT + 8;           // V^T tile row stride (halfs)
   constexpr int NT = 64 * NW;          // threads
   constexpr int KCH = KT * DP / 8;     // 16-byte pieces of a K tile (= of a V^T tile)
   constexpr int PPT = (KCH + NT - 1) / NT;  // pieces of each per thread
   __shared__ __align__(16) half_t sk[KT * KR];
-  __shared__ __align__(16) half_t svt[DP * VR];
+  __shared__ __align__(16) half_t svt[S32 * DP * VR];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int h = blockIdx.y;
@@ -423,23 +427,23 @@ __global__ __launch_bounds__(64 * NW) void k_fa_attn_h(const float* __restrict__
   const int wq_last = min(qw0 + 15, T - 1);
   const half_t* kb = k16 + (size_t)kvh * Tp * DP;
   const half_t* vb = v16t + (size_t)kvh * Tp * DP;  // Tp / KT tiles of DP x KT
-  const float rs = 1.f / sqrt_hd;
+  // Scores in the base-2 domain: s2 = (q.k) log2(e) / sqrt(head_dim), p = 2^(s2 - max).
+  const float rs = 1.4426950408889634f / sqrt_hd;
 
-  // Staging pieces of this thread: K piece i -> row i / (DP / 8), V^T piece i -> row i / 4.
+  // Staging pieces of this thread: K piece i -> row i / (DP / 8), V^T piece i -> row i / 4
+  // (the rows of the S32 value blocks follow each other).
   int4_t pk[PPT], pv[PPT];
-  auto fetch = [&](int kt) {
-    const int4_t* ks = (const int4_t*)(kb + (size_t)kt * KT * DP);
-    const int4_t* vs = (const int4_t*)(vb + (size_t)kt * KT * DP);
 #pragma unroll
-    for (int u = 0; u < PPT; ++u) {
-      const int i = tid + NT * u;
-      if (KCH % NT == 0 || i < KCH) {
-        pk[u] = ks[i];
-        pv[u] = vs[i];
-      }
+  for (int u = 0; u < PPT; ++u) {
+    const int i = tid + NT * u;
+    if (KCH % NT == 0 || i < KCH) {
+      pk[u] = ((const int4_t*)kb)[i];
+      pv[u] = ((const int4_t*)vb)[i];
     }
-  };
-  auto stage = [&]() {
+  }
+  for (int kt = 0; kt < ntile; ++kt) {
+    const int k0 = kt * KT;
+    __syncthreads();  // the previous tile's LDS reads are done
 #pragma unroll
     for (int u = 0; u < PPT; ++u) {
       const int i = tid + NT * u;
@@ -448,21 +452,27 @@ __global__ __launch_bounds__(64 * NW) void k_fa_attn_h(const float* __restrict__
         *(int4_t*)(svt + (i >> 2) * VR + (i & 3) * 8) = pv[u];
       }
     }
-  };
-
-  fetch(0);
-  for (int kt = 0; kt < ntile; ++kt) {
-    const int k0 = kt * KT;
-    __syncthreads();  // the previous tile's LDS reads are done
-    stage();
     __syncthreads();
-    if (kt + 1 < ntile) fetch(kt + 1);
+    if (kt + 1 < ntile) {
+      const int4_t* ks = (const int4_t*)(kb + (size_t)(kt + 1) * KT * DP);
+      const int4_t* vs = (const int4_t*)(vb + (size_t)(kt + 1) * KT * DP);
+#pragma unroll
+      for (int u = 0; u < PPT; ++u) {
+        const int i = tid + NT * u;
+        if (KCH % NT == 0 || i < KCH) {
+          pk[u] = ks[i];
+          pv[u] = vs[i];
+        }
+      }
+    }
     if (k0 > wq_last) continue;  // every key of the tile is after every query of the wave
+    // Only tiles reaching past the wave's first query or past T need the mask.
+    const bool need_mask = k0 + KT - 1 > qw0 || k0 + KT > T;
 
-    float sv[2][4];
+    float sv[2 * S32][4];
     float mt = -INFINITY;
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
+    for (int b = 0; b < 2 * S32; ++b) {
       float4_t sc = (float4_t){0.f, 0.f, 0.f, 0.f};
       const half_t* krow = sk + (16 * b + ql) * KR + 8 * g;
 #pragma unroll
@@ -470,26 +480,30 @@ __global__ __launch_bounds__(64 * NW) void k_fa_attn_h(const float* __restrict__
         sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const half8_t*)(krow + 32 * c), qf[c], sc,
                                                     0, 0, 0);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = k0 + 16 * b + 4 * g + r;
-        const bool masked = key > qi || key >= T;
-        sv[b][r] = masked ? -INFINITY : sc[r] * rs;
-        mt = fmaxf(mt, sv[b][r]);
+      for (int r = 0; r < 4; ++r) sv[b][r] = sc[r] * rs;
+      if (need_mask) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = k0 + 16 * b + 4 * g + r;
+          if (key > qi || key >= T) sv[b][r] = -INFINITY;
+        }
       }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mt = fmaxf(mt, sv[b][r]);
     }
     mt = fmaxf(mt, __shfl_xor(mt, 16));
     mt = fmaxf(mt, __shfl_xor(mt, 32));
     const float mnew = fmaxf(mrun, mt);
-    const float alpha = expf(mrun - mnew);  // 0 on the first tile (mrun = -inf)
-    half8_t pf;
+    const float alpha = __builtin_amdgcn_exp2f(mrun - mnew);  // 0 on the first tile
+    half8_t pf[S32];
     float ps = 0.f;
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int b = 0; b < 2 * S32; ++b)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float pv = expf(sv[b][r] - mnew);
-        ps += pv;
-        pf[4 * b + r] = (half_t)pv;
+        const float pv2 = __builtin_amdgcn_exp2f(sv[b][r] - mnew);
+        ps += pv2;
+        pf[b >> 1][4 * (b & 1) + r] = (half_t)pv2;
       }
     lrun = lrun * alpha + ps;
     const bool grow = mnew > mrun;
@@ -499,9 +513,12 @@ __global__ __launch_bounds__(64 * NW) void k_fa_attn_h(const float* __restrict__
       for (int f = 0; f < 2 * NC; ++f) oacc[f] *= alpha;
     }
 #pragma unroll
-    for (int f = 0; f < 2 * NC; ++f)
-      oacc[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-          *(const half8_t*)(svt + (16 * f + ql) * VR + 8 * g), pf, oacc[f], 0, 0, 0);
+    for (int s32 = 0; s32 < S32; ++s32)
+#pragma unroll
+      for (int f = 0; f < 2 * NC; ++f)
+        oacc[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+            *(const half8_t*)(svt + (s32 * DP + 16 * f + ql) * VR + 8 * g), pf[s32], oacc[f], 0,
+            0, 0);
   }
   float l = lrun + __shfl_xor(lrun, 16);
   l = l + __shfl_xor(l, 32);
@@ -525,7 +542,7 @@ __global__ __launch_bounds__(64 * NW) void k_fa_attn_h(const float* __restrict__
 template <int NC>
 int launch_attn_h(const float* qg, const float* kk, const float* vv, const FaDims& m, int T,
                   half_t* k16, half_t* v16t, void* act, hipStream_t s) {
-  const int Tp = (T + FA_KT - 1) / FA_KT * FA_KT, DP = NC * 32;
+  const int Tp = (T + FA_TPAD - 1) / FA_TPAD * FA_TPAD, DP = NC * 32;
   const long pieces = (long)m.nkv * Tp * (DP / 8);
   mx_clear_error();
   hipLaunchKernelGGL(k_fa_pack_kv, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, s, kk,
@@ -533,8 +550,8 @@ int launch_attn_h(const float* qg, const float* kk, const float* vv, const FaDim
   MX_TRY(mx_launch_status());
   const dim3 grid(mx_ceil_div(T, 16 * FA_H_NW), m.nh);
   const float sqrt_hd = (float)sqrt((double)m.hd);
-  hipLaunchKernelGGL((k_fa_attn_h<NC, FA_H_NW>), grid, dim3(64 * FA_H_NW), 0, s, qg, k16, v16t,
-                     m, T, Tp, sqrt_hd, (half_t*)act);
+  hipLaunchKernelGGL((k_fa_attn_h<NC, FA_H_NW, FA_H_S32>), grid, dim3(64 * FA_H_NW), 0, s, qg,
+                     k16, v16t, m, T, Tp, sqrt_hd, (half_t*)act);
   return mx_launch_status();
 }
 
