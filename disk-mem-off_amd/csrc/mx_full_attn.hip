@@ -210,11 +210,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, FA_WPE))
   // Q fragment (B operand of S^T): qf[c] = Q[qi][16 c + 4 g .. + 3].
   float4 qf[NC];
   const float* qrow = qg + (size_t)qc * m.qw + (size_t)h * m.hd;
+  // Loads at clamped (in-row) offsets first, all in flight together; pad dims zeroed after.
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    const int d = 16 * c + 4 * g;
-    qf[c] = d < m.hd ? *(const float4*)(qrow + d) : make_float4(0.f, 0.f, 0.f, 0.f);
-  }
+  for (int c = 0; c < NC; ++c) qf[c] = *(const float4*)(qrow + min(16 * c + 4 * g, m.hd - 4));
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+    if (16 * c + 4 * g >= m.hd) qf[c] = make_float4(0.f, 0.f, 0.f, 0.f);
   float4_t oacc[NC];
 #pragma unroll
   for (int f = 0; f < NC; ++f) oacc[f] = (float4_t){0.f, 0.f, 0.f, 0.f};
@@ -314,18 +315,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, FA_WPE))
   if (qi >= T) return;
   const float* gate = qg + (size_t)qi * m.qw + (size_t)m.od + (size_t)h * m.hd;
   const size_t orow = (size_t)qi * m.od + (size_t)h * m.hd;
+  float4 gv[NC];  // gate loads first (clamped offsets), then the ordered math and stores
+#pragma unroll
+  for (int f = 0; f < NC; ++f) gv[f] = *(const float4*)(gate + min(16 * f + 4 * g, m.hd - 4));
 #pragma unroll
   for (int f = 0; f < NC; ++f) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int d = 16 * f + 4 * g + r;
-      if (d < m.hd) {
-        const float a = (oacc[f][r] / l) * mx_sigmoid(gate[d]);
-        if (act16)
-          act16[orow + d] = (half_t)a;
-        else
-          act32[orow + d] = a;
-      }
+    const int d = 16 * f + 4 * g;
+    if (d >= m.hd) continue;
+    const float a0 = (oacc[f][0] / l) * mx_sigmoid(gv[f].x);
+    const float a1 = (oacc[f][1] / l) * mx_sigmoid(gv[f].y);
+    const float a2 = (oacc[f][2] / l) * mx_sigmoid(gv[f].z);
+    const float a3 = (oacc[f][3] / l) * mx_sigmoid(gv[f].w);
+    if (act16) {
+      act16[orow + d] = (half_t)a0;
+      act16[orow + d + 1] = (half_t)a1;
+      act16[orow + d + 2] = (half_t)a2;
+      act16[orow + d + 3] = (half_t)a3;
+    } else {
+      *(float4*)(act32 + orow + d) = make_float4(a0, a1, a2, a3);
     }
   }
 }
@@ -409,13 +416,20 @@ __global__ __launch_bounds__(64 * NW) void k_fa_attn_h(const float* __restrict__
 
   half8_t qf[NC];
   const float* qrow = qg + (size_t)qc * m.qw + (size_t)h * m.hd;
+  {
+    // Loads at clamped (in-row) offsets first, all in flight together; pad dims zeroed after.
+    float4 qv[2 * NC];
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
+    for (int u = 0; u < 2 * NC; ++u)
+      qv[u] = *(const float4*)(qrow + min(32 * (u >> 1) + 8 * g + 4 * (u & 1), m.hd - 4));
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int d = 32 * c + 8 * g + e;
-      qf[c][e] = (half_t)(d < m.hd ? qrow[d] : 0.f);
-    }
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float4 v = qv[2 * c + (e >> 2)];
+        const float x = (e & 3) == 0 ? v.x : (e & 3) == 1 ? v.y : (e & 3) == 2 ? v.z : v.w;
+        qf[c][e] = (half_t)(32 * c + 8 * g + e < m.hd ? x : 0.f);
+      }
   }
   float4_t oacc[2 * NC];
 #pragma unroll
@@ -525,13 +539,21 @@ __global__ __launch_bounds__(64 * NW) void k_fa_attn_h(const float* __restrict__
   if (qi >= T) return;
   const float* gate = qg + (size_t)qi * m.qw + (size_t)m.od + (size_t)h * m.hd;
   const size_t orow = (size_t)qi * m.od + (size_t)h * m.hd;
+  float4 gv[2 * NC];  // gate loads first (clamped offsets), then the math and 8-byte stores
+#pragma unroll
+  for (int f = 0; f < 2 * NC; ++f)
+    gv[f] = *(const float4*)(gate + min(16 * f + 4 * g, m.hd - 4));
+  const float il = 1.f / l;
 #pragma unroll
   for (int f = 0; f < 2 * NC; ++f) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int d = 16 * f + 4 * g + r;
-      if (d < m.hd) act16[orow + d] = (half_t)((oacc[f][r] / l) * mx_sigmoid(gate[d]));
-    }
+    const int d = 16 * f + 4 * g;
+    if (d >= m.hd) continue;
+    typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+    const half4_t o = {(half_t)(oacc[f][0] * il * mx_sigmoid(gv[f].x)),
+                       (half_t)(oacc[f][1] * il * mx_sigmoid(gv[f].y)),
+                       (half_t)(oacc[f][2] * il * mx_sigmoid(gv[f].z)),
+                       (half_t)(oacc[f][3] * il * mx_sigmoid(gv[f].w))};
+    *(half4_t*)(act16 + orow + d) = o;
   }
 }
 
