@@ -451,6 +451,53 @@ __global__ __launch_bounds__(VPT > 8 ? 512 : 1024) void k_topk_dispatch(
       mx_topk_token<VPT>(logits, 1, T, t, bias, pdt, E, E1, k, mode, norm, scaling, has_seg,
                          ids, tw, shared_w, sid, sw, ssw);
   }
+  if (T == 1) {
+    // One token: wave 0 selected it and writes the tables directly — every chosen expert
+    // is a group of one row, groups in ascending expert id (the order of the general
+    // dispatch), the shared expert's row and group first among tiles.
+    if (threadIdx.x >= 64) return;
+    mx_lds_fence();
+    const int lane = threadIdx.x;
+    const int G0 = has_shared ? 1 : 0, S0 = has_shared ? 1 : 0;
+    const int my_id = lane < k ? sid[lane] : 0x7fffffff;
+    const float my_w = lane < k ? sw[lane] : 0.f;
+    int rank = 0;
+    for (int i = 0; i < k; ++i) rank += __builtin_amdgcn_readlane(my_id, i) < my_id ? 1 : 0;
+    if (lane < k) {
+      sorted_tok[rank] = 0;
+      sorted_w[rank] = my_w;
+      pair_pos[lane] = rank;
+      g_expert[G0 + rank] = my_id;
+      g_start[G0 + rank] = rank;
+      g_count[G0 + rank] = 1;
+      mt_group[S0 + rank] = G0 + rank;
+      mt_row0[S0 + rank] = 0;
+    }
+    for (int e = lane; e <= E; e += 64) {
+      int below = 0, hit = 0;
+      for (int i = 0; i < k; ++i) {
+        const int id = __builtin_amdgcn_readlane(my_id, i);
+        below += id < e ? 1 : 0;
+        hit |= id == e ? 1 : 0;
+      }
+      if (e < E) counts[e] = hit;
+      offsets[e] = below;
+    }
+    if (lane == 0) {
+      if (has_shared) {
+        g_expert[0] = E;
+        g_start[0] = k;
+        g_count[0] = 1;
+        mt_group[0] = 0;
+        mt_row0[0] = 0;
+        sorted_tok[k] = 0;
+        sorted_w[k] = shared_w ? ssw[0] : 1.f;
+      }
+      *n_groups = G0 + k;
+      *n_mtiles = S0 + k;
+    }
+    return;
+  }
   mx_lds_sync();
   mx_dispatch_block_small(smem, sid, sw, shared_w ? ssw : nullptr, T, k, E, has_shared, m_blk,
                           counts, offsets, sorted_tok, sorted_w, pair_pos, g_expert, g_start,
@@ -505,8 +552,10 @@ int mx_router_decode_launch(const MxMoeDesc* d, const MxMoeWeights* w, int T, co
 #undef RL_TT
 #undef RL_LAUNCH
   MX_TRY(mx_launch_status());
+  // One token with a single-wave selection needs one wave only.
+  const int nwl = (T == 1 && vpt < 6) ? 1 : nw;
 #define TD_LAUNCH(V)                                                                           \
-  hipLaunchKernelGGL((k_topk_dispatch<V>), dim3(1), dim3(64 * nw), lds, s, logits, b,           \
+  hipLaunchKernelGGL((k_topk_dispatch<V>), dim3(1), dim3(64 * nwl), lds, s, logits, b,          \
                      d->param_dtype, T, E, e1, d->top_k, d->router_mode, d->norm_topk_prob,     \
                      d->routed_scaling, d->has_shared_gate, has_shared, m_blk, ids, tw,         \
                      shared_w, counts, offsets, sorted_tok, sorted_w, pair_pos, g_expert,       \
