@@ -385,7 +385,7 @@ __global__ __launch_bounds__(256) void k_expert(const ExpertParams p) {
 #define MX_LDS_RA 4
 #endif
 #ifndef MX_LDS_KM_F16
-#define MX_LDS_KM_F16 1
+#define MX_LDS_KM_F16 2
 #endif
 #ifndef MX_LDS_RB_KM2
 #define MX_LDS_RB_KM2 2
