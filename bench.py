@@ -280,10 +280,10 @@ def linear_attn_case(backend, stream, shape: syn.LinearAttnShape, tokens: tuple[
 
 def full_attn_case(backend, stream, shape: syn.FullAttnShape, tokens: tuple[int, ...],
                    steps: int, warmup: int) -> dict[str, dict]:
-    """Qwen3-Next gated full-attention block: fp16 projections, fp32 qk-norm / RoPE /
-    attention (fp32 MFMA), timed like the other cases.  Roofline of the attention kernel:
-    4 * heads * head_dim * T (T + 1) / 2 flops (QK^T and PV over the causal triangle) on
-    fp32 MFMA; of the projections: weight bytes from HBM."""
+    """Qwen3-Next gated full-attention block: fp16 projections, fp32 qk-norm / RoPE, fp16
+    K/V operands with fp32 softmax and accumulation (fp16 MFMA), timed like the other cases.
+    Roofline of the attention kernel: 4 * heads * head_dim * T (T + 1) / 2 flops (QK^T and PV
+    over the causal triangle) on fp16 MFMA; of the projections: weight bytes from HBM."""
     from moe_mi355x.full_attn import DeviceFullAttnLayer
 
     t = syn.make_full_attn_tensors(shape, SEED, weight_dtype=np.float16, param_dtype=np.float32)
@@ -337,7 +337,7 @@ def full_attn_case(backend, stream, shape: syn.FullAttnShape, tokens: tuple[int,
                 "stage_ms": {nm: round(float(v), 4) for nm, v in zip(_lib.FA_STAGE_NAMES, st)},
                 "attention": {"ms": round(st[5], 4), "flops": att_flops,
                               "TFLOPs": round(att_flops / att_s / 1e12, 2),
-                              "frac_fp32_mfma_peak": round(att_flops / att_s / MFMA_F32_PEAK, 4)},
+                              "frac_f16_mfma_peak": round(att_flops / att_s / MFMA_F16_PEAK, 4)},
                 "projections": {"ms": round(proj_s * 1e3, 4), "weight_bytes": w_bytes,
                                 "hbm_frac": round(w_bytes / proj_s / HBM_PEAK, 4),
                                 "mfma_frac": round(T * w_bytes / proj_s / MFMA_F16_PEAK, 4)},
