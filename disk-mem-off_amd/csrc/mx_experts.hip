@@ -26,6 +26,7 @@
 //   fp32 weights: EPL = 4,  four v_mfma_f32_16x16x4_f32 per chunk (A = fp32 activations)
 #include "mx_common.h"
 #include "mx_internal.h"
+#include "mx_route_dev.h"
 
 typedef __amdgpu_buffer_rsrc_t mx_rsrc_t;
 #define MX_RSRC_DW3 0x00020000
@@ -112,6 +113,13 @@ struct ExpertParams {
   int tiled;              // weights in MX_LAYOUT_FRAG16 (else row-major)
 };
 
+// One-token selection inside the gate/up launch (used in place of the top-k/dispatch
+// launch when the batch is one token): every wave of every block selects the token's
+// experts from the router logits itself, which costs less than the launch it replaces,
+// and the first wave of block (0, 0) writes the selection and the dispatch tables that
+// the down and combine launches (and the workspace views) read.
+typedef MxOneTokenSelect SelectParams;
+
 // Byte offset of the 16-byte piece lane (j, q) loads from fragment row block n16 (first
 // row, a multiple of 16 for tiled weights) at chunk 0, and the byte step per chunk.
 // Row-major: row n16 + j, column q * EPL.  MX_LAYOUT_FRAG16: 1 KiB fragment per
@@ -123,8 +131,8 @@ __device__ __forceinline__ uint32_t mx_bfrag_base(bool tiled, int n16, int j, in
                : (uint32_t)(n16 + j) * (uint32_t)K * ESZ + (uint32_t)q * EPL * ESZ;
 }
 
-template <int WF, int MT, int NBI, bool GU, int UK, int KS, bool NT>
-__global__ __launch_bounds__(256) void k_expert(const ExpertParams p) {
+template <int WF, int MT, int NBI, bool GU, int UK, int KS, bool NT, bool SEL>
+__global__ __launch_bounds__(256) void k_expert(const ExpertParams p, const SelectParams sp) {
   using Tr = WTr<WF>;
   constexpr int EPL = Tr::EPL, ESZ = Tr::ESZ, AESZ = Tr::AESZ, AV = Tr::AV;
   constexpr int KC = 4 * EPL;          // reduction columns per chunk (per wave)
@@ -135,12 +143,48 @@ __global__ __launch_bounds__(256) void k_expert(const ExpertParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int slab = wave / KS, ks = wave % KS;
   const int mt = blockIdx.x;
-  if (mt >= *p.n_mtiles) return;
-  const int g = p.mt_group[mt];
-  const int row0 = p.mt_row0[mt];
-  const int eid = p.g_expert[g];
-  const int gstart = p.g_start[g];
-  const int gcount = p.g_count[g];
+  int row0, eid, gstart, gcount;
+  if constexpr (SEL) {
+    // One token: tile 0 is the shared expert (when there is one), tile S0 + r the r-th
+    // chosen expert in ascending id; each is a group of the token's single row.
+    static_assert(GU && MT == 1, "selection runs in the one-token gate/up launch");
+    const MxSel sel = mx_topk_select<MX_SEL_VPT>(sp.logits, 1, 1, 0, sp.bias, sp.pdt, p.E, sp.E1,
+                                                 sp.k, sp.mode, sp.norm, sp.scaling);
+    if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0) {
+      const float gsh = mx_shared_gate(sp.logits, 1, 1, 0, p.E, sp.E1, sp.has_seg);
+      if (lane < sp.k) {
+        sp.ids[lane] = sel.id;
+        sp.tw[lane] = sel.w;
+      }
+      if (lane == 0 && sp.shared_w) sp.shared_w[0] = gsh;
+      mx_dispatch_one_token(sel.id, sel.w, sp.shared_w ? gsh : 1.f, sp.k, p.E, sp.has_shared,
+                            sp.counts, sp.offsets, sp.sorted_tok, sp.sorted_w, sp.pair_pos,
+                            sp.g_expert, sp.g_start, sp.g_count, sp.n_groups, sp.mt_group,
+                            sp.mt_row0, sp.n_mtiles);
+    }
+    const int S0 = sp.has_shared;
+    if (mt >= sp.k + S0) return;
+    if (mt < S0) {
+      eid = p.E;
+      gstart = sp.k;
+    } else {
+      const int id = lane < sp.k ? sel.id : 0x7fffffff;
+      int rank = 0;
+      for (int i = 0; i < sp.k; ++i) rank += __builtin_amdgcn_readlane(id, i) < id ? 1 : 0;
+      const unsigned long long hit = __ballot(lane < sp.k && rank == mt - S0);
+      eid = __builtin_amdgcn_readlane(id, __builtin_ctzll(hit));
+      gstart = mt - S0;
+    }
+    row0 = 0;
+    gcount = 1;
+  } else {
+    if (mt >= *p.n_mtiles) return;
+    const int g = p.mt_group[mt];
+    row0 = p.mt_row0[mt];
+    eid = p.g_expert[g];
+    gstart = p.g_start[g];
+    gcount = p.g_count[g];
+  }
   const bool sh = eid == p.E;
   const int N = sh ? p.N_s : p.N_r;
   const int K = sh ? p.K_s : p.K_r;
@@ -169,7 +213,7 @@ __global__ __launch_bounds__(256) void k_expert(const ExpertParams p) {
     const int m = 16 * mi + j;
     if (m < mrows) {
       const int r = gstart + row0 + m;
-      const int arow = GU ? p.sorted_tok[r] : r;
+      const int arow = SEL ? 0 : (GU ? p.sorted_tok[r] : r);
       aoff[mi] = (uint32_t)arow * (uint32_t)p.lda * AESZ + q * EPL * AESZ;
     } else {
       aoff[mi] = MX_OOB;
@@ -682,15 +726,26 @@ static int decode_ksplit(bool gu, long waves_unsplit) {
   return waves_unsplit < 2048 ? 4 : (waves_unsplit < 4096 ? 2 : 1);
 }
 
-template <int WF, int MT, bool GU, int KS>
-static void launch_expert_ks(const ExpertParams& p, int mt_max, int nmax, hipStream_t s) {
+template <int WF, int MT, bool GU, int KS, bool SEL = false>
+static void launch_expert_ks(const ExpertParams& p, int mt_max, int nmax, hipStream_t s,
+                             const SelectParams& sp = SelectParams{}) {
   constexpr int NBI = GU ? MX_DEC_NBI_GU : MX_DEC_NBI_DN;
   constexpr int UK = (WF == MX_DT_I8) ? (MT >= 4 ? 1 : MX_DEC_UK / 2)
                                       : (MT >= 4 ? 2 : MX_DEC_UK);
   constexpr bool NT = !(WF == MX_DT_I8 && GU && MT == 1 && KS == 1);
   const dim3 grid(mt_max, mx_ceil_div(nmax, (4 / KS) * 16 * NBI));
   mx_clear_error();
-  hipLaunchKernelGGL((k_expert<WF, MT, NBI, GU, UK, KS, NT>), grid, dim3(256), 0, s, p);
+  hipLaunchKernelGGL((k_expert<WF, MT, NBI, GU, UK, KS, NT, SEL>), grid, dim3(256), 0, s, p, sp);
+}
+
+template <int WF>
+static void launch_gate_up_select(const ExpertParams& p, const SelectParams& sp, int mt_max,
+                                  int nmax, hipStream_t s) {
+  const long waves = (long)mt_max * mx_ceil_div(nmax, 4 * 16 * MX_DEC_NBI_GU) * 4;
+  const int ks = decode_ksplit(true, waves);
+  if (ks == 4) return launch_expert_ks<WF, 1, true, 4, true>(p, mt_max, nmax, s, sp);
+  if (ks == 2) return launch_expert_ks<WF, 1, true, 2, true>(p, mt_max, nmax, s, sp);
+  launch_expert_ks<WF, 1, true, 1, true>(p, mt_max, nmax, s, sp);
 }
 
 template <int WF, int MT, bool GU>
@@ -838,6 +893,44 @@ extern "C" int mx_expert_gate_up(const MxMoeDesc* desc, const MxExpertPtrs* expe
   p.K_s = desc->hidden;
   p.tiled = desc->weight_layout == MX_LAYOUT_FRAG16;
   return launch_grouped<true>(desc, p, tokens, m_blk, p.ldo, (hipStream_t)stream);
+}
+
+int mx_expert_gate_up_select(const MxMoeDesc* desc, const MxExpertPtrs* experts, const void* a,
+                             void* act, const MxOneTokenSelect& sp, hipStream_t s) {
+  MX_TRY(expert_check(desc));
+  if (!experts || !a || !act || !sp.logits || !sp.ids || !sp.tw || !sp.sorted_w) return MX_ERR_INVALID;
+  if (desc->n_experts > 64 * MX_SEL_VPT || desc->top_k > TK_MAXK) return MX_ERR_UNSUPPORTED;
+  if (!mx_aligned16(a) || !mx_aligned16(act)) return MX_ERR_ALIGNMENT;
+  const int aesz = desc->weight_dtype == MX_DT_F32 ? 4 : 2;
+  ExpertParams p;
+  p.experts = experts;
+  p.g_expert = sp.g_expert;
+  p.g_start = sp.g_start;
+  p.g_count = sp.g_count;
+  p.mt_group = sp.mt_group;
+  p.mt_row0 = sp.mt_row0;
+  p.n_mtiles = sp.n_mtiles;
+  p.sorted_tok = sp.sorted_tok;
+  p.a = a;
+  p.a_bytes = (uint32_t)((long)desc->hidden * aesz);
+  p.lda = desc->hidden;
+  p.out = act;
+  p.ldo = desc->inter > desc->shared_inter ? desc->inter : desc->shared_inter;
+  p.sorted_w = nullptr;
+  p.E = desc->n_experts;
+  p.N_r = desc->inter;
+  p.K_r = desc->hidden;
+  p.N_s = desc->shared_inter;
+  p.K_s = desc->hidden;
+  p.tiled = desc->weight_layout == MX_LAYOUT_FRAG16;
+  const int mt_max = desc->top_k + (desc->shared_inter > 0 ? 1 : 0);
+  switch (desc->weight_dtype) {
+    case MX_DT_F16: launch_gate_up_select<MX_DT_F16>(p, sp, mt_max, p.ldo, s); break;
+    case MX_DT_I8: launch_gate_up_select<MX_DT_I8>(p, sp, mt_max, p.ldo, s); break;
+    case MX_DT_F32: launch_gate_up_select<MX_DT_F32>(p, sp, mt_max, p.ldo, s); break;
+    default: return MX_ERR_INVALID;
+  }
+  return mx_launch_status();
 }
 
 extern "C" int mx_expert_down(const MxMoeDesc* desc, const MxExpertPtrs* experts, int32_t tokens,

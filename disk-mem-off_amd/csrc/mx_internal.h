@@ -22,12 +22,44 @@ int mx_rmsnorm_launch(const float* x, const void* norm_w, int param_dtype, float
 // top-k/dispatch kernel.  mx_router_decode_ok tells whether the shape and the pointer
 // alignment fit it; the launch returns MX_ERR_UNSUPPORTED otherwise.
 bool mx_router_decode_ok(const MxMoeDesc* d, const MxMoeWeights* w, int T, const float* x);
+// With select_later the top-k/dispatch launch is left out (the one-token gate/up launch
+// selects instead; mx_one_token_select_ok).
 int mx_router_decode_launch(const MxMoeDesc* d, const MxMoeWeights* w, int T, const float* x,
                             float* h32, void* h16, float* logits, int* ids, float* tw,
                             float* shared_w, int m_blk, int* counts, int* offsets,
                             int* sorted_tok, float* sorted_w, int* pair_pos, int* g_expert,
                             int* g_start, int* g_count, int* n_groups, int* mt_group,
-                            int* mt_row0, int* n_mtiles, hipStream_t s);
+                            int* mt_row0, int* n_mtiles, hipStream_t s,
+                            bool select_later = false);
+
+// A one-token batch whose experts are selected inside the gate/up launch (replacing the
+// decode top-k/dispatch launch; E <= 256): the router logits and routing configuration,
+// and the selection and dispatch tables the launch writes for the later stages.
+#define MX_SEL_VPT 4
+struct MxOneTokenSelect {
+  const float* logits;  // [E1] router logits of the token
+  const void* bias;
+  int pdt, E1, k, mode, norm, has_seg, has_shared;
+  float scaling;
+  int* ids;
+  float* tw;
+  float* shared_w;
+  int* counts;
+  int* offsets;
+  int* sorted_tok;
+  float* sorted_w;
+  int* pair_pos;
+  int* g_expert;
+  int* g_start;
+  int* g_count;
+  int* n_groups;
+  int* mt_group;
+  int* mt_row0;
+  int* n_mtiles;
+};
+bool mx_one_token_select_ok(const MxMoeDesc* d);
+int mx_expert_gate_up_select(const MxMoeDesc* desc, const MxExpertPtrs* experts, const void* a,
+                             void* act, const MxOneTokenSelect& sp, hipStream_t s);
 
 // Single-group tables for dense products on the grouped-GEMM kernels (device pointers).
 struct MxDenseTables {

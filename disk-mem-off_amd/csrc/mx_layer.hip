@@ -91,8 +91,19 @@ int layout(const MxMoeDesc* d, int T, void* ws, MxMoeViews* v, size_t* total,
   return MX_OK;
 }
 
+// One token, when stages 1-4 run in one call: the gate/up launch selects the experts
+// (and writes the dispatch tables), so the top-k/dispatch launch is left out.
+#ifndef MX_SELECT_IN_GATE_UP
+#define MX_SELECT_IN_GATE_UP 1
+#endif
+bool select_in_gate_up(const MxMoeDesc* d, const MxMoeWeights* w, int T, const float* x,
+                       int st_begin, int st_end) {
+  return MX_SELECT_IN_GATE_UP && T == 1 && st_begin <= 1 && st_end >= 5 &&
+         use_decode_router(d, w, T, x) && mx_one_token_select_ok(d);
+}
+
 int run_stage(int stage, const MxMoeDesc* d, const MxMoeWeights* w, const float* x, float* out,
-              int T, const MxMoeViews& v, void* scratch, hipStream_t s) {
+              int T, const MxMoeViews& v, void* scratch, hipStream_t s, bool sel1) {
   const int has_sh = d->shared_inter > 0;
   const bool decode = use_decode_router(d, w, T, x);
   if (decode && (stage == 0 || stage == 2 || stage == 3)) return MX_OK;  // in stage 1
@@ -106,7 +117,7 @@ int run_stage(int stage, const MxMoeDesc* d, const MxMoeWeights* w, const float*
         return mx_router_decode_launch(d, w, T, x, v.h32, v.h16, v.logits, v.topk_ids, v.topk_w,
                                        v.shared_w, v.m_blk, v.counts, v.offsets, v.sorted_tok,
                                        v.sorted_w, v.pair_pos, v.g_expert, v.g_start, v.g_count,
-                                       v.n_groups, v.mt_group, v.mt_row0, v.n_mtiles, s);
+                                       v.n_groups, v.mt_group, v.mt_row0, v.n_mtiles, s, sel1);
       return mx_router_logits(v.h32, w->router_w, d->has_shared_gate ? w->shared_gate_w : nullptr,
                               d->param_dtype, T, d->hidden, d->n_experts, v.router_splits,
                               v.logits, s);
@@ -127,6 +138,36 @@ int run_stage(int stage, const MxMoeDesc* d, const MxMoeWeights* w, const float*
                          v.g_expert, v.g_start, v.g_count, v.n_groups, v.mt_group, v.mt_row0,
                          v.n_mtiles, s);
     case 4:
+      if (sel1) {
+        MxOneTokenSelect sp;
+        sp.logits = v.logits;
+        sp.bias = (d->router_mode == MX_ROUTER_SOFTMAX || !d->has_bias) ? nullptr : w->bias;
+        sp.pdt = d->param_dtype;
+        sp.E1 = d->n_experts + (d->has_shared_gate ? 1 : 0);
+        sp.k = d->top_k;
+        sp.mode = d->router_mode;
+        sp.norm = d->norm_topk_prob;
+        sp.has_seg = d->has_shared_gate;
+        sp.has_shared = has_sh;
+        sp.scaling = d->routed_scaling;
+        sp.ids = v.topk_ids;
+        sp.tw = v.topk_w;
+        sp.shared_w = v.shared_w;
+        sp.counts = v.counts;
+        sp.offsets = v.offsets;
+        sp.sorted_tok = v.sorted_tok;
+        sp.sorted_w = v.sorted_w;
+        sp.pair_pos = v.pair_pos;
+        sp.g_expert = v.g_expert;
+        sp.g_start = v.g_start;
+        sp.g_count = v.g_count;
+        sp.n_groups = v.n_groups;
+        sp.mt_group = v.mt_group;
+        sp.mt_row0 = v.mt_row0;
+        sp.n_mtiles = v.n_mtiles;
+        return mx_expert_gate_up_select(
+            d, w->experts, d->weight_dtype == MX_DT_F32 ? (const void*)v.h32 : v.h16, v.act, sp, s);
+      }
       return mx_expert_gate_up(d, w->experts, T,
                                d->weight_dtype == MX_DT_F32 ? (const void*)v.h32 : v.h16,
                                v.sorted_tok, v.g_expert, v.g_start, v.g_count, v.mt_group,
@@ -155,9 +196,10 @@ int forward(const MxMoeDesc* d, const MxMoeWeights* w, const float* x, float* ou
   void* scratch = nullptr;
   MX_TRY(layout(d, T, ws, &v, &need, &scratch));
   if (ws_bytes < need) return MX_ERR_WORKSPACE;
+  const bool sel1 = select_in_gate_up(d, w, T, x, st_begin, st_end);
   for (int st = st_begin; st < st_end; ++st) {
     if (events) MX_TRY(mx_status(hipEventRecord((hipEvent_t)events[st], s)));
-    MX_TRY(run_stage(st, d, w, x, out, T, v, scratch, s));
+    MX_TRY(run_stage(st, d, w, x, out, T, v, scratch, s, sel1));
   }
   if (events) MX_TRY(mx_status(hipEventRecord((hipEvent_t)events[MX_N_STAGES], s)));
   return MX_OK;

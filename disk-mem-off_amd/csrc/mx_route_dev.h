@@ -8,13 +8,19 @@
 
 #define TK_MAXK 32
 
+// The selection of one token by one wave: lane r < k holds slot r's expert id and its
+// final weight (renormalised and scaled as configured).
+struct MxSel {
+  int id;
+  float w;
+};
+
 // One wave selects the experts of token t (logits summed over S H-slices).
 template <int VPT>
-__device__ __forceinline__ void mx_topk_token(
-    const float* __restrict__ logits, int S, int T, int t, const void* __restrict__ bias,
-    int pdt, int E, int E1, int k, int mode, int norm, float scaling, int has_seg,
-    int* __restrict__ ids, float* __restrict__ tw, float* __restrict__ shared_w,
-    int* lds_ids = nullptr, float* lds_w = nullptr, float* lds_sw = nullptr) {
+__device__ __forceinline__ MxSel mx_topk_select(const float* __restrict__ logits, int S, int T,
+                                                int t, const void* __restrict__ bias, int pdt,
+                                                int E, int E1, int k, int mode, int norm,
+                                                float scaling) {
   const int lane = threadIdx.x & 63;
   // All logit and bias loads first, at clamped indices, so they are in flight together.
   float lg[VPT], bs[VPT];
@@ -136,26 +142,92 @@ __device__ __forceinline__ void mx_topk_token(
   mx_lds_fence();  // the row is reused by this wave's next token
   float sum = 0.f;  // sequential over the k slots, identical on every lane
   for (int r = 0; r < k; ++r) sum += mx_readlane(my_w, r);
+  return MxSel{my_id, (norm ? my_w / (sum + 1e-20f) : my_w) * scaling};
+}
+
+// Weight of the shared expert's row: sigmoid of the shared-gate logit (Qwen3-Next), else 1.
+__device__ __forceinline__ float mx_shared_gate(const float* __restrict__ logits, int S, int T,
+                                                int t, int E, int E1, int has_seg) {
+  float g = 1.f;
+  if (has_seg) {
+    float l = 0.f;
+    for (int s = 0; s < S; ++s) l += logits[((size_t)s * T + t) * E1 + E];
+    g = mx_sigmoid(l);
+  }
+  return g;
+}
+
+// One wave selects token t and writes its ids / weights (and the shared weight).
+template <int VPT>
+__device__ __forceinline__ void mx_topk_token(
+    const float* __restrict__ logits, int S, int T, int t, const void* __restrict__ bias,
+    int pdt, int E, int E1, int k, int mode, int norm, float scaling, int has_seg,
+    int* __restrict__ ids, float* __restrict__ tw, float* __restrict__ shared_w,
+    int* lds_ids = nullptr, float* lds_w = nullptr, float* lds_sw = nullptr) {
+  const int lane = threadIdx.x & 63;
+  const MxSel sel = mx_topk_select<VPT>(logits, S, T, t, bias, pdt, E, E1, k, mode, norm, scaling);
   if (lane < k) {
-    const float w = (norm ? my_w / (sum + 1e-20f) : my_w) * scaling;
-    ids[(size_t)t * k + lane] = my_id;
-    tw[(size_t)t * k + lane] = w;
+    ids[(size_t)t * k + lane] = sel.id;
+    tw[(size_t)t * k + lane] = sel.w;
     if (lds_ids) {
-      lds_ids[t * k + lane] = my_id;
-      lds_w[t * k + lane] = w;
+      lds_ids[t * k + lane] = sel.id;
+      lds_w[t * k + lane] = sel.w;
     }
   }
-  if (lane == 0) {
-    if (shared_w) {
-      float g = 1.f;
-      if (has_seg) {
-        float l = 0.f;
-        for (int s = 0; s < S; ++s) l += logits[((size_t)s * T + t) * E1 + E];
-        g = mx_sigmoid(l);
-      }
-      shared_w[t] = g;
-      if (lds_sw) lds_sw[t] = g;
+  if (lane == 0 && shared_w) {
+    const float g = mx_shared_gate(logits, S, T, t, E, E1, has_seg);
+    shared_w[t] = g;
+    if (lds_sw) lds_sw[t] = g;
+  }
+}
+
+// Dispatch tables of a one-token batch, written by the wave that selected it (lane r < k
+// holds slot r's id and weight): every chosen expert is a group of one row, groups in
+// ascending expert id (the order of the general dispatch), the shared expert's row last
+// and its group and tile first.
+__device__ __forceinline__ void mx_dispatch_one_token(
+    int my_id, float my_w, float shared_gate, int k, int E, int has_shared,
+    int* __restrict__ counts, int* __restrict__ offsets, int* __restrict__ sorted_tok,
+    float* __restrict__ sorted_w, int* __restrict__ pair_pos, int* __restrict__ g_expert,
+    int* __restrict__ g_start, int* __restrict__ g_count, int* __restrict__ n_groups,
+    int* __restrict__ mt_group, int* __restrict__ mt_row0, int* __restrict__ n_mtiles) {
+  const int lane = threadIdx.x & 63;
+  const int G0 = has_shared ? 1 : 0, S0 = has_shared ? 1 : 0;
+  const int id = lane < k ? my_id : 0x7fffffff;
+  int rank = 0;
+  for (int i = 0; i < k; ++i) rank += __builtin_amdgcn_readlane(id, i) < id ? 1 : 0;
+  if (lane < k) {
+    sorted_tok[rank] = 0;
+    sorted_w[rank] = my_w;
+    pair_pos[lane] = rank;
+    g_expert[G0 + rank] = id;
+    g_start[G0 + rank] = rank;
+    g_count[G0 + rank] = 1;
+    mt_group[S0 + rank] = G0 + rank;
+    mt_row0[S0 + rank] = 0;
+  }
+  for (int e = lane; e <= E; e += 64) {
+    int below = 0, hit = 0;
+    for (int i = 0; i < k; ++i) {
+      const int x = __builtin_amdgcn_readlane(id, i);
+      below += x < e ? 1 : 0;
+      hit |= x == e ? 1 : 0;
     }
+    if (e < E) counts[e] = hit;
+    offsets[e] = below;
+  }
+  if (lane == 0) {
+    if (has_shared) {
+      g_expert[0] = E;
+      g_start[0] = k;
+      g_count[0] = 1;
+      mt_group[0] = 0;
+      mt_row0[0] = 0;
+      sorted_tok[k] = 0;
+      sorted_w[k] = shared_gate;
+    }
+    *n_groups = G0 + k;
+    *n_mtiles = S0 + k;
   }
 }
 

@@ -452,50 +452,14 @@ __global__ __launch_bounds__(VPT > 8 ? 512 : 1024) void k_topk_dispatch(
                          ids, tw, shared_w, sid, sw, ssw);
   }
   if (T == 1) {
-    // One token: wave 0 selected it and writes the tables directly — every chosen expert
-    // is a group of one row, groups in ascending expert id (the order of the general
-    // dispatch), the shared expert's row and group first among tiles.
+    // One token: wave 0 selected it and writes the tables directly.
     if (threadIdx.x >= 64) return;
     mx_lds_fence();
     const int lane = threadIdx.x;
-    const int G0 = has_shared ? 1 : 0, S0 = has_shared ? 1 : 0;
-    const int my_id = lane < k ? sid[lane] : 0x7fffffff;
-    const float my_w = lane < k ? sw[lane] : 0.f;
-    int rank = 0;
-    for (int i = 0; i < k; ++i) rank += __builtin_amdgcn_readlane(my_id, i) < my_id ? 1 : 0;
-    if (lane < k) {
-      sorted_tok[rank] = 0;
-      sorted_w[rank] = my_w;
-      pair_pos[lane] = rank;
-      g_expert[G0 + rank] = my_id;
-      g_start[G0 + rank] = rank;
-      g_count[G0 + rank] = 1;
-      mt_group[S0 + rank] = G0 + rank;
-      mt_row0[S0 + rank] = 0;
-    }
-    for (int e = lane; e <= E; e += 64) {
-      int below = 0, hit = 0;
-      for (int i = 0; i < k; ++i) {
-        const int id = __builtin_amdgcn_readlane(my_id, i);
-        below += id < e ? 1 : 0;
-        hit |= id == e ? 1 : 0;
-      }
-      if (e < E) counts[e] = hit;
-      offsets[e] = below;
-    }
-    if (lane == 0) {
-      if (has_shared) {
-        g_expert[0] = E;
-        g_start[0] = k;
-        g_count[0] = 1;
-        mt_group[0] = 0;
-        mt_row0[0] = 0;
-        sorted_tok[k] = 0;
-        sorted_w[k] = shared_w ? ssw[0] : 1.f;
-      }
-      *n_groups = G0 + k;
-      *n_mtiles = S0 + k;
-    }
+    mx_dispatch_one_token(lane < k ? sid[lane] : 0, lane < k ? sw[lane] : 0.f,
+                          shared_w ? ssw[0] : 1.f, k, E, has_shared, counts, offsets, sorted_tok,
+                          sorted_w, pair_pos, g_expert, g_start, g_count, n_groups, mt_group,
+                          mt_row0, n_mtiles);
     return;
   }
   mx_lds_sync();
@@ -511,6 +475,10 @@ static size_t decode_lds_bytes(const MxMoeDesc* d, int T) {
   return mx_dispatch_small_lds_bytes(d->n_experts) + (size_t)T * d->top_k * 8 + (size_t)T * 4;
 }
 
+bool mx_one_token_select_ok(const MxMoeDesc* d) {
+  return d->n_experts <= 64 * MX_SEL_VPT && d->top_k <= TK_MAXK;
+}
+
 bool mx_router_decode_ok(const MxMoeDesc* d, const MxMoeWeights* w, int T, const float* x) {
   const uintptr_t walign = d->param_dtype == MX_DT_F16 ? 7u : 15u;
   return T >= 1 && T <= 64 && d->n_experts <= 1024 && d->top_k <= MX_DISPATCH_MAXK &&
@@ -523,11 +491,12 @@ int mx_router_decode_launch(const MxMoeDesc* d, const MxMoeWeights* w, int T, co
                             float* shared_w, int m_blk, int* counts, int* offsets,
                             int* sorted_tok, float* sorted_w, int* pair_pos, int* g_expert,
                             int* g_start, int* g_count, int* n_groups, int* mt_group,
-                            int* mt_row0, int* n_mtiles, hipStream_t s) {
+                            int* mt_row0, int* n_mtiles, hipStream_t s, bool select_later) {
   const int E = d->n_experts, H = d->hidden;
   const int e1 = E + (d->has_shared_gate ? 1 : 0);
   const int has_shared = d->shared_inter > 0;
   if (!mx_router_decode_ok(d, w, T, x)) return MX_ERR_UNSUPPORTED;
+  if (select_later && !(T == 1 && mx_one_token_select_ok(d))) return MX_ERR_INVALID;
   const int vpt = mx_ceil_div(E, 64);
   const int nw = vpt > 8 ? 8 : 16;
   const size_t lds = decode_lds_bytes(d, T);
@@ -552,6 +521,7 @@ int mx_router_decode_launch(const MxMoeDesc* d, const MxMoeWeights* w, int T, co
 #undef RL_TT
 #undef RL_LAUNCH
   MX_TRY(mx_launch_status());
+  if (select_later) return MX_OK;
   // One token with a single-wave selection needs one wave only.
   const int nwl = (T == 1 && vpt < 6) ? 1 : nw;
 #define TD_LAUNCH(V)                                                                           \
