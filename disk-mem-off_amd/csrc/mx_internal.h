@@ -33,9 +33,12 @@ int mx_router_decode_launch(const MxMoeDesc* d, const MxMoeWeights* w, int T, co
                             bool select_later = false);
 
 // A one-token batch whose experts are selected inside the gate/up launch (replacing the
-// decode top-k/dispatch launch; E <= 256): the router logits and routing configuration,
-// and the selection and dispatch tables the launch writes for the later stages.
-#define MX_SEL_VPT 4
+// decode top-k/dispatch launch; E <= MX_SEL_MAX_E): the router logits and routing
+// configuration, and the selection and dispatch tables the launch writes for the later
+// stages.
+#ifndef MX_SEL_MAX_E
+#define MX_SEL_MAX_E 512
+#endif
 struct MxOneTokenSelect {
   const float* logits;  // [E1] router logits of the token
   const void* bias;

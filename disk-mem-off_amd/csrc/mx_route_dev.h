@@ -257,57 +257,83 @@ __device__ __forceinline__ uint32_t mx_key_image(float kv, bool valid) {
   return valid ? ((b & 0x80000000u) ? ~b : (b | 0x80000000u)) : 0u;
 }
 
-// Phase 1, by wave `wv` < T * NP of the block: candidates of token wv / NP.
+// Phase 1, by wave `wv` < T * NP of the block: candidates of token wv / NP.  A part holds
+// 64 * VPC consecutive experts (VPC per lane, lane-major within each 64).
+template <int VPC = 1>
 __device__ __forceinline__ void mx_topk_par_cand(MxTopkPar& sh, const float* __restrict__ logits,
                                                  const void* __restrict__ bias, int pdt, int E,
                                                  int E1, int k, int mode, int NP, int wv) {
   const int lane = threadIdx.x & 63;
   const int t = wv / NP, part = wv - t * NP;
-  const int e = part * 64 + lane;
-  const bool valid = e < E;
-  const int ec = min(e, E - 1);
-  const float l = logits[(size_t)t * E1 + ec];
-  float b = 0.f;
-  if (bias) b = pdt == MX_DT_F16 ? (float)((const half_t*)bias)[ec] : ((const float*)bias)[ec];
-  float key, wsrc;
-  if (mode == MX_ROUTER_SIGMOID_SELECT_BIAS) {
-    wsrc = mx_sigmoid(l);
-    key = valid ? wsrc + b : -INFINITY;
-  } else {
-    key = valid ? ((mode == MX_ROUTER_REF_SOFTMAX_BIAS) ? l + b : l) : -INFINITY;
-    wsrc = key;
-    const float m = mx_wave_max(key);
-    const float s = mx_wave_sum(valid ? expf(key - m) : 0.f);
-    if (lane == 0) {
-      sh.m[wv] = m;
-      sh.sm[wv] = s;
+  bool valid[VPC];
+  float key[VPC], wsrc[VPC];
+#pragma unroll
+  for (int i = 0; i < VPC; ++i) {
+    const int e = part * 64 * VPC + 64 * i + lane;
+    valid[i] = e < E;
+    const int ec = min(e, E - 1);
+    const float l = logits[(size_t)t * E1 + ec];
+    float b = 0.f;
+    if (bias) b = pdt == MX_DT_F16 ? (float)((const half_t*)bias)[ec] : ((const float*)bias)[ec];
+    if (mode == MX_ROUTER_SIGMOID_SELECT_BIAS) {
+      wsrc[i] = mx_sigmoid(l);
+      key[i] = valid[i] ? wsrc[i] + b : -INFINITY;
+    } else {
+      key[i] = valid[i] ? ((mode == MX_ROUTER_REF_SOFTMAX_BIAS) ? l + b : l) : -INFINITY;
+      wsrc[i] = key[i];
     }
   }
-  const uint32_t u = mx_key_image(key, valid);
+  if (mode != MX_ROUTER_SIGMOID_SELECT_BIAS) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < VPC; ++i) mx = fmaxf(mx, key[i]);
+    const float m = mx_wave_max(mx);
+    float ls = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPC; ++i) ls += valid[i] ? expf(key[i] - m) : 0.f;
+    const float sm = mx_wave_sum(ls);
+    if (lane == 0) {
+      sh.m[wv] = m;
+      sh.sm[wv] = sm;
+    }
+  }
+  uint32_t u[VPC];
+#pragma unroll
+  for (int i = 0; i < VPC; ++i) u[i] = mx_key_image(key[i], valid[i]);
   uint32_t tau = 0;
   for (int bit = 31; bit >= 0; --bit) {
     const uint32_t cand = tau | (1u << bit);
-    if (__popcll(__builtin_amdgcn_uicmp(u, cand, 35 /* uge */)) >= k) tau = cand;
+    int c = 0;
+#pragma unroll
+    for (int i = 0; i < VPC; ++i) c += __popcll(__builtin_amdgcn_uicmp(u[i], cand, 35 /* uge */));
+    if (c >= k) tau = cand;
   }
   const unsigned long long below = (1ull << lane) - 1ull;
-  const int ngt = __popcll(__ballot(u > tau));
-  const unsigned long long eq = __ballot(u == tau);
-  const bool sel = u > tau || (u == tau && __popcll(eq & below) < k - ngt);
-  if (sel) {
-    const int slot = t * NP * k + part * k + __popcll(__ballot(sel) & below);
-    sh.u[slot] = u;
-    sh.id[slot] = e;
-    sh.w[slot] = wsrc;
+  int ngt = 0;
+#pragma unroll
+  for (int i = 0; i < VPC; ++i) ngt += __popcll(__ballot(u[i] > tau));
+  int ties = 0, ahead = 0;
+#pragma unroll
+  for (int i = 0; i < VPC; ++i) {
+    const unsigned long long eq = __ballot(u[i] == tau);
+    const bool sel = u[i] > tau || (u[i] == tau && ties + __popcll(eq & below) < k - ngt);
+    ties += __popcll(eq);
+    const unsigned long long sm = __ballot(sel);
+    if (sel) {
+      const int slot = t * NP * k + part * k + ahead + __popcll(sm & below);
+      sh.u[slot] = u[i];
+      sh.id[slot] = part * 64 * VPC + 64 * i + lane;
+      sh.w[slot] = wsrc[i];
+    }
+    ahead += __popcll(sm);
   }
 }
 
-// Phase 2, by one wave per token (after a workgroup LDS sync): the token's top-k.
+// Phase 2, by one wave per token (after a workgroup LDS sync): the token's top-k, returned
+// like mx_topk_select (lane r < k: slot r's id and final weight).
 template <int VC>
-__device__ __forceinline__ void mx_topk_par_final(
-    const MxTopkPar& sh, const float* __restrict__ logits, int t, int E, int E1, int k,
-    int mode, int norm, float scaling, int NP, int has_seg, int* __restrict__ ids,
-    float* __restrict__ tw, float* __restrict__ shared_w, int* lds_ids, float* lds_w,
-    float* lds_sw) {
+__device__ __forceinline__ MxSel mx_topk_par_select(const MxTopkPar& sh, int t, int k, int mode,
+                                                    int norm, float scaling, int NP) {
   const int lane = threadIdx.x & 63;
   const int C = NP * k, c0 = t * C;
   uint32_t u[VC];
@@ -378,14 +404,26 @@ __device__ __forceinline__ void mx_topk_par_final(
   mx_lds_fence();
   const int my_id = lane < k ? s_id[wv][lane] : 0;
   const float my_w = lane < k ? s_w[wv][lane] : 0.f;
+  mx_lds_fence();  // the row is reused by this wave's next call
   float sum = 0.f;  // sequential over the k slots, identical on every lane
   for (int r = 0; r < k; ++r) sum += mx_readlane(my_w, r);
+  return MxSel{my_id, (norm ? my_w / (sum + 1e-20f) : my_w) * scaling};
+}
+
+// Phase 2 with the results written out (ids / weights / shared weight, global and LDS).
+template <int VC>
+__device__ __forceinline__ void mx_topk_par_final(
+    const MxTopkPar& sh, const float* __restrict__ logits, int t, int E, int E1, int k,
+    int mode, int norm, float scaling, int NP, int has_seg, int* __restrict__ ids,
+    float* __restrict__ tw, float* __restrict__ shared_w, int* lds_ids, float* lds_w,
+    float* lds_sw) {
+  const int lane = threadIdx.x & 63;
+  const MxSel sel = mx_topk_par_select<VC>(sh, t, k, mode, norm, scaling, NP);
   if (lane < k) {
-    const float w = (norm ? my_w / (sum + 1e-20f) : my_w) * scaling;
-    ids[(size_t)t * k + lane] = my_id;
-    tw[(size_t)t * k + lane] = w;
-    lds_ids[t * k + lane] = my_id;
-    lds_w[t * k + lane] = w;
+    ids[(size_t)t * k + lane] = sel.id;
+    tw[(size_t)t * k + lane] = sel.w;
+    lds_ids[t * k + lane] = sel.id;
+    lds_w[t * k + lane] = sel.w;
   }
   if (lane == 0 && shared_w) {
     const float g = has_seg ? mx_sigmoid(logits[(size_t)t * E1 + E]) : 1.f;

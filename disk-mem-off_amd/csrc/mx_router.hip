@@ -476,7 +476,7 @@ static size_t decode_lds_bytes(const MxMoeDesc* d, int T) {
 }
 
 bool mx_one_token_select_ok(const MxMoeDesc* d) {
-  return d->n_experts <= 64 * MX_SEL_VPT && d->top_k <= TK_MAXK;
+  return d->n_experts <= MX_SEL_MAX_E && d->n_experts <= 512 && d->top_k <= TK_MAXK;
 }
 
 bool mx_router_decode_ok(const MxMoeDesc* d, const MxMoeWeights* w, int T, const float* x) {
