@@ -240,6 +240,72 @@ def test_many_experts_ties_match_single_wave_selection(mi355x, stream):
         np.testing.assert_allclose(v8["w"][r], v1["w"][0], rtol=1e-6, atol=1e-7)
 
 
+# ---- one token: the experts are selected inside the gate/up launch ------------------------
+
+@pytest.mark.parametrize("E,k,mode,shared", [
+    (512, 32, orc.REF_SOFTMAX_BIAS, True),    # 4 waves x 128 experts, 128 candidates
+    (300, 32, orc.SIGMOID_SELECT_BIAS, True),
+    (257, 4, orc.SIGMOID_SELECT_BIAS, False),  # first size past one wave's 256 experts
+    (256, 16, orc.SOFTMAX, True),              # one wave, 4 experts per lane
+    (9, 8, orc.REF_SOFTMAX_BIAS, False),       # one expert more than top-k
+])
+def test_one_token_selection_edges(mi355x, stream, E, k, mode, shared):
+    say(f"[gpu] one token E={E} k={k} mode={mode} shared={shared}")
+    qwen = mode == orc.SOFTMAX
+    shape = syn.MoeShape(syn.QWEN if qwen else syn.GLM, 256, E, k, 64, 64 if shared else 0,
+                         1.0 if qwen else 2.5, 1e-6, has_bias=not qwen,
+                         has_shared_gate=qwen and shared)
+    t = syn.make_tensors(shape, 300 + E + k)
+    x = syn.make_inputs(301 + E, 1, shape.hidden)
+    spec = spec_for(shape, mode)
+    out, views = run_device(mi355x, stream, t, shape, spec, x)
+    ref = orc.moe_block(x, t, spec)
+    check_routing(views, ref, ref["logits"], t.get("mlp.gate.e_score_correction_bias"), spec,
+                  f"one token E{E}/k{k}/{mode}")
+    assert views["n_groups"] == k + (1 if shared else 0)
+    assert views["n_mtiles"] == k + (1 if shared else 0)
+    assert normwise_err(out, ref["out"]) <= FP32_REL
+
+
+@pytest.mark.parametrize("E,k,mode", [(160, 8, orc.SIGMOID_SELECT_BIAS),
+                                      (512, 10, orc.SOFTMAX)])
+def test_one_token_split_stages_match_one_call(mi355x, stream, E, k, mode):
+    """The staged entry (stages 0-3, then 4-6, as the expert-granular runtime calls it) keeps
+    the top-k/dispatch launch; one call selects inside the gate/up launch.  Same ids and
+    dispatch tables, outputs equal to fp32 rounding."""
+    say(f"[gpu] one token, staged vs one call, E={E}")
+    qwen = mode == orc.SOFTMAX
+    shape = syn.MoeShape(syn.QWEN if qwen else syn.GLM, 256, E, k, 64, 64,
+                         1.0 if qwen else 2.5, 1e-6, has_bias=not qwen, has_shared_gate=qwen)
+    t = syn.make_tensors(shape, 400 + E)
+    x = syn.make_inputs(401 + E, 1, shape.hidden)
+    spec = spec_for(shape, mode)
+    dl = DeviceMoeLayer.from_host(mi355x, t, stream)
+    try:
+        cfg = dl.config(top_k=k, router_mode=MODE_CODE[mode], routed_scaling=spec.routed_scaling,
+                        eps=spec.eps, norm_topk_prob=spec.norm_topk_prob)
+        desc = cfg.desc()
+
+        def tables():
+            v = dl.runner.views(desc, 1)
+            return [read_device(mi355x, p, np.int32, n, stream) for p, n in
+                    ((v.topk_ids, k), (v.sorted_tok, k + 1), (v.pair_pos, k),
+                     (v.g_expert, k + 1), (v.g_start, k + 1), (v.mt_group, k + 1))]
+
+        one = dl.forward_numpy(cfg, x)
+        t_one = tables()
+        w = dl.prepare(cfg, 1)
+        used = dl.runner.route_numpy(desc, w, x, stream)
+        staged = dl.runner.finish_numpy(desc, w, stream)
+        t_staged = tables()
+    finally:
+        dl.close()
+    assert used == sorted(int(e) for e in t_one[0])
+    for a, b in zip(t_one, t_staged):
+        assert np.array_equal(a, b)
+    np.testing.assert_allclose(staged, one, rtol=1e-5, atol=1e-6)
+
+
 # ---- error paths through the ABI ----------------------------------------------------------
 
 def test_forward_rejects_bad_arguments(mi355x, stream):
