@@ -107,8 +107,10 @@ extern "C" int mx_rmsnorm(const float* x, const void* norm_w, int32_t param_dtyp
 
 // ------------------------------------------------------------------------------------
 // Router logits on fp32 MFMA (v_mfma_f32_16x16x4_f32: full fp32 products and sums).
-// Block = 4 waves over a 64-token x 64-expert tile; wave w takes the 32 x 32 quarter
-// (tokens (w & 1) * 32.., experts (w >> 1) * 32..), i.e. 2 x 2 fragments of 16 x 16.
+// Block = 4 waves over a 256-token x 32-expert tile; wave w takes tokens w * 64.. and
+// the block's 32 experts, i.e. 4 x 2 fragments of 16 x 16.  (Measured on MI355X against
+// 2 x 2 fragments per wave over 64 x 64 tiles: Qwen3-Next 4096 tokens 154 -> 133 us,
+// GLM-4.7 2048 tokens 76 -> 63 us; wider expert tiles or deeper load batches were slower.)
 // Row e == E is the Qwen3-Next shared-expert gate (qwen3_next.py:328), which rides along
 // as an extra "expert".  Grid z splits H into slices; out[s][t][e] holds the partial sum
 // of slice s and the top-k kernel adds the slices in ascending order, so the result does
@@ -134,56 +136,76 @@ __device__ __forceinline__ float4 rt_load4<half_t>(const half_t* p) {
   return make_float4((float)v[0], (float)v[1], (float)v[2], (float)v[3]);
 }
 
-#define RM_UK 4  // chunks per load batch
+#ifndef RM_UK
+#define RM_UK 1  // chunks per load batch (two batches in flight)
+#endif
+// Block shape: each wave computes RT_FA x RT_FB fragments of 16 x 16 (tokens x experts);
+// the 4 waves of a block are RT_WA along tokens by 4 / RT_WA along experts.
+#ifndef RT_FA
+#define RT_FA 4
+#endif
+#ifndef RT_FB
+#define RT_FB 2
+#endif
+#ifndef RT_WA
+#define RT_WA 4
+#endif
+constexpr int RT_BT = 16 * RT_FA * RT_WA;        // tokens per block
+constexpr int RT_BE = 16 * RT_FB * (4 / RT_WA);  // experts per block
+
+#ifndef RT_WPE
+#define RT_WPE 4  // waves per SIMD the prefill router is compiled for
+#endif
 
 template <typename WT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, RT_WPE))) void
 k_router_logits(const float* __restrict__ h32, const WT* __restrict__ wr,
                 const WT* __restrict__ wseg, int T, int H, int E, int E1, int kslice,
                 float* __restrict__ out) {
+  constexpr int FA = RT_FA, FB = RT_FB;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane & 15, q = lane >> 4;
-  const int t0 = blockIdx.x * 64 + (wave & 1) * 32;
-  const int e0 = blockIdx.y * 64 + (wave >> 1) * 32;
+  const int t0 = blockIdx.x * RT_BT + (wave % RT_WA) * 16 * FA;
+  const int e0 = blockIdx.y * RT_BE + (wave / RT_WA) * 16 * FB;
   const int s = blockIdx.z;
   const int kb = s * kslice, ke = min(H, kb + kslice);
   if (kb >= ke) return;
-  const float* arow[2];
-  const WT* brow[2];
+  const float* arow[FA];
+  const WT* brow[FB];
 #pragma unroll
-  for (int a = 0; a < 2; ++a) arow[a] = h32 + (size_t)min(t0 + 16 * a + j, T - 1) * H;
+  for (int a = 0; a < FA; ++a) arow[a] = h32 + (size_t)min(t0 + 16 * a + j, T - 1) * H;
 #pragma unroll
-  for (int b = 0; b < 2; ++b) {
+  for (int b = 0; b < FB; ++b) {
     const int e = e0 + 16 * b + j;
     brow[b] = e < E ? wr + (size_t)e * H : ((e == E && wseg) ? wseg : wr + (size_t)(E - 1) * H);
   }
-  float4_t acc[2][2];
+  float4_t acc[FA][FB];
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int a = 0; a < FA; ++a)
 #pragma unroll
-    for (int b = 0; b < 2; ++b) acc[a][b] = (float4_t){0.f, 0.f, 0.f, 0.f};
+    for (int b = 0; b < FB; ++b) acc[a][b] = (float4_t){0.f, 0.f, 0.f, 0.f};
 
   const int nch = (ke - kb + 15) / 16;
-  auto load = [&](int c, float4 (&av)[2], float4 (&bv)[2]) {
+  auto load = [&](int c, float4 (&av)[FA], float4 (&bv)[FB]) {
     const int k = kb + 16 * c + 4 * q;
     const bool in = k < ke;
     const int kk = in ? k : ke - 4;  // clamped in bounds, masked below
 #pragma unroll
-    for (int a = 0; a < 2; ++a) {
+    for (int a = 0; a < FA; ++a) {
       const float4 v = *(const float4*)(arow[a] + kk);
       av[a] = in ? v : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
+    for (int b = 0; b < FB; ++b) {
       const float4 v = rt_load4<WT>(brow[b] + kk);
       bv[b] = in ? v : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   };
-  auto mma = [&](const float4 (&av)[2], const float4 (&bv)[2]) {
+  auto mma = [&](const float4 (&av)[FA], const float4 (&bv)[FB]) {
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < FA; ++a)
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
+      for (int b = 0; b < FB; ++b) {
         acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[a].x, bv[b].x, acc[a][b], 0, 0, 0);
         acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[a].y, bv[b].y, acc[a][b], 0, 0, 0);
         acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[a].z, bv[b].z, acc[a][b], 0, 0, 0);
@@ -193,7 +215,7 @@ k_router_logits(const float* __restrict__ h32, const WT* __restrict__ wr,
   // Batches of RM_UK chunks, two register sets; the batch count is padded to even and
   // padding chunks read (masked) zeros.
   const int nb = (nch + RM_UK - 1) / RM_UK;
-  float4 ax[RM_UK][2], bx[RM_UK][2], ay[RM_UK][2], by[RM_UK][2];
+  float4 ax[RM_UK][FA], bx[RM_UK][FB], ay[RM_UK][FA], by[RM_UK][FB];
 #pragma unroll
   for (int u = 0; u < RM_UK; ++u) load(u, ax[u], bx[u]);
   for (int bt = 0; bt < nb; bt += 2) {
@@ -207,9 +229,9 @@ k_router_logits(const float* __restrict__ h32, const WT* __restrict__ wr,
     for (int u = 0; u < RM_UK; ++u) mma(ay[u], by[u]);
   }
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int a = 0; a < FA; ++a)
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
+    for (int b = 0; b < FB; ++b) {
       const int e = e0 + 16 * b + j;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -220,9 +242,9 @@ k_router_logits(const float* __restrict__ h32, const WT* __restrict__ wr,
 }
 
 // Number of H-slices the router uses for T tokens (a pure function of the shape): enough
-// 64 x 64 tiles x slices to give about 1024 blocks, at most one slice per RT_KCH columns.
+// block tiles x slices to give about 1024 blocks, at most one slice per RT_KCH columns.
 int mx_router_splits_for(int tokens, int hidden, int e1) {
-  const int tiles = mx_ceil_div(tokens > 0 ? tokens : 1, 64) * mx_ceil_div(e1, 64);
+  const int tiles = mx_ceil_div(tokens > 0 ? tokens : 1, RT_BT) * mx_ceil_div(e1, RT_BE);
   const int kch = mx_ceil_div(hidden, RT_KCH);
   int s = 1;
   while (tiles * s < 1024 && s * 2 <= kch && s < 16) s *= 2;
@@ -252,7 +274,7 @@ extern "C" int mx_router_logits(const float* h32, const void* router_w, const vo
   const int kslice = router_kslice(hidden, splits);
   if (mx_ceil_div(hidden, kslice) != splits) return MX_ERR_INVALID;
   const int e1 = n_experts + (shared_gate_w ? 1 : 0);
-  dim3 grid(mx_ceil_div(tokens, 64), mx_ceil_div(e1, 64), splits);
+  dim3 grid(mx_ceil_div(tokens, RT_BT), mx_ceil_div(e1, RT_BE), splits);
   mx_clear_error();
   hipStream_t s = (hipStream_t)stream;
   if (param_dtype == MX_DT_F16)
