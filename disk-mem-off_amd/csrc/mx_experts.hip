@@ -458,9 +458,9 @@ struct LdsShape {
   static constexpr int KM = WF == MX_DT_F16 ? MX_LDS_KM_F16 : 1;
 };
 
-// One block's work: MB = 16 * MTX rows (from `base` of group g) x 4 waves of 16 * NBIX
+// One block's work: MB = 16 * MTX rows (from `base` of group g) x NW waves of 16 * NBIX
 // columns (x 2 for gate and up) starting at column n0b.
-template <int WF, bool GU, int MTX, int NBIX>
+template <int WF, bool GU, int MTX, int NBIX, int NW>
 __device__ __forceinline__ void expert_lds_tile(const ExpertParams& p, char* lds, int g,
                                                 int base, int trows, int n0b) {
   using Tr = WTr<WF>;
@@ -472,7 +472,7 @@ __device__ __forceinline__ void expert_lds_tile(const ExpertParams& p, char* lds
   constexpr int AROW = KS * 2 + 16;          // LDS bytes per staged activation row
   constexpr int ATILE = MB * AROW;
   constexpr int CPR = KS * 2 / 16;           // 16-byte chunks per row and stage
-  constexpr int ACH = MB * CPR / 256;        // chunks each thread stages
+  constexpr int ACH = MB * CPR / (64 * NW);  // chunks each thread stages
   constexpr int RB = KM == 1 ? MX_LDS_RB : MX_LDS_RB_KM2;  // weight stages in flight
   constexpr int RA = (WF == MX_DT_F16 && GU && KM == 1) ? MX_LDS_RA : 2;  // activation stages
   static_assert(RB % RA == 0 && RA % 2 == 0, "ring sizes must divide the unroll");
@@ -507,7 +507,7 @@ __device__ __forceinline__ void expert_lds_tile(const ExpertParams& p, char* lds
   int alds[ACH], acol[ACH];
 #pragma unroll
   for (int i = 0; i < ACH; ++i) {
-    const int c = tid + 256 * i;
+    const int c = tid + 64 * NW * i;
     const int row = c / CPR, cc = c % CPR;
     acol[i] = cc * 8;
     alds[i] = row * AROW + cc * 16;
@@ -659,8 +659,16 @@ __device__ __forceinline__ void expert_lds_tile(const ExpertParams& p, char* lds
   }
 }
 
-template <int WF, bool GU>
-__global__ __launch_bounds__(256, LdsShape<WF>::OCC) void k_expert_lds(
+// Waves per block of the prefill kernel: 4 (two blocks per CU) or 8 (fp16 only; one block
+// per CU, one staged activation tile for twice the columns).  Measured on MI355X: 8 waves
+// win for reductions of 1024-3072 columns (GLM-4.7 down, K = 1536: 731 -> 692 us;
+// Qwen3-Next gate/up, K = 2048: 531 -> 499 us) and lose outside (GLM-4.7 gate/up,
+// K = 5120: 1111 -> 1170 us; Qwen3-Next down, K = 512: 369 -> 477 us, where a lone block's
+// pipeline fill and epilogue are no longer hidden behind a second block on the CU).
+static bool lds_eight_waves(int wdt, int K) { return wdt == MX_DT_F16 && K >= 1024 && K <= 3072; }
+
+template <int WF, bool GU, int NW>
+__global__ __launch_bounds__((64 * NW), (LdsShape<WF>::OCC * 4 / NW)) void k_expert_lds(
     const ExpertParams p, int mt_max, int nblk) {
   constexpr int KS = 4 * WTr<WF>::EPL * LdsShape<WF>::KM;
   constexpr int NBI = GU ? 2 : 4;
@@ -675,9 +683,9 @@ __global__ __launch_bounds__(256, LdsShape<WF>::OCC) void k_expert_lds(
   const int g = p.mt_group[mt];
   const int row0 = p.mt_row0[mt];
   const int N = p.g_expert[g] == p.E ? p.N_s : p.N_r;
-  const int n0b = nb * 4 * 16 * NBI;
+  const int n0b = nb * NW * 16 * NBI;
   if (n0b >= N) return;  // whole block past this expert's columns
-  expert_lds_tile<WF, GU, 8, NBI>(p, lds, g, row0, min(MB, p.g_count[g] - row0), n0b);
+  expert_lds_tile<WF, GU, 8, NBI, NW>(p, lds, g, row0, min(MB, p.g_count[g] - row0), n0b);
 }
 
 // ------------------------------------------------------------------------------------
@@ -808,17 +816,21 @@ static int launch_grouped_mt(int wdt, const ExpertParams& p, int mt_max, int m_b
                              hipStream_t s) {
   if (m_blk == 128) {
     if (wdt == MX_DT_F32) return MX_ERR_INVALID;
-    const int cols = 4 * 16 * (GU ? 2 : 4);
+    const int nw = lds_eight_waves(wdt, p.K_r) ? 8 : 4;
+    const int cols = nw * 16 * (GU ? 2 : 4);
     const int nblk = mx_ceil_div(nmax, cols);
     const long blocks = ((long)mt_max * nblk + 7) / 8 * 8;
     if (blocks > (1l << 31) - 1) return MX_ERR_UNSUPPORTED;
     mx_clear_error();
-    if (wdt == MX_DT_F16)
-      hipLaunchKernelGGL((k_expert_lds<MX_DT_F16, GU>), dim3((unsigned)blocks), dim3(256), 0, s,
-                         p, mt_max, nblk);
+    if (wdt == MX_DT_F16 && nw == 8)
+      hipLaunchKernelGGL((k_expert_lds<MX_DT_F16, GU, 8>), dim3((unsigned)blocks), dim3(512), 0,
+                         s, p, mt_max, nblk);
+    else if (wdt == MX_DT_F16)
+      hipLaunchKernelGGL((k_expert_lds<MX_DT_F16, GU, 4>), dim3((unsigned)blocks), dim3(256), 0,
+                         s, p, mt_max, nblk);
     else
-      hipLaunchKernelGGL((k_expert_lds<MX_DT_I8, GU>), dim3((unsigned)blocks), dim3(256), 0, s,
-                         p, mt_max, nblk);
+      hipLaunchKernelGGL((k_expert_lds<MX_DT_I8, GU, 4>), dim3((unsigned)blocks), dim3(256), 0,
+                         s, p, mt_max, nblk);
     return mx_launch_status();
   }
   if (m_blk != 16 && m_blk != 32 && m_blk != 64) return MX_ERR_INVALID;
