@@ -97,6 +97,24 @@ def test_tiled_layer_matches_row_major(mi355x, stream, wdt, T):
     assert np.array_equal(a, b)
 
 
+def test_tiled_layer_matches_row_major_eight_wave_blocks(mi355x, stream):
+    """hidden = inter = 1024, fp16, 300 tokens: both projections run the prefill kernel's
+    8-wave blocks; the narrower shared expert leaves some waves without columns."""
+    say("[gpu] tiled vs rows, 8-wave prefill blocks")
+    shape = syn.MoeShape(syn.GLM, 1024, 24, 4, 1024, 320, 2.5, 1e-5)
+    base = syn.make_tensors(shape, 777)
+    bias = np.zeros(shape.n_experts, np.float32)
+    bias[:2] = [0.6, 0.3]
+    base["mlp.gate.e_score_correction_bias"] = bias
+    t = {n: (v.astype(np.float16) if n.startswith(("mlp.experts.", "mlp.shared_experts."))
+             else v) for n, v in base.items()}
+    x = syn.make_inputs(777, 300, shape.hidden)
+    spec = spec_for(shape, orc.SIGMOID_SELECT_BIAS)
+    a = _forward(mi355x, stream, t, spec, x, tiled=False)
+    b = _forward(mi355x, stream, t, spec, x, tiled=True)
+    assert np.array_equal(a, b)
+
+
 def test_tile_rejects_partial_fragments(mi355x, stream):
     shape = syn.MoeShape(syn.GLM, 64, 4, 2, 40, 40, 2.5, 1e-5)  # 40 rows: no whole fragments
     t = syn.make_tensors(shape, 3, weight_dtype=np.float16)

@@ -176,6 +176,29 @@ def test_skewed_prefill(mi355x, stream, wdt, T):
     assert err <= LOWP_ABS
 
 
+def test_prefill_eight_wave_blocks(mi355x, stream):
+    """fp16 reductions of 1024-3072 columns run the prefill kernel with 8-wave blocks (gate/up
+    over hidden 1024, down over inter 1024); the shared expert is narrower (320 columns), so
+    some waves of its blocks own no columns, and two hot experts span several m-tiles."""
+    say("[gpu] 8-wave prefill blocks")
+    shape = syn.MoeShape(syn.GLM, 1024, 16, 4, 1024, 320, 2.5, 1e-5)
+    base = syn.make_tensors(shape, 4242)
+    bias = np.zeros(shape.n_experts, np.float32)
+    bias[:2] = [0.6, 0.3]
+    base["mlp.gate.e_score_correction_bias"] = bias
+    t = {n: (v.astype(np.float16) if n.startswith(("mlp.experts.", "mlp.shared_experts."))
+             else v) for n, v in base.items()}
+    x = syn.make_inputs(4242, 300, shape.hidden)
+    spec = spec_for(shape, orc.SIGMOID_SELECT_BIAS)
+    out, views = run_device(mi355x, stream, t, shape, spec, x)
+    ref = orc.moe_block(x, t, spec)
+    assert views["m_blk"] == 128 and ref["counts"][:2].min() > 128
+    check_routing(views, ref, ref["logits"], bias, spec, "eight-wave")
+    err = float(np.max(np.abs(out - ref["out"])))
+    say(f"    max abs err {err:.3e}, counts[:2]={ref['counts'][:2].tolist()}")
+    assert err <= LOWP_ABS
+
+
 # ---- Qwen3-Next structure: softmax router, no bias, gated shared expert --------------------
 
 @pytest.mark.parametrize("wdt", ["float32", "float16"])
