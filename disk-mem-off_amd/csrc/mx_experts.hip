@@ -420,7 +420,8 @@ __global__ __launch_bounds__(256) void k_expert(const ExpertParams p, const Sele
 //
 // With many rows per expert the activation tile is reused by every column slab, so it is
 // staged once per block in LDS (double-buffered, rows padded by 16 bytes so the 16-byte
-// fragment reads of 8 consecutive lanes hit distinct banks) and shared by the 4 waves.
+// fragment reads of 8 consecutive lanes hit distinct banks) and shared by the block's 4
+// waves (8 for fp16 reductions of 1024-3072 columns, see lds_eight_waves).
 // Weights go straight from HBM into MFMA B registers; each wave holds 4 B fragments per
 // k-chunk (gate/up: 2 gate + 2 up column blocks; down: 4 column blocks), so every A
 // fragment read from LDS feeds 4 MFMAs, and each wave owns a 128-row x 4-fragment tile.
@@ -429,7 +430,10 @@ __global__ __launch_bounds__(256) void k_expert(const ExpertParams p, const Sele
 // block b goes to XCD b % 8, logical id = (b % 8) * (grid / 8) + b / 8.  Logical ids walk
 // the m-tiles of one column slab before moving to the next slab.  (Sharing an expert's
 // weights between its m-tiles, through L2 or by 256-row tiles, measured slower on
-// MI355X: the sibling tiles drift apart, and the taller tile doubles the LDS reads.)
+// MI355X: the sibling tiles drift apart; a taller tile per wave doubles the LDS reads, and
+// 256-row blocks that pass weight fragments between wave pairs through LDS stage as many
+// activation bytes as weight bytes and cannot share a launch with the 128-row tiles
+// without spilling.)
 // ------------------------------------------------------------------------------------
 // Tunables (compile-time; the defaults are the measured best on MI355X).
 //   MX_LDS_RB:      weight stages in flight per wave (even).
