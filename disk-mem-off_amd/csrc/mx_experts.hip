@@ -643,23 +643,31 @@ __device__ __forceinline__ void expert_lds_tile(const ExpertParams& p, char* lds
         }
     }
   } else {
+    // Fragments f and f + 1 of a row are the two 64-byte halves of one 128-byte line of y:
+    // they are stored by consecutive instructions so that L2 merges them before write-back.
+    float sd[NBIX];
 #pragma unroll
     for (int f = 0; f < NBIX; ++f) {
-      const int n = n0 + 16 * f + j;
-      if (n >= N) continue;
-      float sd = 1.f;
-      if constexpr (WF == MX_DT_I8) sd = (float)((const half_t*)ep.down_scale)[n];
-#pragma unroll
-      for (int mi = 0; mi < MTX; ++mi)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int m = 16 * mi + 4 * q + r;
-          if (m < trows) {
-            const int row = orow + m;
-            ((float*)p.out)[(size_t)row * p.ldo + n] = p.sorted_w[row] * (acc[mi][f][r] * sd);
-          }
-        }
+      sd[f] = 1.f;
+      if constexpr (WF == MX_DT_I8) {
+        const int n = n0 + 16 * f + j;
+        if (n < N) sd[f] = (float)((const half_t*)ep.down_scale)[n];
+      }
     }
+#pragma unroll
+    for (int mi = 0; mi < MTX; ++mi)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = 16 * mi + 4 * q + r;
+        if (m >= trows) continue;
+        const int row = orow + m;
+        const float w = p.sorted_w[row];
+#pragma unroll
+        for (int f = 0; f < NBIX; ++f) {
+          const int n = n0 + 16 * f + j;
+          if (n < N) ((float*)p.out)[(size_t)row * p.ldo + n] = w * (acc[mi][f][r] * sd[f]);
+        }
+      }
   }
 }
 
