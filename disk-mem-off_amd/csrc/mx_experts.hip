@@ -443,6 +443,9 @@ __global__ __launch_bounds__(256) void k_expert(const ExpertParams p, const Sele
 #ifndef MX_LDS_RB
 #define MX_LDS_RB 4
 #endif
+#ifndef MX_LDS_NT
+#define MX_LDS_NT 0  // nontemporal hint on the prefill kernel's weight loads
+#endif
 #ifndef MX_LDS_RA
 #define MX_LDS_RA 4
 #endif
@@ -544,7 +547,7 @@ __device__ __forceinline__ void expert_lds_tile(const ExpertParams& p, char* lds
 #pragma unroll
       for (int f = 0; f < NF; ++f) {
         const int fi = GU ? (f % NBIX) : f;
-        br[km][f] = mx_ld16((GU && f >= NBIX) ? rb1 : rb0, kin ? boff[fi] + kb : MX_OOB);
+        br[km][f] = mx_ldw16<MX_LDS_NT>((GU && f >= NBIX) ? rb1 : rb0, kin ? boff[fi] + kb : MX_OOB);
       }
     }
   };
