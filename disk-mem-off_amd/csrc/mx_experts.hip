@@ -443,8 +443,15 @@ __global__ __launch_bounds__(256) void k_expert(const ExpertParams p, const Sele
 #ifndef MX_LDS_RB
 #define MX_LDS_RB 4
 #endif
-#ifndef MX_LDS_NT
-#define MX_LDS_NT 0  // nontemporal hint on the prefill kernel's weight loads
+// Nontemporal hint on the prefill kernel's weight loads, per projection; both off.  The
+// sibling m-tiles of hot experts share weight lines through L2 (GLM-4.7 Zipf prefill with
+// nt: gate/up 1.109 -> 1.361 ms, down 671 -> 690 us); single-tile experts gain a little
+// from it (Qwen3-Next 4096 tokens: gate/up 497 -> 480 us, down 340 -> 333 us).
+#ifndef MX_LDS_NT_GU
+#define MX_LDS_NT_GU 0
+#endif
+#ifndef MX_LDS_NT_DN
+#define MX_LDS_NT_DN 0
 #endif
 #ifndef MX_LDS_RA
 #define MX_LDS_RA 4
@@ -547,7 +554,8 @@ __device__ __forceinline__ void expert_lds_tile(const ExpertParams& p, char* lds
 #pragma unroll
       for (int f = 0; f < NF; ++f) {
         const int fi = GU ? (f % NBIX) : f;
-        br[km][f] = mx_ldw16<MX_LDS_NT>((GU && f >= NBIX) ? rb1 : rb0, kin ? boff[fi] + kb : MX_OOB);
+        br[km][f] = mx_ldw16<GU ? MX_LDS_NT_GU : MX_LDS_NT_DN>((GU && f >= NBIX) ? rb1 : rb0,
+                                                                kin ? boff[fi] + kb : MX_OOB);
       }
     }
   };
