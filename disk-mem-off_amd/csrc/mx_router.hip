@@ -241,13 +241,16 @@ k_router_logits(const float* __restrict__ h32, const WT* __restrict__ wr,
     }
 }
 
-// Number of H-slices the router uses for T tokens (a pure function of the shape): enough
-// block tiles x slices to give about 1024 blocks, at most one slice per RT_KCH columns.
+// Number of H-slices the router uses for T tokens (a pure function of the shape), at most
+// one slice per RT_KCH columns and at most 16.
 int mx_router_splits_for(int tokens, int hidden, int e1) {
   const int tiles = mx_ceil_div(tokens > 0 ? tokens : 1, RT_BT) * mx_ceil_div(e1, RT_BE);
   const int kch = mx_ceil_div(hidden, RT_KCH);
+  // Largest slice count whose blocks fit one round at 4 waves per SIMD (1024 blocks of 4
+  // waves on 256 CUs).  Qwen3-Next, 4096 tokens: 3 slices (816 blocks) against 4 (1088,
+  // a second round of 64 blocks): router + top-k 149 -> 145 us.
   int s = 1;
-  while (tiles * s < 1024 && s * 2 <= kch && s < 16) s *= 2;
+  while (tiles * (s + 1) <= 1024 && s + 1 <= kch && s < 16) ++s;
   const int per = mx_ceil_div(kch, s);
   return mx_ceil_div(kch, per);
 }
