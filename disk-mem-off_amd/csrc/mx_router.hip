@@ -121,7 +121,9 @@ extern "C" int mx_rmsnorm(const float* x, const void* norm_w, int32_t param_dtyp
 // four MFMAs cover the chunk's 16 columns once each.  Loads are clamped in bounds and
 // masked (branch-free), and a chunk batch is in flight while the previous one runs.
 // ------------------------------------------------------------------------------------
+#ifndef RT_KCH
 #define RT_KCH 256  // H-slice granularity (elements)
+#endif
 
 template <typename WT>
 __device__ __forceinline__ float4 rt_load4(const WT* p);
