@@ -122,7 +122,7 @@ extern "C" int mx_rmsnorm(const float* x, const void* norm_w, int32_t param_dtyp
 // masked (branch-free), and a chunk batch is in flight while the previous one runs.
 // ------------------------------------------------------------------------------------
 #ifndef RT_KCH
-#define RT_KCH 256  // H-slice granularity (elements)
+#define RT_KCH 256  // H-slice granularity of the prefill router (elements)
 #endif
 
 template <typename WT>
@@ -378,7 +378,10 @@ k_router_logits_decode(
   const int e = blockIdx.x;
   const int t0 = blockIdx.y * TT;
   const WT* row = (e < E) ? wr + (size_t)e * H : wseg;
-  const int hq = (H / 4 + 255) / 256 * 256;  // H quarter per wave, in 256-element sweeps
+  // One sweep of the wave covers 64 lanes x 4 columns; the loop stride is that sweep and
+  // does not follow the prefill router's slice width.
+  constexpr int SWEEP = 64 * 4;
+  const int hq = (H / 4 + SWEEP - 1) / SWEEP * SWEEP;  // H quarter per wave, whole sweeps
   const int kb = wave * hq, ke = min(H, kb + hq);
   float acc[TT], ss[TT];
   const float* xrow[TT];
@@ -389,7 +392,7 @@ k_router_logits_decode(
     xrow[t] = x + (size_t)min(t0 + t, T - 1) * H;
   }
 #pragma unroll 4
-  for (int c = kb + lane * 4; c < ke; c += RT_KCH) {
+  for (int c = kb + lane * 4; c < ke; c += SWEEP) {
     const float4 wv = rt_load4<WT>(row + c);
     const float4 nv = rt_load4<WT>(norm_w + c);
     const float4 g = make_float4(nv.x * wv.x, nv.y * wv.y, nv.z * wv.z, nv.w * wv.w);

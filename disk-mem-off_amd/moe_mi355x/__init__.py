@@ -3,9 +3,11 @@
 Compute runs only in ``libmoe_mi355x.so`` (HIP kernels, C ABI, see include/moe_mi355x.h);
 this package is the host side: backend, pools, runtime, layer layout and executors.
 """
-from .backends import DeviceBackend, MI355XBackend, NullBackend, ROCmBackend, detect_backend
-from .buffer_pool import DeviceBufferPool, PinnedHostBufferPool
-from .executors import GLM4MoeExecutor, Qwen3NextExecutor, host_attention, read_layer_tensors
+from .backends import DeviceBackend, MI355XBackend, ROCmBackend, detect_backend
+from .buffer_pool import DeviceBufferPool
+from .pinned_pool import PinnedHostBufferPool
+from .executors import (GLM4MoeExecutor, Qwen3NextExecutor, host_attention, host_dense,
+                        read_layer_tensors)
 from .layout import MoeLayerLayout, make_layer_spec, pack_tensors, unpack_host
 from .moe import ROUTER_MODES, MoeConfig, MoeRunner
 from .quantize import (CompositeDequantizer, Float16Dequantizer, Int8Dequantizer,
@@ -19,9 +21,9 @@ __all__ = [
     "CompositeDequantizer", "DeviceBackend", "DeviceBuffer", "DeviceBufferPool",
     "Float16Dequantizer", "GLM4MoeExecutor", "HostBuffer", "InMemoryStorage", "Int8Dequantizer",
     "LayerExecutor", "LayerMetrics", "LayerSpec", "LayerStorage", "LookaheadScheduler",
-    "MI355XBackend", "MoeConfig", "MoeLayerLayout", "MoeRunner", "NullBackend",
+    "MI355XBackend", "MoeConfig", "MoeLayerLayout", "MoeRunner",
     "OffloadRuntime", "PinnedHostBufferPool", "PrefetchScheduler", "Qwen3NextExecutor",
     "ROCmBackend", "ROUTER_MODES", "RuntimeMetrics", "dequantize_rows_int8", "detect_backend",
-    "host_attention", "make_layer_spec", "pack_tensors", "quantize_moe_tensors",
+    "host_attention", "host_dense", "make_layer_spec", "pack_tensors", "quantize_moe_tensors",
     "quantize_rows_int8", "read_layer_tensors", "unpack_host",
 ]

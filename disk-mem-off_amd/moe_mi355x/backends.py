@@ -1,5 +1,5 @@
-"""Device backends: the ``DeviceBackend`` contract, a CPU ``NullBackend`` for tests, and
-``MI355XBackend``, the ROCm backend built on ``libmoe_mi355x.so``.
+"""Device backends: the ``DeviceBackend`` contract and ``MI355XBackend``, the ROCm backend
+built on ``libmoe_mi355x.so``.
 
 Contract and error behaviour follow offload_runtime/backends/base.py:9-77 and
 offload_runtime/backends/rocm_backend.py:33-119 (name ``"rocm"``, non-blocking streams,
@@ -69,65 +69,6 @@ class DeviceBackend(ABC):
 
     @abstractmethod
     def synchronize_stream(self, stream: Any) -> None: ...
-
-
-class NullBackend(DeviceBackend):
-    """CPU stand-in: device buffers are bytearrays, copies are synchronous, streams and
-    events are opaque tokens.  Used by the CPU tests of the runtime and pools
-    (behaviour of offload_runtime/backends/null_backend.py:9-76)."""
-
-    name = "null"
-
-    def __init__(self) -> None:
-        self._buffers: dict[int, bytearray] = {}
-        self._pinned: set[int] = set()
-
-    @property
-    def supports_pinned_host(self) -> bool:
-        return True
-
-    def alloc_pinned_host(self, nbytes: int) -> HostBuffer:
-        buf = bytearray(nbytes)
-        self._pinned.add(id(buf))
-        return HostBuffer(view=memoryview(buf), pinned=True)
-
-    def free_pinned_host(self, buf: HostBuffer) -> None:
-        self._pinned.discard(id(buf.view.obj))
-
-    def create_stream(self, purpose: str) -> Any:
-        return object()
-
-    def destroy_stream(self, stream: Any) -> None:
-        return None
-
-    def alloc_device(self, nbytes: int) -> DeviceBuffer:
-        buf = bytearray(nbytes)
-        self._buffers[id(buf)] = buf
-        return DeviceBuffer(handle=id(buf), nbytes=nbytes, backend=self.name)
-
-    def free_device(self, buf: DeviceBuffer) -> None:
-        self._buffers.pop(int(buf.handle), None)
-
-    def copy_h2d_async(self, dst: DeviceBuffer, src: HostBuffer, stream: Any) -> None:
-        target = self._buffers[int(dst.handle)]
-        data = src.view.tobytes()
-        target[: len(data)] = data
-
-    def copy_d2h_async(self, dst: HostBuffer, src: DeviceBuffer, stream: Any) -> None:
-        source = self._buffers[int(src.handle)]
-        dst.view[: len(source)] = source
-
-    def record_event(self, stream: Any) -> Any:
-        return object()
-
-    def destroy_event(self, event: Any) -> None:
-        return None
-
-    def wait_event(self, stream: Any, event: Any) -> None:
-        return None
-
-    def synchronize_stream(self, stream: Any) -> None:
-        return None
 
 
 def _view_address(view: memoryview) -> int:
@@ -268,13 +209,14 @@ ROCmBackend = MI355XBackend
 
 
 def detect_backend(device_id: int = 0) -> DeviceBackend:
-    """The MI355X backend when a ROCm device is usable, else ``NullBackend``
-    (order of offload_runtime/backends/__init__.py:22-31 restricted to ROCm)."""
-    try:
-        lib = _lib.load()
-        n = ctypes.c_int32(0)
-        if lib.mx_get_device_count(ctypes.byref(n)) == 0 and n.value > device_id:
-            return MI355XBackend(device_id)
-    except (RuntimeError, OSError):
-        pass
-    return NullBackend()
+    """The MI355X backend (the ROCm entry of offload_runtime/backends/__init__.py:22-31).
+
+    There is no CPU fallback: the MoE step only runs in the HIP library, so a missing
+    library or device raises ``RuntimeError`` instead of handing back a host stand-in."""
+    lib = _lib.load()
+    n = ctypes.c_int32(0)
+    rc = lib.mx_get_device_count(ctypes.byref(n))
+    if rc != 0 or n.value <= device_id:
+        raise RuntimeError(f"no ROCm device {device_id} (hipGetDeviceCount status {rc}, "
+                           f"{n.value} devices)")
+    return MI355XBackend(device_id)

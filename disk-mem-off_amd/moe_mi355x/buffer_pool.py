@@ -1,6 +1,6 @@
-"""Exact-size free lists for device buffers and pinned host buffers.
+"""Exact-size free list for device buffers.
 
-Behaviour of offload_runtime/buffer_pool.py:9-30 and offload_runtime/pinned_pool.py:9-30:
+Behaviour of offload_runtime/buffer_pool.py:9-30:
 ``acquire(n)`` pops a released buffer of exactly ``n`` bytes or allocates a new one,
 ``release`` returns a buffer to its size class, ``drain`` frees everything.
 
@@ -15,7 +15,7 @@ from collections import defaultdict
 from typing import Any
 
 from .backends import DeviceBackend
-from .types import DeviceBuffer, HostBuffer
+from .types import DeviceBuffer
 
 
 class DeviceBufferPool:
@@ -44,29 +44,5 @@ class DeviceBufferPool:
                 if ev is not None:
                     self._backend.destroy_event(ev)
                 self._backend.free_device(buf)
-            pool.clear()
-        self._free.clear()
-
-
-class PinnedHostBufferPool:
-    """Reuses pinned host buffers of the same size to avoid frequent alloc/free."""
-
-    def __init__(self, backend: DeviceBackend) -> None:
-        self._backend = backend
-        self._free: dict[int, list[HostBuffer]] = defaultdict(list)
-
-    def acquire(self, nbytes: int) -> HostBuffer:
-        pool = self._free.get(nbytes)
-        if pool:
-            return pool.pop()
-        return self._backend.alloc_pinned_host(nbytes)
-
-    def release(self, buf: HostBuffer) -> None:
-        self._free[buf.nbytes].append(buf)
-
-    def drain(self) -> None:
-        for pool in self._free.values():
-            for buf in pool:
-                self._backend.free_pinned_host(buf)
             pool.clear()
         self._free.clear()

@@ -15,6 +15,13 @@ example the reference executor's own ``_attention_block``): it copies back only 
 layer's non-MLP tensors (``read_layer_tensors``) where the reference reads back the whole
 layer (glm4_moe.py:96-97, _common.py:20-34).
 
+GLM4-MoE layers whose ``metadata["is_moe"]`` is false or absent (the reference's default,
+glm4_moe.py:102: the ``first_k_dense_replace`` layers) run a dense MLP, which is not part
+of the MoE path either: pass ``dense=callable`` with the same signature as ``attention``;
+``host_dense(fn)`` runs ``fn(x, tensors)`` on the host over the layer's
+``post_attention_layernorm`` and ``mlp.{gate,up,down}_proj`` tensors (for example the
+reference's ``_dense_mlp_block``, glm4_moe.py:166-172).
+
 Before ``run_layer`` returns, the compute stream is synchronised: the runtime frees or
 re-pools ``device_weights`` right after the call (runtime.py:180).
 """
@@ -104,14 +111,28 @@ def host_attention(fn: Callable[[np.ndarray, dict[str, np.ndarray]], np.ndarray]
     return run
 
 
+def _dense_tensor(name: str) -> bool:
+    return name == NORM or name in {f"mlp.{p}.weight" for p in ("gate_proj", "up_proj",
+                                                                 "down_proj")}
+
+
+def host_dense(fn: Callable[[np.ndarray, dict[str, np.ndarray]], np.ndarray]) -> AttentionFn:
+    """A ``dense=`` hook that runs ``fn(x, tensors)`` on the host over the dense MLP tensors
+    of the layer (``post_attention_layernorm.weight``, ``mlp.{gate,up,down}_proj.weight``),
+    copied back by ``read_layer_tensors``."""
+    return host_attention(fn, keep=_dense_tensor)
+
+
 class _MoeExecutorBase:
     _router_default: int = _lib.MX_ROUTER_REF_SOFTMAX_BIAS
 
     def __init__(self, config: dict[str, Any], *, router_mode: int | str | None = None,
-                 attention: AttentionFn | None = None, max_tokens: int = 32) -> None:
+                 attention: AttentionFn | None = None, dense: AttentionFn | None = None,
+                 max_tokens: int = 32) -> None:
         self.hidden_size = int(config["hidden_size"])
         self.router_mode = router_mode if router_mode is not None else self._router_default
         self.attention = attention
+        self.dense = dense
         self.max_tokens = max_tokens
         self._runner: MoeRunner | None = None
         self._layouts: dict[int, tuple[list, MoeLayerLayout]] = {}
@@ -214,12 +235,23 @@ class _MoeExecutorBase:
                                  device_weights, backend, stream)
         return self.moe_block_granular(layer, x, device_weights, backend, stream, fetch, pre=pre)
 
+    def is_moe_layer(self, layer: LayerSpec) -> bool:
+        """Whether the layer's MLP is the MoE block (else a dense MLP)."""
+        return True
+
     def run_layer(self, layer: LayerSpec, activations: Any, device_weights: DeviceBuffer,
                   backend: Any, stream: Any) -> Any:
         x, pre = self._attention(layer, np.asarray(activations, dtype=np.float32),
                                  device_weights, backend, stream)
-        if not layer.metadata.get("is_moe", True):
-            raise NotImplementedError("dense MLP layers are not handled by this executor")
+        if not self.is_moe_layer(layer):
+            if self.dense is None:
+                raise NotImplementedError(
+                    f"layer {layer.layer_id} is a dense MLP layer (metadata is_moe false); "
+                    "pass dense=... (for example host_dense(fn)) to run it")
+            if pre is not None:
+                raise NotImplementedError("a dense MLP after a device attention block")
+            return np.asarray(self.dense(x, layer, device_weights, backend, stream),
+                              dtype=np.float32)
         return self.moe_block(layer, x, device_weights, backend, stream, pre=pre)
 
     @staticmethod
@@ -263,6 +295,10 @@ class GLM4MoeExecutor(_MoeExecutorBase):
         self.norm_topk_prob = bool(config.get("norm_topk_prob", True))
         self.num_experts_per_tok = self.top_k
         self.routed_scaling_factor = self.routed_scaling
+
+    def is_moe_layer(self, layer: LayerSpec) -> bool:
+        # glm4_moe.py:102: a layer without the flag is a dense (first_k_dense_replace) layer.
+        return bool(layer.metadata.get("is_moe", False))
 
 
 class Qwen3NextExecutor(_MoeExecutorBase):

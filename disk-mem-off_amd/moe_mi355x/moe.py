@@ -107,7 +107,11 @@ class MoeRunner:
         self.lib = _lib.load()
         self._ws: DeviceBuffer | None = None
         self._table_dev: DeviceBuffer | None = None
-        self._table_key: Any = None
+        # The layout object and buffer address the uploaded pointer table was built from;
+        # the layout is held by reference so a new layout can never be taken for it.
+        self._table_layout: MoeLayerLayout | None = None
+        self._table_base: int | None = None
+        self._table_ev: Any = None
         self._io: dict[str, DeviceBuffer] = {}
         self._pinned: dict[str, Any] = {}
         self._split_tokens = 0
@@ -133,27 +137,39 @@ class MoeRunner:
                 self._pinned[key] = self.backend.alloc_pinned_host(max(nbytes_act, 16))
 
     def bind(self, layout: MoeLayerLayout, base: int, stream: Any) -> _lib.MxMoeWeights:
-        """Upload the expert pointer table for a layer buffer at ``base`` (cached)."""
-        key = (id(layout), base)
+        """Upload the expert pointer table for a layer buffer at ``base`` (cached while the
+        same layout object is bound at the same address)."""
         nbytes = ctypes.sizeof(_lib.MxExpertPtrs) * (layout.n_experts + 1)
         if self._table_dev is None or self._table_dev.nbytes < nbytes:
+            self._wait_table_upload()
             if self._table_dev is not None:
                 self.backend.free_device(self._table_dev)
             self._table_dev = self.backend.alloc_device(nbytes)
-            self._table_key = None
+            self._table_layout = self._table_base = None
             pin = self._pinned.pop("table", None)
             if pin is not None:
                 self.backend.free_pinned_host(pin)
             self._pinned["table"] = self.backend.alloc_pinned_host(nbytes)
-        if self._table_key != key:
+        if self._table_layout is not layout or self._table_base != base:
             table = layout.expert_table(base)
             pin = self._pinned["table"]
+            # The previous upload may still be reading the pinned staging copy.
+            self._wait_table_upload()
             ctypes.memmove(ctypes.addressof(ctypes.c_char.from_buffer(pin.view)), table, nbytes)
             self.backend.copy_h2d_ptr_async(self._table_dev.handle,
                                             ctypes.addressof(ctypes.c_char.from_buffer(pin.view)),
                                             nbytes, stream)
-            self._table_key = key
+            self._table_ev = self.backend.record_event(stream)
+            self._table_layout, self._table_base = layout, base
         return layout.weights(base, self._table_dev.handle)
+
+    def _wait_table_upload(self) -> None:
+        if self._table_ev is not None:
+            sync = getattr(self.backend, "event_synchronize", None)
+            if sync is not None:
+                sync(self._table_ev)
+            self.backend.destroy_event(self._table_ev)
+            self._table_ev = None
 
     # -- hot path --
     def forward_device(self, desc: _lib.MxMoeDesc, weights: _lib.MxMoeWeights, x: int, out: int,
@@ -253,12 +269,14 @@ class MoeRunner:
         return v
 
     def close(self) -> None:
+        self._wait_table_upload()
         for buf in [self._ws, self._table_dev, *self._io.values()]:
             if buf is not None:
                 self.backend.free_device(buf)
         for pin in self._pinned.values():
             self.backend.free_pinned_host(pin)
         self._ws = self._table_dev = None
+        self._table_layout = self._table_base = None
         self._io.clear()
         self._pinned.clear()
 

@@ -18,7 +18,6 @@ the runtime to expand the whole layer to fp32 on the host.
 from __future__ import annotations
 
 import re
-import struct
 from typing import Any, Protocol
 
 import numpy as np

@@ -22,7 +22,8 @@ from dataclasses import dataclass, field
 from typing import Any, Protocol
 
 from .backends import DeviceBackend
-from .buffer_pool import DeviceBufferPool, PinnedHostBufferPool
+from .buffer_pool import DeviceBufferPool
+from .pinned_pool import PinnedHostBufferPool
 from .scheduler import PrefetchScheduler
 from .storage import LayerStorage
 from .types import DeviceBuffer, HostBuffer, LayerSpec
@@ -229,7 +230,9 @@ class OffloadRuntime:
             lm.compressed_nbytes = compressed
             metrics.compressed_bytes += compressed
         nbytes = host.nbytes
-        granular = self.expert_granular and layer.metadata.get("is_moe", True)
+        is_moe = getattr(self.executor, "is_moe_layer", None)
+        granular = self.expert_granular and (is_moe(layer) if is_moe is not None else
+                                             bool(layer.metadata.get("is_moe", False)))
         staged = host if granular else self._stage_pinned(host)
         device = self._alloc_device(nbytes)
         t0 = time.perf_counter()

@@ -6,7 +6,7 @@ import pytest
 
 from moe_mi355x import _lib
 from moe_mi355x import synthetic as syn
-from moe_mi355x.backends import NullBackend
+from null_backend import NullBackend
 from moe_mi355x.executors import GLM4MoeExecutor, Qwen3NextExecutor
 from moe_mi355x.layout import make_layer_spec, pack_tensors
 
@@ -152,3 +152,77 @@ def test_host_attention_hook_runs_before_the_moe_step():
     y = hook(x, layer, DeviceBuffer(handle=0, nbytes=len(buf), backend="null"), be, None)
     assert np.array_equal(y, np.broadcast_to(t["input_layernorm.weight"], (3, 32)))
     assert "self_attn.o_proj.weight" in seen and not any(n.startswith("mlp.") for n in seen)
+
+
+def _dense_layer(is_moe=None, seed=7):
+    """A GLM4 dense (first_k_dense_replace) layer: attention tensors + a dense SwiGLU MLP."""
+    rng = np.random.default_rng(seed)
+    H, inter = 32, 48
+    t = {
+        "input_layernorm.weight": rng.standard_normal(H).astype(np.float32),
+        "self_attn.o_proj.weight": rng.standard_normal((H, H)).astype(np.float32),
+        "post_attention_layernorm.weight": rng.standard_normal(H).astype(np.float32),
+        "mlp.gate_proj.weight": (0.1 * rng.standard_normal((inter, H))).astype(np.float32),
+        "mlp.up_proj.weight": (0.1 * rng.standard_normal((inter, H))).astype(np.float32),
+        "mlp.down_proj.weight": (0.1 * rng.standard_normal((H, inter))).astype(np.float32),
+    }
+    buf, meta = pack_tensors(t)
+    layer = make_layer_spec(0, meta, len(buf))
+    del layer.metadata["is_moe"]
+    if is_moe is not None:
+        layer.metadata["is_moe"] = is_moe
+    return t, buf, layer
+
+
+def _dense_mlp(x, t, eps=1e-5):
+    # glm4_moe.py:166-172 restated: x + down(silu(gate(h)) * up(h)), h = rms_norm(x)
+    h = t["post_attention_layernorm.weight"] * (x / np.sqrt(np.mean(x * x, -1, keepdims=True) + eps))
+    g = h @ t["mlp.gate_proj.weight"].T
+    u = h @ t["mlp.up_proj.weight"].T
+    return x + ((g / (1 + np.exp(-g))) * u) @ t["mlp.down_proj.weight"].T
+
+
+@pytest.mark.parametrize("is_moe", [None, False])
+def test_glm_layer_without_is_moe_is_a_dense_layer(is_moe):
+    """glm4_moe.py:102 defaults is_moe to False: such layers take the dense hook."""
+    from moe_mi355x.executors import DeviceBuffer, host_attention, host_dense
+
+    t, buf, layer = _dense_layer(is_moe)
+    cfg = {"hidden_size": 32}
+    be = _PtrBackend(buf)
+    dev = DeviceBuffer(handle=0, nbytes=len(buf), backend="null")
+    x = np.random.default_rng(1).standard_normal((3, 32)).astype(np.float32)
+    attn = host_attention(lambda x_, tt: x_ + tt["input_layernorm.weight"])
+    ex = GLM4MoeExecutor(cfg, attention=attn)
+    assert not ex.is_moe_layer(layer)
+    with pytest.raises(NotImplementedError, match="dense"):
+        ex.run_layer(layer, x, dev, be, None)
+    seen = {}
+
+    def dense(x_, tt):
+        seen.update(tt)
+        return _dense_mlp(x_, tt)
+
+    ex2 = GLM4MoeExecutor(cfg, attention=attn, dense=host_dense(dense))
+    y = ex2.run_layer(layer, x, dev, be, None)
+    assert set(seen) == {"post_attention_layernorm.weight", "mlp.gate_proj.weight",
+                         "mlp.up_proj.weight", "mlp.down_proj.weight"}
+    want = _dense_mlp(x + t["input_layernorm.weight"], t)
+    np.testing.assert_allclose(y, want, rtol=1e-6, atol=1e-6)
+
+
+def test_moe_flag_per_executor():
+    _, _, layer = _dense_layer(None)
+    assert not GLM4MoeExecutor({"hidden_size": 32}).is_moe_layer(layer)
+    layer.metadata["is_moe"] = True
+    assert GLM4MoeExecutor({"hidden_size": 32}).is_moe_layer(layer)
+    # Qwen3-Next runs its MoE block on every layer (qwen3_next.py:155-156).
+    del layer.metadata["is_moe"]
+    assert Qwen3NextExecutor({"hidden_size": 32}).is_moe_layer(layer)
+
+
+def test_detect_backend_has_no_cpu_fallback():
+    from moe_mi355x.backends import detect_backend
+
+    with pytest.raises(RuntimeError):
+        detect_backend(10 ** 6)

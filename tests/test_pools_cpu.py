@@ -2,7 +2,7 @@
 tests/test_buffer_pool.py:12-50 and tests/test_pinned_pool.py:12-48)."""
 from __future__ import annotations
 
-from moe_mi355x.backends import NullBackend
+from null_backend import NullBackend
 from moe_mi355x.buffer_pool import DeviceBufferPool
 from moe_mi355x.pinned_pool import PinnedHostBufferPool
 

@@ -7,7 +7,7 @@ from typing import Any
 
 import pytest
 
-from moe_mi355x.backends import NullBackend
+from null_backend import NullBackend
 from moe_mi355x.quantize import CompositeDequantizer, Int8Dequantizer
 from moe_mi355x.runtime import OffloadRuntime, RuntimeMetrics
 from moe_mi355x.scheduler import LookaheadScheduler
@@ -163,7 +163,7 @@ def test_transfers_issued_ahead_of_compute():
 
 
 def test_expert_granular_needs_capable_executor_and_backend():
-    from moe_mi355x.backends import NullBackend
+    from null_backend import NullBackend
     from moe_mi355x.runtime import OffloadRuntime
     from moe_mi355x.scheduler import LookaheadScheduler
     from moe_mi355x.storage import InMemoryStorage
