@@ -170,6 +170,14 @@ class DeviceMoeLayer:
             out = frag16_to_rows(out, out.shape[0], out.shape[1], out.dtype)
         return out
 
+    def write(self, offset: int, arr: np.ndarray) -> None:
+        """Copy a host array into the layer buffer at byte ``offset`` (synchronous)."""
+        arr = np.ascontiguousarray(arr)
+        if offset < 0 or offset + arr.nbytes > self.buf.nbytes:
+            raise ValueError(f"write of {arr.nbytes} bytes at {offset} outside the layer "
+                             f"buffer ({self.buf.nbytes} bytes)")
+        _upload(self.backend, self.buf.handle + offset, arr, self.stream)
+
     def read_tensors(self, names: list[str]) -> dict[str, np.ndarray]:
         out = {}
         for n in names:

@@ -147,40 +147,72 @@ def route(logits: np.ndarray, bias: np.ndarray | None, spec: MoeSpec
         sel_key = np.take_along_axis(key, idx, axis=-1)
         order = np.argsort(-sel_key, axis=-1, kind="stable")
         idx = np.take_along_axis(idx, order, axis=-1)
-        w = np.take_along_axis(scores, idx, axis=-1)
     else:
-        z = logits + bias if (spec.router_mode == REF_SOFTMAX_BIAS and bias is not None) \
-            else logits
-        probs = softmax(z, axis=-1)
+        probs = _probs(logits, bias, spec)
         idx = np.argpartition(-probs, k, axis=-1)[:, :k] if probs.shape[-1] > k else \
             np.tile(np.arange(probs.shape[-1]), (probs.shape[0], 1))
         w = np.take_along_axis(probs, idx, axis=-1)
         order = np.argsort(-w, axis=-1)
         idx = np.take_along_axis(idx, order, axis=-1)
-        w = np.take_along_axis(w, order, axis=-1)
+    return idx, route_weights(logits, bias, idx, spec)
+
+
+def _probs(logits: np.ndarray, bias: np.ndarray | None, spec: MoeSpec) -> np.ndarray:
+    """softmax(logits + bias) (glm4_moe.py:182-185) or softmax(logits) (qwen3_next.py:279)."""
+    z = logits + bias if (spec.router_mode == REF_SOFTMAX_BIAS and bias is not None) \
+        else logits
+    return softmax(z, axis=-1)
+
+
+def route_weights(logits: np.ndarray, bias: np.ndarray | None, ids: np.ndarray,
+                  spec: MoeSpec) -> np.ndarray:
+    """Routing weights of the experts ``ids`` [T, k] (in that slot order): the scores at
+    those ids (softmax probabilities, or the unbiased sigmoid scores), renormalised over
+    the k slots when norm_topk_prob (glm4_moe.py:198-199, + 1e-20) and times the routed
+    scaling (glm4_moe.py:200).  ``route`` uses it on its own selection; the parity tests
+    use it on a device selection that differs from ``route`` only between near-tied
+    candidates."""
+    if spec.router_mode == SIGMOID_SELECT_BIAS:
+        w = np.take_along_axis(sigmoid(logits), ids, axis=-1)
+    else:
+        w = np.take_along_axis(_probs(logits, bias, spec), ids, axis=-1)
     if spec.norm_topk_prob:
         w = w / (w.sum(axis=-1, keepdims=True) + 1e-20)
-    w = w * spec.routed_scaling
-    return idx, w
+    return w * spec.routed_scaling
+
+
+def selection_keys(logits: np.ndarray, bias: np.ndarray | None, spec: MoeSpec) -> np.ndarray:
+    """The fp64 keys top-k ranks (an order-preserving image of each mode's key): sigmoid
+    score + bias, logit + bias (softmax is monotonic), or the logit."""
+    l64 = logits.astype(np.float64)
+    b64 = None if bias is None else bias.astype(np.float64)
+    if spec.router_mode == SIGMOID_SELECT_BIAS:
+        return 1.0 / (1.0 + np.exp(-l64)) + (b64 if b64 is not None else 0.0)
+    if spec.router_mode == REF_SOFTMAX_BIAS and b64 is not None:
+        return l64 + b64
+    return l64
 
 
 def topk_margin(logits: np.ndarray, bias: np.ndarray | None, spec: MoeSpec) -> np.ndarray:
     """Per token, the fp64 gap between the k-th and (k+1)-th selection keys.  A token whose
     gap is below fp32 noise may legitimately select differently under another summation
     order of the router product."""
-    l64 = logits.astype(np.float64)
-    b64 = None if bias is None else bias.astype(np.float64)
-    if spec.router_mode == SIGMOID_SELECT_BIAS:
-        key = 1.0 / (1.0 + np.exp(-l64)) + (b64 if b64 is not None else 0.0)
-    elif spec.router_mode == REF_SOFTMAX_BIAS and b64 is not None:
-        key = l64 + b64
-    else:
-        key = l64
-    s = -np.sort(-key, axis=-1)
+    s = -np.sort(-selection_keys(logits, bias, spec), axis=-1)
     k = spec.top_k
     if s.shape[-1] <= k:
         return np.full(s.shape[0], np.inf)
     return s[:, k - 1] - s[:, k]
+
+
+def order_margin(logits: np.ndarray, bias: np.ndarray | None, spec: MoeSpec) -> np.ndarray:
+    """Per token, the smallest fp64 gap between consecutive keys among the k + 1 largest:
+    below fp32 noise, the selected set or the slot order of the ids may differ under
+    another summation order of the router product."""
+    s = -np.sort(-selection_keys(logits, bias, spec), axis=-1)
+    n = min(spec.top_k + 1, s.shape[-1])
+    if n < 2:
+        return np.full(s.shape[0], np.inf)
+    return np.min(s[:, : n - 1] - s[:, 1:n], axis=-1)
 
 
 # ---- expert products ------------------------------------------------------------------------
@@ -250,17 +282,24 @@ def moe_block_faithful(x: np.ndarray, t: dict[str, np.ndarray], spec: MoeSpec) -
     return x + output
 
 
-def moe_block(x: np.ndarray, t: dict[str, np.ndarray], spec: MoeSpec) -> dict[str, Any]:
+def moe_block(x: np.ndarray, t: dict[str, np.ndarray], spec: MoeSpec,
+              ids: np.ndarray | None = None) -> dict[str, Any]:
     """Same mathematics as ``moe_block_faithful``, grouped by expert, with intermediates.
 
     Returns h, logits, ids, w, shared_w (1 or the Qwen sigmoid gate), the dispatch
     tables, act (per sorted row, routed rows then shared rows), y (weighted per-row
-    outputs) and out = x + sum of the k routed rows + shared row."""
+    outputs) and out = x + sum of the k routed rows + shared row.  ``ids`` [T, k], when
+    given, replaces the top-k selection (weights from ``route_weights`` at those ids): the
+    block evaluated on a selection that differs only between near-tied experts."""
     E = n_experts(t)
     h = rms_norm(x, t["post_attention_layernorm.weight"], spec.eps)
     logits = router_logits(h, t)
     bias = t.get("mlp.gate.e_score_correction_bias")
-    ids, w = route(logits, bias, spec)
+    if ids is None:
+        ids, w = route(logits, bias, spec)
+    else:
+        ids = np.asarray(ids, dtype=np.int64)
+        w = route_weights(logits, bias, ids, spec)
     d = dispatch(ids, E)
     T, k = ids.shape
     H = x.shape[1]
