@@ -170,6 +170,20 @@ class DeviceMoeLayer:
             out = frag16_to_rows(out, out.shape[0], out.shape[1], out.dtype)
         return out
 
+    def to_pinned(self) -> Any:
+        """A copy of the whole layer buffer in a new pinned host buffer (``HostBuffer``; the
+        caller frees it with ``free_pinned_host``): a layer as the offload runtime streams
+        it from host memory."""
+        pin = self.backend.alloc_pinned_host(self.layer.nbytes)
+        try:
+            self.backend.copy_d2h_ptr_async(ctypes.addressof(ctypes.c_char.from_buffer(pin.view)),
+                                            self.buf.handle, self.layer.nbytes, self.stream)
+            self.backend.synchronize_stream(self.stream)
+        except BaseException:
+            self.backend.free_pinned_host(pin)
+            raise
+        return pin
+
     def write(self, offset: int, arr: np.ndarray) -> None:
         """Copy a host array into the layer buffer at byte ``offset`` (synchronous)."""
         arr = np.ascontiguousarray(arr)
