@@ -5,9 +5,19 @@
 // Qwen3NextExecutor._moe_mlp_block (offload_runtime/executors/qwen3_next.py:273-333).
 // Everything runs on the caller's stream out of the caller's workspace; nothing is
 // allocated here.
+#include <atomic>
+#include <mutex>
+
 #include "mx_common.h"
 #include "mx_internal.h"
 #include "mx_dispatch_dev.h"
+
+// Workspace of mx_moe_forward_noalloc: one array per device, part of the library's code
+// object, so that entry point needs no allocation.  Host code must never use this name as
+// a device address (on the host it is only a stand-in symbol); it uses the per-device
+// address hipGetSymbolAddress returns (noalloc_scratch below).  No byte of it needs to
+// start at zero: every stage writes all the workspace that a later stage reads.
+static __device__ __align__(256) unsigned char scratch[MX_NOALLOC_MAX_WORKSPACE];
 
 namespace {
 
@@ -44,7 +54,7 @@ bool use_decode_router(const MxMoeDesc* d, const MxMoeWeights* w, int T, const f
 }
 
 int layout(const MxMoeDesc* d, int T, void* ws, MxMoeViews* v, size_t* total,
-           void** scratch = nullptr) {
+           void** dscratch = nullptr) {
   MX_TRY(check_desc(d));
   if (T < 0) return MX_ERR_INVALID;
   const int Tn = T > 0 ? T : 1;
@@ -85,7 +95,7 @@ int layout(const MxMoeDesc* d, int T, void* ws, MxMoeViews* v, size_t* total,
   size_t dscr = 0;
   MX_TRY(mx_dispatch_scratch_size(Tn, d->top_k, d->n_experts, &dscr));
   void* dispatch_scratch = c.take(dscr);
-  if (scratch) *scratch = dispatch_scratch;
+  if (dscratch) *dscratch = dispatch_scratch;
   if (v) *v = t;
   if (total) *total = mx_align_up(c.off, 256);
   return MX_OK;
@@ -103,7 +113,7 @@ bool select_in_gate_up(const MxMoeDesc* d, const MxMoeWeights* w, int T, const f
 }
 
 int run_stage(int stage, const MxMoeDesc* d, const MxMoeWeights* w, const float* x, float* out,
-              int T, const MxMoeViews& v, void* scratch, hipStream_t s, bool sel1) {
+              int T, const MxMoeViews& v, void* dscratch, hipStream_t s, bool sel1) {
   const int has_sh = d->shared_inter > 0;
   const bool decode = use_decode_router(d, w, T, x);
   if (decode && (stage == 0 || stage == 2 || stage == 3)) return MX_OK;  // in stage 1
@@ -128,9 +138,9 @@ int run_stage(int stage, const MxMoeDesc* d, const MxMoeWeights* w, const float*
                             v.topk_w, v.shared_w, s);
     case 3:
       // Many-workgroup dispatch once the single workgroup's serial token walk dominates.
-      if (scratch && T >= 512 && d->n_experts * 48 <= 64 * 1024)
+      if (dscratch && T >= 512 && d->n_experts * 48 <= 64 * 1024)
         return mx_dispatch_chunked(v.topk_ids, v.topk_w, v.shared_w, T, d->top_k, d->n_experts,
-                                   has_sh, v.m_blk, scratch, v.counts, v.offsets, v.sorted_tok,
+                                   has_sh, v.m_blk, dscratch, v.counts, v.offsets, v.sorted_tok,
                                    v.sorted_w, v.pair_pos, v.g_expert, v.g_start, v.g_count,
                                    v.n_groups, v.mt_group, v.mt_row0, v.n_mtiles, s);
       return mx_dispatch(v.topk_ids, v.topk_w, v.shared_w, T, d->top_k, d->n_experts, has_sh,
@@ -193,13 +203,13 @@ int forward(const MxMoeDesc* d, const MxMoeWeights* w, const float* x, float* ou
   if (T == 0) return MX_OK;
   MxMoeViews v;
   size_t need = 0;
-  void* scratch = nullptr;
-  MX_TRY(layout(d, T, ws, &v, &need, &scratch));
+  void* dscratch = nullptr;
+  MX_TRY(layout(d, T, ws, &v, &need, &dscratch));
   if (ws_bytes < need) return MX_ERR_WORKSPACE;
   const bool sel1 = select_in_gate_up(d, w, T, x, st_begin, st_end);
   for (int st = st_begin; st < st_end; ++st) {
     if (events) MX_TRY(mx_status(hipEventRecord((hipEvent_t)events[st], s)));
-    MX_TRY(run_stage(st, d, w, x, out, T, v, scratch, s, sel1));
+    MX_TRY(run_stage(st, d, w, x, out, T, v, dscratch, s, sel1));
   }
   if (events) MX_TRY(mx_status(hipEventRecord((hipEvent_t)events[MX_N_STAGES], s)));
   return MX_OK;
@@ -244,4 +254,44 @@ extern "C" int mx_moe_forward_stages(const MxMoeDesc* desc, const MxMoeWeights* 
     return MX_ERR_INVALID;
   return forward(desc, weights, x, out, tokens, workspace, workspace_bytes, (hipStream_t)stream,
                  nullptr, stage_begin, stage_end);
+}
+
+// ---- no-allocation entry ------------------------------------------------------------------
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_addr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the current device, looked up once per device (with
+// that device current) and kept.
+int noalloc_scratch(void** addr) {
+  int dev = 0;
+  MX_TRY(mx_status(hipGetDevice(&dev)));
+  if (dev < 0 || dev >= kMaxDevices) return MX_ERR_UNSUPPORTED;
+  void* p = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_addr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      MX_TRY(mx_status(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))));
+      if (!p) return MX_ERR_UNSUPPORTED;
+      g_scratch_addr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *addr = p;
+  return MX_OK;
+}
+
+}  // namespace
+
+extern "C" int mx_moe_forward_noalloc(const MxMoeDesc* desc, const MxMoeWeights* weights,
+                                      const float* x, float* out, int32_t tokens, void* stream) {
+  size_t need = 0;
+  MX_TRY(layout(desc, tokens, nullptr, nullptr, &need));
+  if (need > (size_t)MX_NOALLOC_MAX_WORKSPACE) return MX_ERR_WORKSPACE;
+  void* ws = nullptr;
+  MX_TRY(noalloc_scratch(&ws));
+  return forward(desc, weights, x, out, tokens, ws, (size_t)MX_NOALLOC_MAX_WORKSPACE,
+                 (hipStream_t)stream, nullptr);
 }

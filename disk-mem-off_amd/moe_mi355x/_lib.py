@@ -34,6 +34,7 @@ MX_LAYOUT_ROWS = 0
 MX_LAYOUT_FRAG16 = 1
 
 MX_N_STAGES = 7
+MX_NOALLOC_MAX_WORKSPACE = 16 << 20
 STAGE_NAMES = ("rmsnorm", "router_logits", "router_topk", "dispatch", "expert_gate_up",
                "expert_down", "combine")
 
@@ -158,6 +159,8 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "mx_moe_views": (ctypes.c_int, [P(MxMoeDesc), c_int32, c_void_p, P(MxMoeViews)]),
     "mx_moe_forward": (ctypes.c_int, [P(MxMoeDesc), P(MxMoeWeights), c_void_p, c_void_p,
                                       c_int32, c_void_p, c_size_t, c_void_p]),
+    "mx_moe_forward_noalloc": (ctypes.c_int, [P(MxMoeDesc), P(MxMoeWeights), c_void_p,
+                                              c_void_p, c_int32, c_void_p]),
     "mx_moe_forward_profiled": (ctypes.c_int, [P(MxMoeDesc), P(MxMoeWeights), c_void_p,
                                                c_void_p, c_int32, c_void_p, c_size_t,
                                                c_void_p, P(c_void_p), c_int32]),

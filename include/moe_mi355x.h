@@ -4,7 +4,8 @@
  * Every entry point returns int: 0 on success, a positive hipError_t code when a HIP
  * runtime call failed, or a negative MX_ERR_* code for argument errors detected on the
  * host.  No entry point throws across the ABI and no hot-path entry point allocates
- * device memory: the caller owns every buffer, including the workspace.
+ * device memory: the caller owns every buffer, including the workspace (or, for
+ * mx_moe_forward_noalloc, the library's own per-device scratch array stands in for it).
  *
  * Pointers are plain addresses.  "Device" pointers are hipMalloc'd (or offsets into a
  * hipMalloc'd layer buffer); streams and events are hipStream_t / hipEvent_t passed as
@@ -203,6 +204,20 @@ int mx_moe_forward_profiled(const MxMoeDesc* desc, const MxMoeWeights* weights,
                             const float* x, float* out, int32_t tokens, void* workspace,
                             size_t workspace_bytes, void* stream, void* const* events,
                             int32_t n_events);
+
+/* No counterpart in the reference.  mx_moe_forward for callers that cannot allocate device
+ * memory: code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.  The same computation, without the workspace arguments: the stages run out of
+ * a scratch array of MX_NOALLOC_MAX_WORKSPACE bytes that the library holds on every device
+ * it runs on until the process ends.  Nothing is allocated and no memset is issued.
+ * Returns MX_ERR_WORKSPACE when mx_moe_workspace_size(desc, tokens) exceeds that size
+ * (16 MiB: GLM-4.7 shapes up to 64 tokens, Qwen3-Next shapes up to 128).  Every call on
+ * one device shares that device's scratch: calls that overlap on one device (other
+ * streams, other host threads) race and must be serialised by the caller; calls on one
+ * stream are ordered by it.                                                            */
+#define MX_NOALLOC_MAX_WORKSPACE (16u << 20)
+int mx_moe_forward_noalloc(const MxMoeDesc* desc, const MxMoeWeights* weights, const float* x,
+                           float* out, int32_t tokens, void* stream);
 
 /* ---- individual stages (each replaces the reference lines cited) -------------------- */
 

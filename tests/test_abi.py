@@ -84,3 +84,18 @@ def test_error_strings():
         _lib.check(_lib.MX_ERR_INVALID, "x")
     with pytest.raises(RuntimeError):
         _lib.check(_lib.MX_ERR_UNSUPPORTED, "x")
+
+
+def test_noalloc_refuses_batches_beyond_its_scratch_on_the_host():
+    """mx_moe_forward_noalloc checks the batch's workspace against its fixed scratch before
+    any HIP call: an oversized batch or a bad descriptor is refused here, without a GPU."""
+    lib = _lib.load()
+    w = _lib.MxMoeWeights()
+    big = _desc(hidden=5120, inter=1536, shared_inter=1536, n_experts=160, top_k=8)
+    T = 1
+    while _ws(big, T)[1] <= _lib.MX_NOALLOC_MAX_WORKSPACE:
+        T *= 2
+    assert lib.mx_moe_forward_noalloc(ctypes.byref(big), ctypes.byref(w), None, None, T,
+                                      None) == _lib.MX_ERR_WORKSPACE
+    assert lib.mx_moe_forward_noalloc(ctypes.byref(_desc(top_k=0)), ctypes.byref(w), None,
+                                      None, 4, None) == _lib.MX_ERR_INVALID
