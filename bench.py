@@ -47,6 +47,12 @@ from moe_mi355x.workloads import (HBM_PEAK, MFMA_F16_PEAK, MFMA_F32_PEAK, call_t
 
 METRIC = "MoE-layer tokens/s at decode (HBM GB/s %peak) and prefill (MFMA %peak), 1 GPU"
 SEED = 2026
+LAYER_SEED_STEP = 1000
+# Decode workloads cycle this many resident layers (GLM-4.7: 4 x 7.6 GB fp16): one decode
+# step's routed experts (71 MB for Qwen3-Next at one token, 214 MB int8 / 426 MB fp16 for
+# GLM-4.7) fit or half fit in the 256 MB Infinity Cache, so re-running one layer would
+# time cache hits rather than HBM reads.
+DECODE_LAYERS = 4
 
 
 def log(msg: str) -> None:
@@ -54,33 +60,42 @@ def log(msg: str) -> None:
 
 
 class Case:
-    """One timed workload on a device layer."""
+    """One timed workload: a block call per step on device-resident layers.
 
-    def __init__(self, backend, stream, layer: DeviceMoeLayer, shape: syn.MoeShape, wdt: str,
-                 tokens: int, mode: int, x: np.ndarray):
-        self.backend, self.stream, self.layer = backend, stream, layer
+    Decode steps cycle through ``layers`` (distinct resident layers of the same shape, one
+    per step in turn), as a decode walks the model's layers: a step never finds the
+    previous step's expert weights in the 256 MB Infinity Cache, so the measured rate is
+    HBM traffic.  Each layer has its own workspace and pointer table; the input and
+    output buffers are shared."""
+
+    def __init__(self, backend, stream, layers: list[DeviceMoeLayer], shape: syn.MoeShape,
+                 wdt: str, tokens: int, mode: int, x: np.ndarray):
+        self.backend, self.stream, self.layers = backend, stream, list(layers)
         self.shape, self.wdt, self.T = shape, wdt, tokens
-        self.cfg = layer.config(top_k=shape.top_k, router_mode=mode,
-                                routed_scaling=shape.routed_scaling, eps=shape.eps)
+        self.cfg = self.layers[0].config(top_k=shape.top_k, router_mode=mode,
+                                         routed_scaling=shape.routed_scaling, eps=shape.eps)
         self.desc = self.cfg.desc()
-        self.weights = layer.prepare(self.cfg, tokens)
-        r = layer.runner
+        self.weights = [lay.prepare(self.cfg, tokens) for lay in self.layers]
+        r = self.layers[0].runner
         self.x_dev = r._io["x"].handle
         self.out_dev = r._io["out"].handle
+        self.n_steps = 0
         xh = np.ascontiguousarray(x, dtype=np.float32)
         backend.copy_h2d_ptr_async(self.x_dev, xh.ctypes.data, xh.nbytes, stream)
         backend.synchronize_stream(stream)
 
-    def step(self, events=None):
-        self.layer.runner.forward_device(self.desc, self.weights, self.x_dev, self.out_dev,
-                                         self.T, self.stream, events)
+    def step(self, events=None, layer: int | None = None):
+        j = self.n_steps % len(self.layers) if layer is None else layer
+        self.n_steps += 1
+        self.layers[j].runner.forward_device(self.desc, self.weights[j], self.x_dev,
+                                             self.out_dev, self.T, self.stream, events)
 
     def run(self, steps: int, warmup: int) -> dict:
         """Timed pass: K steps bracketed by two HIP events on the launch stream.  Then a
         second pass of K steps records an event between every stage (each in-stream timing
         event costs ~4-5 us of GPU time, so the stage pass is kept out of the timed one)."""
         b = self.backend
-        for _ in range(warmup):
+        for _ in range(max(warmup, len(self.layers))):
             self.step()
         b.synchronize_stream(self.stream)
         start, end = b.create_timing_event(), b.create_timing_event()
@@ -101,19 +116,26 @@ class Case:
                 b.destroy_event(x)
         b.destroy_event(start)
         b.destroy_event(end)
-        v = self.layer.runner.views(self.desc, self.T)
-        n_groups = int(read_device(b, v.n_groups, np.int32, 1, self.stream)[0])
+        # every layer's workspace holds its last call's routing
+        n_active = []
+        for lay in self.layers:
+            v = lay.runner.views(self.desc, self.T)
+            ng = int(read_device(b, v.n_groups, np.int32, 1, self.stream)[0])
+            n_active.append(ng - (1 if self.shape.shared_inter else 0))
+        v = self.layers[0].runner.views(self.desc, self.T)
         counts = read_device(b, v.counts, np.int32, self.shape.n_experts, self.stream)
-        n_active = n_groups - (1 if self.shape.shared_inter else 0)
-        tr = call_traffic(self.shape, self.wdt, self.T, n_active)
+        tr = call_traffic(self.shape, self.wdt, self.T, float(np.mean(n_active)))
         ms = total_ms / steps
         st = stage.mean(axis=0)
         return {"ms_per_step": ms, "tokens_per_s": self.T / (ms / 1e3), "stage_ms": st,
-                "n_active": n_active, "counts": counts, "traffic": tr,
+                "n_active": float(np.mean(n_active)), "counts": counts, "traffic": tr,
+                "distinct_layers": len(self.layers),
                 "layer_hbm_frac": tr["layer_bytes"] / (ms / 1e3) / HBM_PEAK,
                 "layer_mfma_frac": tr["layer_flops"] / (ms / 1e3) / MFMA_F16_PEAK}
 
     def output(self) -> np.ndarray:
+        """Output of one call on the first layer (the one the parity checks read)."""
+        self.step(layer=0)
         return read_device(self.backend, self.out_dev, np.float32, self.T * self.shape.hidden,
                            self.stream).reshape(self.T, -1)
 
@@ -125,7 +147,8 @@ def summarize(res: dict, name: str, wdt: str) -> dict:
     peak_flops = MFMA_F32_PEAK if wdt == "float32" else MFMA_F16_PEAK
     return {
         "workload": name, "tokens_per_s": round(res["tokens_per_s"], 1),
-        "ms_per_step": round(res["ms_per_step"], 4), "active_experts": res["n_active"],
+        "ms_per_step": round(res["ms_per_step"], 4), "active_experts": round(res["n_active"], 2),
+        "distinct_layers": res["distinct_layers"],
         "layer_GBps": round(tr["layer_bytes"] / (res["ms_per_step"] / 1e3) / 1e9, 1),
         "layer_hbm_frac": round(res["layer_hbm_frac"], 4),
         "layer_mfma_frac": round(tr["layer_flops"] / (res["ms_per_step"] / 1e3) / peak_flops, 4),
@@ -153,7 +176,7 @@ def profiled_traffic(workload: str, kernel: str) -> float | None:
     return None
 
 
-def cpu_baseline(layer: DeviceMoeLayer, shape: syn.MoeShape, x: np.ndarray, budget_s: float):
+def cpu_baseline(layer: DeviceMoeLayer, shape: syn.MoeShape, x: np.ndarray, runs: int = 5):
     """Oracle in the reference's loop structure on the host cores (routed experts only are
     copied to the host; the copy is not timed).  Returns (baseline dict, oracle output)."""
     from oracle import moe_oracle as orc
@@ -178,13 +201,10 @@ def cpu_baseline(layer: DeviceMoeLayer, shape: syn.MoeShape, x: np.ndarray, budg
         threads, blas_name = len(os.sched_getaffinity(0)), "unknown"
     out = orc.moe_block_faithful(x, t, spec)  # warm-up, and the full-size parity reference
     times = []
-    t_end = time.perf_counter() + budget_s
-    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 10):
+    for _ in range(max(1, runs)):
         t0 = time.perf_counter()
         orc.moe_block_faithful(x, t, spec)
         times.append(time.perf_counter() - t0)
-        if time.perf_counter() > t_end and len(times) >= 1:
-            break
     med = float(np.median(times))
     cpu_model = "unknown"
     try:
@@ -199,7 +219,8 @@ def cpu_baseline(layer: DeviceMoeLayer, shape: syn.MoeShape, x: np.ndarray, budg
             "sample": (f"full GLM-4.7-shape layer, {x.shape[0]} tokens, NumPy oracle in the "
                        f"reference loop structure (per-expert BLAS, per-token scatter), fp16 "
                        f"weights promoted to fp32; median of {len(times)} runs "
-                       f"({med * 1e3:.1f} ms each) after 1 warm-up; {blas_name}, "
+                       f"({med * 1e3:.1f} ms; min {min(times) * 1e3:.1f}, max "
+                       f"{max(times) * 1e3:.1f}) after 1 warm-up; {blas_name}, "
                        f"{len(os.sched_getaffinity(0))} host cores visible, {cpu_model}, "
                        f"numpy {np.__version__}")}
     return base, out, ids
@@ -375,11 +396,7 @@ def stream_case(backend, shape: syn.MoeShape, tokens: tuple[int, ...], n_layers:
             dl = DeviceMoeLayer.synthetic(backend, shape, SEED + 100 + i, st, weight_dtype="int8",
                                           param_dtype="float32", layer_id=i)
             try:
-                pin = backend.alloc_pinned_host(dl.layer.nbytes)
-                blobs[i] = pin
-                addr = ctypes.addressof(ctypes.c_char.from_buffer(pin.view))
-                backend.copy_d2h_ptr_async(addr, dl.buf.handle, dl.layer.nbytes, st)
-                backend.synchronize_stream(st)
+                blobs[i] = dl.to_pinned()
                 layers.append(dl.layer)
             finally:
                 dl.close()
@@ -444,6 +461,11 @@ def main() -> int:
     ap.add_argument("--weight-layout", choices=("frag16", "rows"), default="frag16",
                     help="expert weight layout in HBM: re-tiled 1 KiB MFMA fragments (one "
                          "device pass after the layer is built) or the loader's row-major")
+    ap.add_argument("--distinct-layers", type=int, default=DECODE_LAYERS,
+                    help="resident layers a decode workload cycles through, one per step "
+                         "(1 re-reads the same layer every step)")
+    ap.add_argument("--cpu-runs", type=int, default=5,
+                    help="timed runs of the CPU baseline (median reported)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a 1 GiB device copy (HBM counter calibration)")
     args = ap.parse_args()
@@ -466,21 +488,35 @@ def main() -> int:
     def want(name: str) -> bool:
         return only is None or only == name
 
-    # ---- GLM-4.7 fp16 layer -------------------------------------------------------------
+    def build_layers(shape: syn.MoeShape, wdt: str, n: int) -> list[DeviceMoeLayer]:
+        """Layer 0 from SEED (the layer the parity checks and the single-layer workloads
+        use), layers 1.. from other seeds (other routing, other weights)."""
+        t0 = time.perf_counter()
+        out = []
+        for i in range(n):
+            lay = DeviceMoeLayer.synthetic(backend, shape, SEED + LAYER_SEED_STEP * i, stream,
+                                           weight_dtype=wdt, param_dtype="float32",
+                                           layer_id=i)
+            if args.weight_layout == "frag16":
+                lay.tile()
+            out.append(lay)
+        log(f"{shape.arch} {wdt}: {n} layer(s) of {out[0].layer.nbytes / 1e9:.2f} GB built on "
+            f"device in {time.perf_counter() - t0:.1f}s")
+        return out
+
+    nl = max(1, args.distinct_layers)
+
+    # ---- GLM-4.7 fp16 layers ------------------------------------------------------------
     need_glm = only is None or only.startswith("glm47_fp16")
     if need_glm:
-        t0 = time.perf_counter()
-        layer = DeviceMoeLayer.synthetic(backend, G, SEED, stream, weight_dtype="float16",
-                                         param_dtype="float32")
-        if args.weight_layout == "frag16":
-            layer.tile()
-        log(f"GLM-4.7 fp16 layer: {layer.layer.nbytes / 1e9:.2f} GB built on device in "
-            f"{time.perf_counter() - t0:.1f}s")
+        decode_wanted = only is None or "decode" in only
+        layers = build_layers(G, "float16", nl if decode_wanted else 1)
+        layer = layers[0]
         mode = _lib.MX_ROUTER_SIGMOID_SELECT_BIAS
         if only is None:
             T = args.tokens
             x = syn.make_inputs(SEED, T, G.hidden)
-            case = Case(backend, stream, layer, G, "float16", T, mode, x)
+            case = Case(backend, stream, layers, G, "float16", T, mode, x)
             res = case.run(args.steps, args.warmup)
             head = summarize(res, f"glm47_fp16_decode_t{T}", "float16")
             log(f"headline {head['workload']}: {head['tokens_per_s']:.0f} tok/s, "
@@ -488,7 +524,7 @@ def main() -> int:
             gpu_out = case.output()
             result.update({"head": head, "res": res})
             if not args.no_cpu:
-                base, ref_out, ref_ids = cpu_baseline(layer, G, x, budget_s=20.0)
+                base, ref_out, ref_ids = cpu_baseline(layer, G, x, runs=args.cpu_runs)
                 v = layer.runner.views(case.desc, T)
                 gpu_ids = read_device(backend, v.topk_ids, np.int32, T * G.top_k, stream)
                 result["cpu_baseline"] = base
@@ -504,7 +540,7 @@ def main() -> int:
                     continue
                 # the headline batch keeps the headline's inputs when run alone (profiling)
                 x = syn.make_inputs(SEED if T == args.tokens else SEED + T, T, G.hidden)
-                r = Case(backend, stream, layer, G, "float16", T, mode, x).run(
+                r = Case(backend, stream, layers, G, "float16", T, mode, x).run(
                     min(args.steps, 30), 5)
                 sweep[name] = summarize(r, name, "float16")
                 log(f"{name}: {sweep[name]['tokens_per_s']} tok/s")
@@ -521,7 +557,8 @@ def main() -> int:
                 bb = np.ascontiguousarray(bias, np.float32)
                 backend.copy_h2d_ptr_async(layer.buf.handle + off, bb.ctypes.data, bb.nbytes, stream)
                 backend.synchronize_stream(stream)
-                r = Case(backend, stream, layer, G, "float16", T, mode, x).run(
+                # one 7.6 GB layer: every step streams far more than the Infinity Cache holds
+                r = Case(backend, stream, [layer], G, "float16", T, mode, x).run(
                     min(args.steps, 20), 3)
                 s = summarize(r, name, "float16")
                 cnt = np.sort(r["counts"])[::-1]
@@ -529,43 +566,43 @@ def main() -> int:
                              "median_load": int(np.median(cnt)), "top5": cnt[:5].tolist()}
                 sweep[name] = s
                 log(f"{name}: {s['tokens_per_s']} tok/s, mfma {s['layer_mfma_frac']}")
-        layer.close()
+        for lay in layers:
+            lay.close()
 
-    # ---- GLM-4.7 per-row int8 layer ----------------------------------------------------------
+    # ---- GLM-4.7 per-row int8 layers ---------------------------------------------------------
     if not args.no_sweep and (only is None or (only.startswith("glm47_int8")
                                                and "stream" not in only)):
-        layer = DeviceMoeLayer.synthetic(backend, G, SEED, stream, weight_dtype="int8",
-                                         param_dtype="float32")
-        if args.weight_layout == "frag16":
-            layer.tile()
+        layers = build_layers(G, "int8", nl)
         for T in (1, 16):
             name = f"glm47_int8_decode_t{T}"
             if not want(name):
                 continue
             x = syn.make_inputs(SEED + T, T, G.hidden)
-            r = Case(backend, stream, layer, G, "int8", T, _lib.MX_ROUTER_SIGMOID_SELECT_BIAS,
+            r = Case(backend, stream, layers, G, "int8", T, _lib.MX_ROUTER_SIGMOID_SELECT_BIAS,
                      x).run(min(args.steps, 30), 5)
             sweep[name] = summarize(r, name, "int8")
             log(f"{name}: {sweep[name]['tokens_per_s']} tok/s")
-        layer.close()
+        for lay in layers:
+            lay.close()
 
-    # ---- Qwen3-Next fp16 layer ---------------------------------------------------------------
+    # ---- Qwen3-Next fp16 layers --------------------------------------------------------------
     if not args.no_sweep and (only is None or only.startswith("qwen3next_fp16")):
         Q = syn.QWEN3_NEXT
-        layer = DeviceMoeLayer.synthetic(backend, Q, SEED, stream, weight_dtype="float16",
-                                         param_dtype="float32")
-        if args.weight_layout == "frag16":
-            layer.tile()
+        one_wanted = only is None or only == "qwen3next_fp16_t1"
+        layers = build_layers(Q, "float16", nl if one_wanted else 1)
         for T in (1, 4096):
             name = f"qwen3next_fp16_t{T}"
             if not want(name):
                 continue
             x = syn.make_inputs(SEED + T, T, Q.hidden)
-            r = Case(backend, stream, layer, Q, "float16", T, _lib.MX_ROUTER_SOFTMAX, x).run(
+            # 4096 tokens touch all 512 experts (3.2 GB) every step: one layer suffices
+            use = layers if T <= 64 else layers[:1]
+            r = Case(backend, stream, use, Q, "float16", T, _lib.MX_ROUTER_SOFTMAX, x).run(
                 min(args.steps, 20 if T > 64 else 30), 3)
             sweep[name] = summarize(r, name, "float16")
             log(f"{name}: {sweep[name]['tokens_per_s']} tok/s")
-        layer.close()
+        for lay in layers:
+            lay.close()
 
     # ---- Qwen3-Next linear-attention (Gated DeltaNet) block -------------------------------------
     if not args.no_sweep and (only is None or only.startswith("qwen3next_linattn")):
@@ -622,6 +659,7 @@ def main() -> int:
                    "routed_scaling": G.routed_scaling, "weights": "fp16",
                    "weight_layout": args.weight_layout,
                    "tokens": args.tokens, "active_experts": head["active_experts"],
+                   "distinct_layers": head["distinct_layers"],
                    "parallelism": "single-gpu"},
         "roofline": {"kernel": "k_expert gate/up (fp16 MFMA, fused SiLU*up)", "bound": "hbm",
                      "achieved": round(gu_bytes / gu_s / 1e9, 1), "peak": HBM_PEAK / 1e9,

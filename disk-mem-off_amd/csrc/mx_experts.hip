@@ -46,14 +46,17 @@ __device__ __forceinline__ int4_t mx_ld16(mx_rsrc_t r, uint32_t off) {
 // probe; the decode block: 1.07 -> 0.96 ms).  The prefill kernel keeps the default
 // policy: the sibling m-tiles of a hot expert re-read its weights and find part of them
 // in L2 (with nt the 2048-token prefill slowed from 2.19 to 2.58 ms).
-// Exception: the int8 gate/up launch of single-m-frag tiles without a K split (a decode
-// step touching few experts) streams faster with the default policy (GLM-4.7 int8,
-// 1 token: 25 vs 30 µs).
+// (An exception for the int8 gate/up launch of single-m-frag tiles without a K split,
+// default policy there, measured faster only while the timed steps re-read one layer's
+// experts from the Infinity Cache; with distinct layers per step it is equal, and off.)
 #ifndef MX_W_NT
 #define MX_W_NT 1
 #endif
 #ifndef MX_W_AUX
 #define MX_W_AUX 2  // cache-policy bits of the hinted loads (nt)
+#endif
+#ifndef MX_I8_GU_PLAIN
+#define MX_I8_GU_PLAIN 0  // the int8 exception above (default policy) on or off
 #endif
 template <bool NT>
 __device__ __forceinline__ int4_t mx_ldw16(mx_rsrc_t r, uint32_t off) {
@@ -759,25 +762,42 @@ static int expert_check(const MxMoeDesc* d) {
 #ifndef MX_DEC_UK
 #define MX_DEC_UK 4
 #endif
+#ifndef MX_DEC_UK_I8
+#define MX_DEC_UK_I8 (MX_DEC_UK / 2)
+#endif
 
 // K split inside a block for single-m-frag tiles (m_blk 16).  The split is picked from
 // the number of waves the launch would have unsplit (measured on MI355X, fp16 GLM-4.7 and
 // Qwen3-Next shapes at 1-8 tokens): a launch far below one wave per SIMD gains from more,
 // shorter weight streams; one near a wave per SIMD loses from splitting (gate/up); a
 // launch of several waves per SIMD gains tail balance from short waves.  (Down at one
-// GLM-4.7 token, 1440 waves unsplit: 23.2 us with a 2-way split, 22.6 us with 4-way.)
+// GLM-4.7 token, 1440 waves unsplit: 23.2 us with a 2-way split, 22.6 us with 4-way.
+// Gate/up at one GLM-4.7 token, 864 waves unsplit, distinct layers per step: int8
+// 53.5 -> 50.5 us per block with a 2-way split, fp16 equal within noise.)
+#ifndef MX_KS_GU_LO
+#define MX_KS_GU_LO 1024
+#endif
+#ifndef MX_KS_GU_HI
+#define MX_KS_GU_HI 2048
+#endif
+#ifndef MX_KS_DN_LO
+#define MX_KS_DN_LO 2048
+#endif
+#ifndef MX_KS_DN_HI
+#define MX_KS_DN_HI 4096
+#endif
 static int decode_ksplit(bool gu, long waves_unsplit) {
-  if (gu) return waves_unsplit < 512 ? 2 : (waves_unsplit < 2048 ? 1 : 4);
-  return waves_unsplit < 2048 ? 4 : (waves_unsplit < 4096 ? 2 : 1);
+  if (gu) return waves_unsplit < MX_KS_GU_LO ? 2 : (waves_unsplit < MX_KS_GU_HI ? 1 : 4);
+  return waves_unsplit < MX_KS_DN_LO ? 4 : (waves_unsplit < MX_KS_DN_HI ? 2 : 1);
 }
 
 template <int WF, int MT, bool GU, int KS, int SELV = 0>
 static void launch_expert_ks(const ExpertParams& p, int mt_max, int nmax, hipStream_t s,
                              const SelectParams& sp = SelectParams{}) {
   constexpr int NBI = GU ? MX_DEC_NBI_GU : MX_DEC_NBI_DN;
-  constexpr int UK = (WF == MX_DT_I8) ? (MT >= 4 ? 1 : MX_DEC_UK / 2)
+  constexpr int UK = (WF == MX_DT_I8) ? (MT >= 4 ? 1 : MX_DEC_UK_I8)
                                       : (MT >= 4 ? 2 : MX_DEC_UK);
-  constexpr bool NT = !(WF == MX_DT_I8 && GU && MT == 1 && KS == 1);
+  constexpr bool NT = !(MX_I8_GU_PLAIN && WF == MX_DT_I8 && GU && MT == 1 && KS == 1);
   const dim3 grid(mt_max, mx_ceil_div(nmax, (4 / KS) * 16 * NBI));
   mx_clear_error();
   hipLaunchKernelGGL((k_expert<WF, MT, NBI, GU, UK, KS, NT, SELV>), grid, dim3(256), 0, s, p, sp);
