@@ -1,0 +1,259 @@
+// Dense fp16 GEMM on MFMA for the long-input projections of the attention blocks:
+//   y_s[M, N_s] (fp32, row stride ldy_s) = a[M, K] (fp16, row-major) . W_s[N_s, K]^T
+// for up to MX_GEMM_MAX_SEG weight matrices W_s (fp16, nn.Linear row-major) that share the
+// activations a (the q / k / v projections, or qkvz and ba, in one launch).
+// Reference: linear_t = x @ W.T (offload_runtime/executors/_common.py:101-103) at
+// qwen3_next.py:170-174, :211, :231, :245 and :268.
+//
+// Block tile BM x BN over one weight segment; the reduction runs in stages of 32 columns
+// (one MFMA k-step).  Both operands of a stage are copied from global memory straight into
+// LDS by the buffer loads' LDS mode (no register staging), into a ring of NS stage slots:
+// while the waves compute stage s, the copies of stages s + 1 .. s + NS - 1 are in flight.
+// Each copy instruction moves one 16-row x 32-column fragment (1 KiB); the LDS mode stores
+// lane l's 16 bytes at 16 l, so the lane-to-(row, chunk) map of the copy fixes the layout
+// of the fragment in LDS (see below: coalesced rows, rotated chunks, no padding).
+// A stage is waited for with an explicit vmcnt (the copies are this loop's only vector
+// memory operations) and a barrier without a memory fence: a fence on LDS would also wait
+// for every copy still in flight, which would empty the ring at every stage.
+// Each wave owns a WM x WN sub-tile (WM / 16 x WN / 16 accumulator tiles of
+// v_mfma_f32_16x16x32_f16), so every A fragment read from LDS feeds WN / 16 MFMAs and
+// every B fragment WM / 16.  Global reads go through buffer descriptors: rows past M or
+// past N_s read zero.  K must be a multiple of 32 (MX_ERR_UNSUPPORTED otherwise).
+//
+// Fragment layout (lane = 16 q + j): an activation fragment lane holds a[m0 + j][k0 + 8 q ..
+// +8], a weight fragment lane W[n0 + j][k0 + 8 q .. +8]; with the weights as the MFMA's A
+// operand the accumulator lane holds y[m0 + j][n0 + 4 q + r], r = 0..3.
+#include "mx_common.h"
+#include "mx_internal.h"
+
+namespace {
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr uint32_t kRsrcDw3 = 0x00020000;
+constexpr uint32_t kOob = 0x80000000u;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, kRsrcDw3);
+}
+
+struct GemmSeg {
+  const half_t* w;  // [N, K]
+  float* y;         // [M, ldy]
+  int n;            // N of the segment
+  int ldy;
+  int nblk;         // column blocks of the segment
+};
+
+struct GemmArgs {
+  const half_t* a;  // [M, K]
+  int M, K;
+  int mblk;         // row blocks
+  int nseg;
+  GemmSeg seg[MX_GEMM_MAX_SEG];
+};
+
+constexpr int BK = 32;  // reduction columns per stage (one MFMA k-step)
+#ifndef MX_GEMM_NS
+#define MX_GEMM_NS 4  // stage slots in the LDS ring
+#endif
+
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// One 16-byte piece per lane from global memory into LDS: lane l's piece lands at
+// dst + 16 l (the buffer load's LDS mode).
+__device__ __forceinline__ void copy_to_lds16(rsrc_t r, char* dst, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)dst, 16, off, 0, 0, 0);
+}
+
+// Wait until at most n (< 16) vector memory operations of this wave are outstanding, then
+// meet the other waves at a barrier.  No memory fence on the way in (a release fence on
+// LDS would wait for every copy into LDS still in flight); the acquire fence after the
+// barrier keeps the compiler from moving the next LDS reads above it.
+template <int N>
+__device__ __forceinline__ void wait_copies_and_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+template <int BM, int BN, int WM, int WN, int NS, int OCC>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, OCC) void k_gemm_f16_nt(
+    const GemmArgs p) {
+  constexpr int NWN = BN / WN, NW = (BM / WM) * NWN;
+  constexpr int MF = WM / 16, NF = WN / 16;
+  constexpr int FA = BM / 16, FT = FA + BN / 16;  // fragments per stage slot
+  constexpr int SLOT = FT * 1024;
+  constexpr int DPW = FT / NW;                    // copies per wave and stage
+  constexpr int DPA = FA / NW;                    // of which A fragments
+  static_assert(FT % NW == 0 && FA % NW == 0, "fragments must divide among the waves");
+  __shared__ __align__(1024) char lds[NS * SLOT];
+
+  // Blocks are numbered so that consecutive logical ids run on one XCD (hardware block b
+  // goes to XCD b % 8); logical ids walk the row blocks of one column block first, so the
+  // blocks sharing a weight slab run together on one XCD.
+  const int nb_total = gridDim.x;
+  const int b = blockIdx.x;
+  const int logical = (nb_total % 8 == 0) ? (b & 7) * (nb_total >> 3) + (b >> 3) : b;
+  int rem = logical / p.mblk;
+  const int mb = logical - rem * p.mblk;
+  int si = 0;
+#pragma unroll
+  for (int i = 0; i < MX_GEMM_MAX_SEG - 1; ++i)
+    if (si == i && i + 1 < p.nseg && rem >= p.seg[i].nblk) {
+      rem -= p.seg[i].nblk;
+      si = i + 1;
+    }
+  const GemmSeg sg = p.seg[si];
+  const int m0 = mb * BM, n0 = rem * BN;
+  const int M = p.M, K = p.K, N = sg.n;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / NWN, wn = wave % NWN;
+  const int j = lane & 15, q = lane >> 4;
+
+  const rsrc_t ra = make_rsrc(p.a, (uint32_t)((size_t)M * K * 2));
+  const rsrc_t rb = make_rsrc(sg.w, (uint32_t)((size_t)N * K * 2));
+  // The fragments this wave copies: f = wave + i * NW (A fragments first, then B); the
+  // lane's source row and its byte offset at stage 0.
+  // Copy lane l loads row cr = l / 4 of its fragment, 16-byte chunk cq = (l % 4 - cr / 4)
+  // mod 4, so every 4 consecutive lanes read one row's 64 contiguous bytes (the address
+  // unit merges them); the chunk rotation by cr / 4 makes the MFMA operand reads below
+  // (lane (j, q) reads row j, chunk q at position 4 j + (q + j / 4) mod 4) hit 16 distinct
+  // 16-byte bank groups per 16 lanes.
+  const int cr = lane >> 2, cq = ((lane & 3) - (cr >> 2)) & 3;
+  const int rpos = (4 * j + ((q + (j >> 2)) & 3)) * 16;
+  uint32_t goff[DPW];
+#pragma unroll
+  for (int i = 0; i < DPW; ++i) {
+    const int f = wave + i * NW;
+    if (i < DPA) {
+      const int row = m0 + 16 * f + cr;
+      goff[i] = row < M ? (uint32_t)row * (uint32_t)K * 2 + cq * 16 : kOob;
+    } else {
+      const int row = n0 + 16 * (f - FA) + cr;
+      goff[i] = row < N ? (uint32_t)row * (uint32_t)K * 2 + cq * 16 : kOob;
+    }
+  }
+  // K is a multiple of BK, so every piece of a stage lies inside its row; rows past M / N
+  // have offsets at or above kOob, which stay past the end of the descriptor.
+  auto issue = [&](int st) {
+    char* slot = lds + (st % NS) * SLOT;
+#pragma unroll
+    for (int i = 0; i < DPW; ++i) {
+      const int f = wave + i * NW;
+      copy_to_lds16(i < DPA ? ra : rb, slot + f * 1024, goff[i] + (uint32_t)st * (BK * 2));
+    }
+  };
+
+  // acc[mi][ni] holds the transposed product (the weights are the MFMA's A operand):
+  // lane (j, q) has y[m0 + 16 mi + j][n0 + 16 ni + 4 q + r], r = 0..3, so the epilogue
+  // stores 4 consecutive columns per lane.
+  float4_t acc[MF][NF];
+#pragma unroll
+  for (int mi = 0; mi < MF; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < NF; ++ni) acc[mi][ni] = (float4_t){0.f, 0.f, 0.f, 0.f};
+
+  const int nst = (K + BK - 1) / BK;
+#pragma unroll
+  for (int s0 = 0; s0 < NS - 1; ++s0)
+    if (s0 < nst) issue(s0);
+  for (int st = 0; st < nst; ++st) {
+    // This wave's copies of stage st are done (the NS - 2 later stages may still be in
+    // flight), then every wave's are, and every wave has finished computing stage st - 1,
+    // whose slot the next copies overwrite.
+    if (st + NS - 1 <= nst)
+      wait_copies_and_barrier<(NS - 2) * DPW>();
+    else
+      wait_copies_and_barrier<0>();
+    if (st + NS - 1 < nst) issue(st + NS - 1);
+    const char* slot = lds + (st % NS) * SLOT;
+    int4_t af[MF], bf[NF];
+#pragma unroll
+    for (int mi = 0; mi < MF; ++mi) af[mi] = *(const int4_t*)(slot + (wm * MF + mi) * 1024 + rpos);
+#pragma unroll
+    for (int ni = 0; ni < NF; ++ni)
+      bf[ni] = *(const int4_t*)(slot + (FA + wn * NF + ni) * 1024 + rpos);
+#pragma unroll
+    for (int mi = 0; mi < MF; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < NF; ++ni)
+        acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+            __builtin_bit_cast(half8_t, bf[ni]), __builtin_bit_cast(half8_t, af[mi]),
+            acc[mi][ni], 0, 0, 0);
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // no copy into LDS outlives the block (vmcnt 0)
+
+  // Epilogue: fp32 rows of the segment's output, 4 consecutive columns per lane (a
+  // 16-byte store when the row stride and the base allow it).
+  const bool vec = (sg.ldy & 3) == 0 && ((uintptr_t)sg.y & 15) == 0;
+#pragma unroll
+  for (int mi = 0; mi < MF; ++mi) {
+    const int m = m0 + wm * WM + mi * 16 + j;
+    if (m >= M) continue;
+    float* yrow = sg.y + (size_t)m * sg.ldy;
+#pragma unroll
+    for (int ni = 0; ni < NF; ++ni) {
+      const int n = n0 + wn * WN + ni * 16 + 4 * q;
+      if (vec && n + 3 < N) {
+        *(float4_t*)(yrow + n) = acc[mi][ni];
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (n + r < N) yrow[n + r] = acc[mi][ni][r];
+      }
+    }
+  }
+}
+
+template <int BM, int BN, int WM, int WN, int NS, int OCC>
+int launch(GemmArgs& args, const MxGemmSeg* segs, int nseg, hipStream_t s) {
+  args.mblk = mx_ceil_div(args.M, BM);
+  long blocks = 0;
+  for (int i = 0; i < nseg; ++i) {
+    args.seg[i].nblk = mx_ceil_div(segs[i].n, BN);
+    blocks += (long)args.seg[i].nblk * args.mblk;
+  }
+  if (blocks <= 0 || blocks > (1l << 31) - 1) return MX_ERR_UNSUPPORTED;
+  constexpr int threads = (BM / WM) * (BN / WN) * 64;
+  mx_clear_error();
+  hipLaunchKernelGGL((k_gemm_f16_nt<BM, BN, WM, WN, NS, OCC>), dim3((unsigned)blocks), dim3(threads), 0,
+                     s, args);
+  return mx_launch_status();
+}
+
+}  // namespace
+
+int mx_gemm_f16(const void* a, int M, int K, const MxGemmSeg* segs, int nseg, hipStream_t s) {
+  if (!a || !segs || nseg < 1 || nseg > MX_GEMM_MAX_SEG || M <= 0 || K <= 0)
+    return MX_ERR_INVALID;
+  if (K % BK) return MX_ERR_UNSUPPORTED;  // whole stages of 32 columns
+  if (!mx_aligned16(a)) return MX_ERR_ALIGNMENT;
+  if ((long)M * K * 2 >= (1l << 31)) return MX_ERR_UNSUPPORTED;
+  GemmArgs args{};
+  args.a = (const half_t*)a;
+  args.M = M;
+  args.K = K;
+  args.nseg = nseg;
+  long cols = 0;
+  for (int i = 0; i < nseg; ++i) {
+    const MxGemmSeg& g = segs[i];
+    if (!g.w || !g.y || g.n <= 0 || g.ldy < g.n) return MX_ERR_INVALID;
+    if (!mx_aligned16(g.w)) return MX_ERR_ALIGNMENT;
+    if ((long)g.n * K * 2 >= (1l << 31)) return MX_ERR_UNSUPPORTED;
+    args.seg[i].w = (const half_t*)g.w;
+    args.seg[i].y = g.y;
+    args.seg[i].n = g.n;
+    args.seg[i].ldy = g.ldy;
+    cols += g.n;
+  }
+  // 256 x 256 tiles while they give at least two rounds of blocks on 256 CUs; 128 x 128
+  // (four waves, two blocks per CU) otherwise.
+  const long big = (long)mx_ceil_div(M, 256) * mx_ceil_div((int)cols, 256);
+  if (big >= 512) return launch<256, 256, 128, 64, MX_GEMM_NS, 1>(args, segs, nseg, s);
+  return launch<128, 128, 64, 64, MX_GEMM_NS, 2>(args, segs, nseg, s);
+}

@@ -647,10 +647,18 @@ int run_stage(int st, const MxFullAttnDesc* d, const MxFullAttnWeights* w, const
                                s);
     }
     case 1:
+      if (mx_dense_on_gemm(wdt, T, m.H)) {  // q, k and v share h: one GEMM launch
+        const MxGemmSeg g[3] = {{w->q_w, k.v.qg, m.qw, m.qw},
+                                {w->k_w, k.v.k, m.kw, m.kw},
+                                {w->v_w, k.v.v, m.kw, m.kw}};
+        return mx_gemm_f16(h, T, m.H, g, 3, s);
+      }
       return mx_project(k.dw, 0, wdt, w->q_w, T, m.qw, m.H, h, k.v.qg, s);
     case 2:
+      if (mx_dense_on_gemm(wdt, T, m.H)) return MX_OK;  // with q in stage 1
       return mx_project(k.dw, 1, wdt, w->k_w, T, m.kw, m.H, h, k.v.k, s);
     case 3:
+      if (mx_dense_on_gemm(wdt, T, m.H)) return MX_OK;
       return mx_project(k.dw, 2, wdt, w->v_w, T, m.kw, m.H, h, k.v.v, s);
     case 4: {
       const dim3 grid(T, m.nh + m.nkv);

@@ -81,17 +81,21 @@ struct MxDenseTables {
 int mx_dense_linear(int wdt, int tiled, const MxExpertPtrs* entry, const MxDenseTables& tab,
                     int T, int N, int K, const void* a, float* y, hipStream_t s);
 
-// Dense y[T, N] (fp32) = a[T, K] W[N, K]^T on hipBLASLt (dtype MX_DT_F16: fp16 a and W,
-// MX_DT_F32: fp32), fp32 accumulation; ws of ws_bytes (mx_gemm_workspace_bytes()) is the
-// library's workspace.  MX_ERR_UNSUPPORTED when the library has no algorithm for the shape.
-size_t mx_gemm_workspace_bytes();
-int mx_gemm_wt(int dtype, const void* a, const void* w, float* y, int T, int N, int K, void* ws,
-               size_t ws_bytes, hipStream_t s);
+// Dense fp16 GEMM on MFMA (mx_dense_gemm.hip): y_s[M, N_s] (fp32, row stride ldy_s) =
+// a[M, K] (fp16) W_s[N_s, K]^T for up to MX_GEMM_MAX_SEG fp16 weight matrices sharing a.
+#define MX_GEMM_MAX_SEG 3
+struct MxGemmSeg {
+  const void* w;  // [n, K] fp16, row-major (16-byte aligned)
+  float* y;       // [M, ldy] fp32
+  int n;
+  int ldy;
+};
+int mx_gemm_f16(const void* a, int M, int K, const MxGemmSeg* segs, int nseg, hipStream_t s);
 
 // Workspace pieces of the dense projections of an attention block (device pointers):
-// expert-table entries (one per projection), single-group m-tile tables, ones[T] and, for
-// long inputs with fp16 / fp32 weights, the hipBLASLt workspace.
-#define MX_DENSE_BLAS_MIN_TOKENS 65
+// expert-table entries (one per projection), single-group m-tile tables and ones[T] for
+// the grouped-GEMM kernels.  Long inputs with fp16 weights run on mx_gemm_f16 instead.
+#define MX_DENSE_GEMM_MIN_TOKENS 65
 #define MX_DENSE_MAX_ENT 4
 struct MxDenseEntries {
   MxExpertPtrs e[MX_DENSE_MAX_ENT];  // e[i].down / down_scale = projection i's weights
@@ -102,14 +106,17 @@ struct MxDenseWork {
   int* mt_group;
   int* mt_row0;
   float* ones;
-  void* blas_ws;
-  size_t blas_ws_bytes;
   int m_blk, n_mt, n_ent;
 };
 size_t mx_dense_work_bytes(int T, int weight_dtype, int n_ent);
 void mx_dense_work_carve(char* base, int T, int weight_dtype, int n_ent, MxDenseWork* w);
 // Writes the table entries and m-tile tables (one small launch per block call).
 int mx_dense_setup(const MxDenseWork& w, const MxDenseEntries& ents, int T, hipStream_t s);
-// y[T, N] = a[T, K] W^T with W = projection `ent` (wmat, its weights, for the library path).
+// Whether projections of T tokens with these weights and reduction length K run on
+// mx_gemm_f16 (fp16 weights, long inputs, K a multiple of its 32-column stage).
+static inline bool mx_dense_on_gemm(int wdt, int T, int K) {
+  return wdt == MX_DT_F16 && T >= MX_DENSE_GEMM_MIN_TOKENS && K % 32 == 0;
+}
+// y[T, N] = a[T, K] W^T with W = projection `ent` (wmat, its weights, for mx_gemm_f16).
 int mx_project(const MxDenseWork& w, int ent, int wdt, const void* wmat, int T, int N, int K,
                const void* a, float* y, hipStream_t s);

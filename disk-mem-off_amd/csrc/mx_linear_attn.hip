@@ -3,9 +3,10 @@
 //   -> gated output norm -> out projection -> residual,
 // i.e. Qwen3NextExecutor._linear_attn_block (offload_runtime/executors/qwen3_next.py:207-269)
 // with _softplus (:27-28), _causal_conv1d (:35-53) and _gated_delta_rule_recurrence
-// (:56-95).  The three projections run on the grouped-GEMM kernels of the MoE experts as
-// single-group products (HBM-bound decode kernel for short inputs, LDS-staged MFMA kernel
-// for long ones).  Everything runs on the caller's stream out of the caller's workspace.
+// (:56-95).  The projections of short inputs (and int8 / fp32 weights) run on the grouped
+// kernels of the MoE experts as single-group products (HBM-bound weight streaming); long
+// inputs with fp16 weights run on the dense MFMA GEMM, qkvz and ba in one launch.
+// Everything runs on the caller's stream out of the caller's workspace.
 #include <math.h>
 
 #include "mx_common.h"
@@ -651,8 +652,13 @@ int run_stage(int st, const MxLinearAttnDesc* d, const MxLinearAttnWeights* w, c
                                s);
     }
     case 1:
+      if (mx_dense_on_gemm(wdt, T, m.H)) {  // qkvz and ba share h: one GEMM launch
+        const MxGemmSeg g[2] = {{w->qkvz_w, k.v.qkvz, m.W1, m.W1}, {w->ba_w, k.v.ba, m.W2, m.W2}};
+        return mx_gemm_f16(h, T, m.H, g, 2, s);
+      }
       return mx_project(k.dw, 0, wdt, w->qkvz_w, T, m.W1, m.H, h, k.v.qkvz, s);
     case 2:
+      if (mx_dense_on_gemm(wdt, T, m.H)) return MX_OK;  // with qkvz in stage 1
       return mx_project(k.dw, 1, wdt, w->ba_w, T, m.W2, m.H, h, k.v.ba, s);
     case 3: {
       const dim3 grid(mx_ceil_div(m.C + m.n, 256), mx_ceil_div(T, LA_TT));

@@ -35,8 +35,8 @@ HIP_FLAGS = [
 ]
 
 
-# hipBLASLt: the plain dense GEMMs of long linear-attention inputs.
-LINK_LIBS = ["-lhipblaslt"]
+# No vendor libraries: every kernel is this package's own.
+LINK_LIBS: list[str] = []
 
 
 def _hipcc() -> str:

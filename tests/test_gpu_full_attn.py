@@ -109,7 +109,37 @@ def test_block_intermediates_match_oracle(mi355x, stream, hd, nh, nkv, wdt, T):
     assert np.max(np.abs(out - ref["out"])) <= (1e-4 if exact else 2e-2)
 
 
-@pytest.mark.parametrize("T", [1, 100, 1024])
+def test_long_input_odd_hidden_on_the_dense_gemm(mi355x, stream):
+    """Long fp16 inputs run q, k and v as one dense MFMA GEMM launch (three weight
+    segments) and o alone: a hidden size of 224 (seven 32-column stages, a partial column
+    block of the o projection) and a token count that is not a multiple of the row tile;
+    hidden 200 (not a whole number of stages) takes the grouped kernels instead."""
+    for hidden in (224, 200):
+        _long_input_case(mi355x, stream, hidden)
+
+
+def _long_input_case(mi355x, stream, hidden):
+    s = syn.FullAttnShape(hidden, 8, 2, 64, 0.25, 5000000.0, 1e-6)
+    T = 333
+    say(f"[gpu] full attention fp16, hidden {hidden}, T={T}")
+    t = syn.make_full_attn_tensors(s, 79, weight_dtype=np.float16, norm_noise=0.1)
+    x = syn.make_inputs(80, T, s.hidden)
+    out, vw = _block(mi355x, stream, s, t, x, True)
+    ref = fa.full_attn_block(x, t, spec_of(s))
+    od = s.n_heads * s.head_dim
+    e = normwise_err(vw["qg"][:, od:], ref["qg"][:, od:])
+    say(f"    gate normwise err {e:.2e}")
+    assert e <= 5e-3
+    v = ref["v"].transpose(1, 0, 2).reshape(T, s.n_kv_heads * s.head_dim)
+    e = normwise_err(vw["v"], v)
+    say(f"    v normwise err {e:.2e}")
+    assert e <= 5e-3
+    err = normwise_err(out, ref["out"])
+    say(f"    block normwise err {err:.2e}")
+    assert err <= 5e-3 and np.max(np.abs(out - ref["out"])) <= 2e-2
+
+
+@pytest.mark.parametrize("T", [1, 100, 1024, 4096])
 def test_qwen3_next_size_block(mi355x, stream, T):
     s = syn.QWEN3_NEXT_FULL
     say(f"[gpu] Qwen3-Next-size full attention fp16 T={T}")

@@ -154,7 +154,34 @@ def test_block_intermediates_match_oracle(mi355x, stream, wdt, T):
     assert np.max(np.abs(out - ref["out"])) <= (1e-4 if exact else 2e-2)
 
 
-@pytest.mark.parametrize("T", [1, 64, 512])
+def test_long_input_odd_hidden_on_the_dense_gemm(mi355x, stream):
+    """Long fp16 inputs run the projections on the dense MFMA GEMM (qkvz and ba in one
+    launch): a hidden size of 224 (seven 32-column stages, and a partial column block of the
+    out projection), a token count that is not a multiple of the 128 / 256-row tile, and the
+    ba segment's partial column block; hidden 200 (not a whole number of 32-column stages)
+    takes the grouped kernels instead."""
+    for hidden in (224, 200):
+        _long_input_case(mi355x, stream, hidden)
+
+
+def _long_input_case(mi355x, stream, hidden):
+    shape = syn.LinearAttnShape(hidden, 4, 64, 32, 4, 1e-6)
+    T = 333
+    say(f"[gpu] linear attention fp16, hidden {hidden}, T={T}")
+    t = syn.make_linear_attn_tensors(shape, 77, weight_dtype=np.float16, param_dtype=np.float32,
+                                     norm_noise=0.1)
+    x = syn.make_inputs(78, T, shape.hidden)
+    out, views = _block(mi355x, stream, shape, t, x)
+    ref = la.linear_attn_block(x, t, spec_of(shape))
+    for k in ("qkvz", "ba"):
+        e = normwise_err(views[k], ref[k])
+        say(f"    {k} normwise err {e:.2e}")
+        assert e <= 3e-3, k
+    err = normwise_err(out, ref["out"])
+    assert err <= 5e-3 and np.max(np.abs(out - ref["out"])) <= 2e-2
+
+
+@pytest.mark.parametrize("T", [1, 64, 512, 4096])
 def test_qwen3_next_size_block(mi355x, stream, T):
     shape = syn.QWEN3_NEXT_LINEAR
     say(f"[gpu] Qwen3-Next-size linear attention fp16 T={T}")
