@@ -1,28 +1,42 @@
-// Dense fp16 GEMM on MFMA for the long-input projections of the attention blocks:
-//   y_s[M, N_s] (fp32, row stride ldy_s) = a[M, K] (fp16, row-major) . W_s[N_s, K]^T
-// for up to MX_GEMM_MAX_SEG weight matrices W_s (fp16, nn.Linear row-major) that share the
-// activations a (the q / k / v projections, or qkvz and ba, in one launch).
-// Reference: linear_t = x @ W.T (offload_runtime/executors/_common.py:101-103) at
-// qwen3_next.py:170-174, :211, :231, :245 and :268.
+// Dense GEMM on MFMA with an LDS-staged operand ring:
+//   y_s[M, N_s] (fp32, row stride ldy_s) = a[M, K] . W_s[N_s, K]^T
+// for up to MX_GEMM_MAX_SEG weight matrices W_s (nn.Linear row-major) that share the
+// activations a.  Two element types:
+//  * fp16 operands (v_mfma_f32_16x16x32_f16): the long-input projections of the attention
+//    blocks (the q / k / v projections, or qkvz and ba, in one launch).  Reference:
+//    linear_t = x @ W.T (offload_runtime/executors/_common.py:101-103) at
+//    qwen3_next.py:170-174, :211, :231, :245 and :268.
+//  * fp32 operands (v_mfma_f32_16x16x4_f32, full fp32 products), and
+//  * fp32 operands carried as two fp16 planes each (SPLIT): x = hi + 2^-11 lo with
+//    hi = fp16(x), lo = fp16((x - hi) * 2^11), and a . w = a_hi . w_hi + 2^-11 (a_hi . w_lo
+//    + a_lo . w_hi) up to the dropped 2^-22 a_lo . w_lo: three fp16 MFMAs per 32 columns
+//    (exact products, fp32 sums) in place of eight fp32 ones, at the same operand bytes;
+//  both for the router logits of long inputs, h @ Wr.T at glm4_moe.py:181 and
+//  qwen3_next.py:278 (with the shared-expert gate row, qwen3_next.py:328), the reduction
+//  split into slices over gridDim.y whose partial sums the top-k adds in slice order.
 //
-// Block tile BM x BN over one weight segment; the reduction runs in stages of 32 columns
-// (one MFMA k-step).  Both operands of a stage are copied from global memory straight into
-// LDS by the buffer loads' LDS mode (no register staging), into a ring of NS stage slots:
-// while the waves compute stage s, the copies of stages s + 1 .. s + NS - 1 are in flight.
-// Each copy instruction moves one 16-row x 32-column fragment (1 KiB); the LDS mode stores
-// lane l's 16 bytes at 16 l, so the lane-to-(row, chunk) map of the copy fixes the layout
-// of the fragment in LDS (see below: coalesced rows, rotated chunks, no padding).
+// Block tile BM x BN over one weight segment and one reduction slice; the reduction runs in
+// stages of 64 bytes per row (32 fp16 or 16 fp32 columns).  Both operands of a stage are
+// copied from global memory straight into LDS by the buffer loads' LDS mode (no register
+// staging), into a ring of NS stage slots: while the waves compute stage s, the copies of
+// stages s + 1 .. s + NS - 1 are in flight.  Each copy instruction moves one fragment of 16
+// rows x 64 bytes (1 KiB); the LDS mode stores lane l's 16 bytes at 16 l, so the
+// lane-to-(row, chunk) map of the copy fixes the layout of the fragment in LDS (see below:
+// coalesced rows, rotated chunks, no padding).
 // A stage is waited for with an explicit vmcnt (the copies are this loop's only vector
 // memory operations) and a barrier without a memory fence: a fence on LDS would also wait
 // for every copy still in flight, which would empty the ring at every stage.
-// Each wave owns a WM x WN sub-tile (WM / 16 x WN / 16 accumulator tiles of
-// v_mfma_f32_16x16x32_f16), so every A fragment read from LDS feeds WN / 16 MFMAs and
-// every B fragment WM / 16.  Global reads go through buffer descriptors: rows past M or
-// past N_s read zero.  K must be a multiple of 32 (MX_ERR_UNSUPPORTED otherwise).
+// Each wave owns a WM x WN sub-tile (WM / 16 x WN / 16 accumulator tiles), so every A
+// fragment read from LDS feeds WN / 16 products and every B fragment WM / 16.  Global
+// reads go through buffer descriptors: rows past M or past N_s read zero.  K must be a
+// multiple of the stage width (MX_ERR_UNSUPPORTED otherwise).
 //
-// Fragment layout (lane = 16 q + j): an activation fragment lane holds a[m0 + j][k0 + 8 q ..
-// +8], a weight fragment lane W[n0 + j][k0 + 8 q .. +8]; with the weights as the MFMA's A
-// operand the accumulator lane holds y[m0 + j][n0 + 4 q + r], r = 0..3.
+// Fragment layout (lane = 16 q + j): an activation fragment lane holds the 16 bytes of
+// a[m0 + j] at byte 16 q of the stage, a weight fragment lane those of W[n0 + j]; fp16
+// feeds them to one 16x16x32 MFMA (k = 8 q .. 8 q + 7), fp32 to four 16x16x4 MFMAs (the
+// e-th takes element e of both, so the four cover the stage's 16 columns once each).  With
+// the weights as the MFMA's A operand the accumulator lane holds y[m0 + j][n0 + 4 q + r],
+// r = 0..3.
 #include "mx_common.h"
 #include "mx_internal.h"
 
@@ -37,25 +51,30 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
 }
 
 struct GemmSeg {
-  const half_t* w;  // [N, K]
-  float* y;         // [M, ldy]
-  int n;            // N of the segment
+  const void* w;  // [N, K]
+  const void* w_lo;  // SPLIT: the low plane of w
+  float* y;       // [M, ldy] for slice 0; slice z at y + z * yslice
+  int n;          // N of the segment
   int ldy;
-  int nblk;         // column blocks of the segment
+  int nblk;       // column blocks of the segment
 };
 
 struct GemmArgs {
-  const half_t* a;  // [M, K]
+  const void* a;  // [M, K]
+  const void* a_lo;  // SPLIT: the low plane of a
   int M, K;
-  int mblk;         // row blocks
+  int kslice;     // reduction columns per slice (gridDim.y slices)
+  long yslice;    // elements between the outputs of consecutive slices
+  int mblk;       // row blocks
   int nseg;
   GemmSeg seg[MX_GEMM_MAX_SEG];
 };
 
-constexpr int BK = 32;  // reduction columns per stage (one MFMA k-step)
+constexpr int STAGE_BYTES = 64;  // bytes of each row per stage (16 B per lane quarter)
 #ifndef MX_GEMM_NS
 #define MX_GEMM_NS 4  // stage slots in the LDS ring
 #endif
+
 
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -79,16 +98,20 @@ __device__ __forceinline__ void wait_copies_and_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-template <int BM, int BN, int WM, int WN, int NS, int OCC>
-__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, OCC) void k_gemm_f16_nt(
+template <typename ET, bool SPLIT, int BM, int BN, int WM, int WN, int NS, int OCC>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, OCC) void k_gemm_nt(
     const GemmArgs p) {
+  constexpr int ES = sizeof(ET);
+  constexpr int BKE = STAGE_BYTES / ES;           // reduction columns per stage
   constexpr int NWN = BN / WN, NW = (BM / WM) * NWN;
   constexpr int MF = WM / 16, NF = WN / 16;
-  constexpr int FA = BM / 16, FT = FA + BN / 16;  // fragments per stage slot
+  constexpr int PL = SPLIT ? 2 : 1;               // planes per operand
+  constexpr int FA1 = BM / 16, FB1 = BN / 16;     // fragments per plane and stage
+  constexpr int FA = PL * FA1, FT = FA + PL * FB1;  // fragments per stage slot: A planes, B planes
   constexpr int SLOT = FT * 1024;
   constexpr int DPW = FT / NW;                    // copies per wave and stage
-  constexpr int DPA = FA / NW;                    // of which A fragments
-  static_assert(FT % NW == 0 && FA % NW == 0, "fragments must divide among the waves");
+  static_assert(!SPLIT || ES == 2, "split planes are fp16");
+  static_assert(FA1 % NW == 0 && FB1 % NW == 0, "fragments must divide among the waves");
   __shared__ __align__(1024) char lds[NS * SLOT];
 
   // Blocks are numbered so that consecutive logical ids run on one XCD (hardware block b
@@ -109,14 +132,28 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, OCC) void k_gemm_f16_nt
   const GemmSeg sg = p.seg[si];
   const int m0 = mb * BM, n0 = rem * BN;
   const int M = p.M, K = p.K, N = sg.n;
+  const int k0 = blockIdx.y * p.kslice;            // this block's reduction slice
+  const int kn = min(p.kslice, K - k0);
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / NWN, wn = wave % NWN;
   const int j = lane & 15, q = lane >> 4;
 
-  const rsrc_t ra = make_rsrc(p.a, (uint32_t)((size_t)M * K * 2));
-  const rsrc_t rb = make_rsrc(sg.w, (uint32_t)((size_t)N * K * 2));
+  const rsrc_t ra = make_rsrc(p.a, (uint32_t)((size_t)M * K * ES));
+  const rsrc_t rb = make_rsrc(sg.w, (uint32_t)((size_t)N * K * ES));
+  const rsrc_t ral = SPLIT ? make_rsrc(p.a_lo, (uint32_t)((size_t)M * K * ES)) : ra;
+  const rsrc_t rbl = SPLIT ? make_rsrc(sg.w_lo, (uint32_t)((size_t)N * K * ES)) : rb;
+  // Fragment f of a slot: A planes [0, FA) (plane f / FA1), then B planes (plane
+  // (f - FA) / FB1).  The copy i of every wave lies in one plane (each plane's fragment
+  // count is a multiple of NW), so its descriptor is uniform.
+  auto rsrc_of = [&](int i) {
+    const int f0 = i * NW;
+    if (f0 < FA1) return ra;
+    if (f0 < FA) return ral;
+    if (f0 < FA + FB1) return rb;
+    return rbl;
+  };
   // The fragments this wave copies: f = wave + i * NW (A fragments first, then B); the
   // lane's source row and its byte offset at stage 0.
   // Copy lane l loads row cr = l / 4 of its fragment, 16-byte chunk cq = (l % 4 - cr / 4)
@@ -130,35 +167,43 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, OCC) void k_gemm_f16_nt
 #pragma unroll
   for (int i = 0; i < DPW; ++i) {
     const int f = wave + i * NW;
-    if (i < DPA) {
-      const int row = m0 + 16 * f + cr;
-      goff[i] = row < M ? (uint32_t)row * (uint32_t)K * 2 + cq * 16 : kOob;
+    if (i * NW < FA) {
+      const int row = m0 + 16 * (f % FA1) + cr;
+      goff[i] = row < M ? ((uint32_t)row * (uint32_t)K + k0) * ES + cq * 16 : kOob;
     } else {
-      const int row = n0 + 16 * (f - FA) + cr;
-      goff[i] = row < N ? (uint32_t)row * (uint32_t)K * 2 + cq * 16 : kOob;
+      const int row = n0 + 16 * ((f - FA) % FB1) + cr;
+      goff[i] = row < N ? ((uint32_t)row * (uint32_t)K + k0) * ES + cq * 16 : kOob;
     }
   }
-  // K is a multiple of BK, so every piece of a stage lies inside its row; rows past M / N
-  // have offsets at or above kOob, which stay past the end of the descriptor.
+  // K and the slice length are multiples of BKE, so every piece of a stage lies inside its
+  // row; rows past M / N have offsets at or above kOob, which stay past the end of the
+  // descriptor.
   auto issue = [&](int st) {
     char* slot = lds + (st % NS) * SLOT;
 #pragma unroll
     for (int i = 0; i < DPW; ++i) {
       const int f = wave + i * NW;
-      copy_to_lds16(i < DPA ? ra : rb, slot + f * 1024, goff[i] + (uint32_t)st * (BK * 2));
+      copy_to_lds16(rsrc_of(i), slot + f * 1024, goff[i] + (uint32_t)st * STAGE_BYTES);
     }
   };
 
   // acc[mi][ni] holds the transposed product (the weights are the MFMA's A operand):
   // lane (j, q) has y[m0 + 16 mi + j][n0 + 16 ni + 4 q + r], r = 0..3, so the epilogue
   // stores 4 consecutive columns per lane.
-  float4_t acc[MF][NF];
+  // SPLIT: acc2 sums the two cross terms a_hi . w_lo + a_lo . w_hi.
+  float4_t acc[MF][NF], acc2[SPLIT ? MF : 1][SPLIT ? NF : 1];
 #pragma unroll
   for (int mi = 0; mi < MF; ++mi)
 #pragma unroll
     for (int ni = 0; ni < NF; ++ni) acc[mi][ni] = (float4_t){0.f, 0.f, 0.f, 0.f};
+  if constexpr (SPLIT) {
+#pragma unroll
+    for (int mi = 0; mi < MF; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < NF; ++ni) acc2[mi][ni] = (float4_t){0.f, 0.f, 0.f, 0.f};
+  }
 
-  const int nst = (K + BK - 1) / BK;
+  const int nst = kn / BKE;
 #pragma unroll
   for (int s0 = 0; s0 < NS - 1; ++s0)
     if (s0 < nst) issue(s0);
@@ -178,24 +223,65 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, OCC) void k_gemm_f16_nt
 #pragma unroll
     for (int ni = 0; ni < NF; ++ni)
       bf[ni] = *(const int4_t*)(slot + (FA + wn * NF + ni) * 1024 + rpos);
+    if constexpr (SPLIT) {
+      int4_t afl[MF], bfl[NF];
+#pragma unroll
+      for (int mi = 0; mi < MF; ++mi)
+        afl[mi] = *(const int4_t*)(slot + (FA1 + wm * MF + mi) * 1024 + rpos);
+#pragma unroll
+      for (int ni = 0; ni < NF; ++ni)
+        bfl[ni] = *(const int4_t*)(slot + (FA + FB1 + wn * NF + ni) * 1024 + rpos);
+#pragma unroll
+      for (int mi = 0; mi < MF; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < NF; ++ni) {
+          const half8_t ah = __builtin_bit_cast(half8_t, af[mi]);
+          const half8_t bh = __builtin_bit_cast(half8_t, bf[ni]);
+          acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bh, ah, acc[mi][ni], 0, 0, 0);
+          acc2[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              __builtin_bit_cast(half8_t, bfl[ni]), ah, acc2[mi][ni], 0, 0, 0);
+          acc2[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              bh, __builtin_bit_cast(half8_t, afl[mi]), acc2[mi][ni], 0, 0, 0);
+        }
+      continue;
+    }
+#pragma unroll
+    for (int mi = 0; mi < MF; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < NF; ++ni) {
+        if constexpr (ES == 2) {
+          acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              __builtin_bit_cast(half8_t, bf[ni]), __builtin_bit_cast(half8_t, af[mi]),
+              acc[mi][ni], 0, 0, 0);
+        } else {
+          const float4_t av = __builtin_bit_cast(float4_t, af[mi]);
+          const float4_t bv = __builtin_bit_cast(float4_t, bf[ni]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[e], av[e], acc[mi][ni], 0, 0, 0);
+        }
+      }
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // no copy into LDS outlives the block (vmcnt 0)
+  if constexpr (SPLIT) {
 #pragma unroll
     for (int mi = 0; mi < MF; ++mi)
 #pragma unroll
       for (int ni = 0; ni < NF; ++ni)
-        acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-            __builtin_bit_cast(half8_t, bf[ni]), __builtin_bit_cast(half8_t, af[mi]),
-            acc[mi][ni], 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          acc[mi][ni][r] = fmaf(acc2[mi][ni][r], 1.f / 2048.f, acc[mi][ni][r]);
   }
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // no copy into LDS outlives the block (vmcnt 0)
 
   // Epilogue: fp32 rows of the segment's output, 4 consecutive columns per lane (a
   // 16-byte store when the row stride and the base allow it).
-  const bool vec = (sg.ldy & 3) == 0 && ((uintptr_t)sg.y & 15) == 0;
+  float* const ybase = sg.y + (size_t)blockIdx.y * p.yslice;
+  const bool vec = (sg.ldy & 3) == 0 && ((uintptr_t)ybase & 15) == 0;
 #pragma unroll
   for (int mi = 0; mi < MF; ++mi) {
     const int m = m0 + wm * WM + mi * 16 + j;
     if (m >= M) continue;
-    float* yrow = sg.y + (size_t)m * sg.ldy;
+    float* yrow = ybase + (size_t)m * sg.ldy;
 #pragma unroll
     for (int ni = 0; ni < NF; ++ni) {
       const int n = n0 + wn * WN + ni * 16 + 4 * q;
@@ -210,50 +296,89 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, OCC) void k_gemm_f16_nt
   }
 }
 
-template <int BM, int BN, int WM, int WN, int NS, int OCC>
-int launch(GemmArgs& args, const MxGemmSeg* segs, int nseg, hipStream_t s) {
+template <typename ET, bool SPLIT, int BM, int BN, int WM, int WN, int NS, int OCC>
+int launch(GemmArgs& args, const MxGemmSeg* segs, int nseg, int splits, hipStream_t s) {
   args.mblk = mx_ceil_div(args.M, BM);
   long blocks = 0;
   for (int i = 0; i < nseg; ++i) {
     args.seg[i].nblk = mx_ceil_div(segs[i].n, BN);
     blocks += (long)args.seg[i].nblk * args.mblk;
   }
-  if (blocks <= 0 || blocks > (1l << 31) - 1) return MX_ERR_UNSUPPORTED;
+  if (blocks <= 0 || blocks > (1l << 31) - 1 || splits < 1 || splits > 65535)
+    return MX_ERR_UNSUPPORTED;
   constexpr int threads = (BM / WM) * (BN / WN) * 64;
   mx_clear_error();
-  hipLaunchKernelGGL((k_gemm_f16_nt<BM, BN, WM, WN, NS, OCC>), dim3((unsigned)blocks), dim3(threads), 0,
-                     s, args);
+  hipLaunchKernelGGL((k_gemm_nt<ET, SPLIT, BM, BN, WM, WN, NS, OCC>), dim3((unsigned)blocks, splits),
+                     dim3(threads), 0, s, args);
   return mx_launch_status();
+}
+
+// Shared argument checks; fills args (segments, K, slices) for element size es.
+int prepare(GemmArgs& args, const void* a, int M, int K, int es, const MxGemmSeg* segs,
+            int nseg, int kslice, long yslice) {
+  if (!a || !segs || nseg < 1 || nseg > MX_GEMM_MAX_SEG || M <= 0 || K <= 0 || kslice <= 0)
+    return MX_ERR_INVALID;
+  const int bke = STAGE_BYTES / es;
+  if (K % bke || kslice % bke) return MX_ERR_UNSUPPORTED;  // whole stages only
+  if (!mx_aligned16(a)) return MX_ERR_ALIGNMENT;
+  if ((long)M * K * es >= (1l << 31)) return MX_ERR_UNSUPPORTED;
+  args = GemmArgs{};
+  args.a = a;
+  args.M = M;
+  args.K = K;
+  args.kslice = kslice;
+  args.yslice = yslice;
+  args.nseg = nseg;
+  for (int i = 0; i < nseg; ++i) {
+    const MxGemmSeg& g = segs[i];
+    if (!g.w || !g.y || g.n <= 0 || g.ldy < g.n) return MX_ERR_INVALID;
+    if (!mx_aligned16(g.w)) return MX_ERR_ALIGNMENT;
+    if ((long)g.n * K * es >= (1l << 31)) return MX_ERR_UNSUPPORTED;
+    args.seg[i].w = g.w;
+    args.seg[i].w_lo = g.w_lo;
+    args.seg[i].y = g.y;
+    args.seg[i].n = g.n;
+    args.seg[i].ldy = g.ldy;
+  }
+  return MX_OK;
 }
 
 }  // namespace
 
 int mx_gemm_f16(const void* a, int M, int K, const MxGemmSeg* segs, int nseg, hipStream_t s) {
-  if (!a || !segs || nseg < 1 || nseg > MX_GEMM_MAX_SEG || M <= 0 || K <= 0)
-    return MX_ERR_INVALID;
-  if (K % BK) return MX_ERR_UNSUPPORTED;  // whole stages of 32 columns
-  if (!mx_aligned16(a)) return MX_ERR_ALIGNMENT;
-  if ((long)M * K * 2 >= (1l << 31)) return MX_ERR_UNSUPPORTED;
-  GemmArgs args{};
-  args.a = (const half_t*)a;
-  args.M = M;
-  args.K = K;
-  args.nseg = nseg;
+  GemmArgs args;
+  MX_TRY(prepare(args, a, M, K, 2, segs, nseg, K, 0));
   long cols = 0;
-  for (int i = 0; i < nseg; ++i) {
-    const MxGemmSeg& g = segs[i];
-    if (!g.w || !g.y || g.n <= 0 || g.ldy < g.n) return MX_ERR_INVALID;
-    if (!mx_aligned16(g.w)) return MX_ERR_ALIGNMENT;
-    if ((long)g.n * K * 2 >= (1l << 31)) return MX_ERR_UNSUPPORTED;
-    args.seg[i].w = (const half_t*)g.w;
-    args.seg[i].y = g.y;
-    args.seg[i].n = g.n;
-    args.seg[i].ldy = g.ldy;
-    cols += g.n;
-  }
+  for (int i = 0; i < nseg; ++i) cols += segs[i].n;
   // 256 x 256 tiles while they give at least two rounds of blocks on 256 CUs; 128 x 128
   // (four waves, two blocks per CU) otherwise.
   const long big = (long)mx_ceil_div(M, 256) * mx_ceil_div((int)cols, 256);
-  if (big >= 512) return launch<256, 256, 128, 64, MX_GEMM_NS, 1>(args, segs, nseg, s);
-  return launch<128, 128, 64, 64, MX_GEMM_NS, 2>(args, segs, nseg, s);
+  if (big >= 512)
+    return launch<half_t, false, 256, 256, 128, 64, MX_GEMM_NS, 1>(args, segs, nseg, 1, s);
+  return launch<half_t, false, 128, 128, 64, 64, MX_GEMM_NS, 2>(args, segs, nseg, 1, s);
+}
+
+int mx_gemm_f32_slices(const float* a, int M, int K, const MxGemmSeg* segs, int nseg,
+                       int kslice, long yslice, hipStream_t s) {
+  GemmArgs args;
+  MX_TRY(prepare(args, a, M, K, 4, segs, nseg, kslice, yslice));
+  const int splits = mx_ceil_div(K, kslice);
+  if (splits > 1 && yslice <= 0) return MX_ERR_INVALID;
+  return launch<float, false, 128, 128, 64, 64, MX_GEMM_NS, 2>(args, segs, nseg, splits, s);
+}
+
+int mx_gemm_f16x2_slices(const void* a_hi, const void* a_lo, int M, int K, const MxGemmSeg* segs,
+                         int nseg, int kslice, long yslice, hipStream_t s) {
+  GemmArgs args;
+  MX_TRY(prepare(args, a_hi, M, K, 2, segs, nseg, kslice, yslice));
+  if (!a_lo || !mx_aligned16(a_lo)) return a_lo ? MX_ERR_ALIGNMENT : MX_ERR_INVALID;
+  for (int i = 0; i < nseg; ++i) {
+    if (!segs[i].w_lo) return MX_ERR_INVALID;
+    if (!mx_aligned16(segs[i].w_lo)) return MX_ERR_ALIGNMENT;
+  }
+  args.a_lo = a_lo;
+  const int splits = mx_ceil_div(K, kslice);
+  if (splits > 1 && yslice <= 0) return MX_ERR_INVALID;
+  // 256 x 128 tiles of 8 waves, one block per CU (three 48 KiB stage slots).
+  return launch<half_t, true, MX_GEMM_SPLIT_BM, 128, 64, 64, 3, 1>(args, segs, nseg, splits, s);
 }

@@ -5,8 +5,21 @@
 
 #include "moe_mi355x.h"
 
-// Number of H-slices the router logit kernel uses for this shape.
-int mx_router_splits_for(int tokens, int hidden, int e1);
+// Number of H-slices the router logit launch uses for this shape (weight_dtype of the MoE
+// block, or -1 for the stand-alone mx_router_logits).
+int mx_router_splits_for(int tokens, int hidden, int n_experts, int has_shared_gate,
+                         int param_dtype, int weight_dtype);
+// Whether the MoE block's router runs on the split-plane GEMM (its RMSNorm then also
+// writes the low plane of h16, and its workspace holds the router rows' planes).
+bool mx_router_on_split(int tokens, int hidden, int e1, int weight_dtype);
+size_t mx_router_split_bytes(int hidden, int e1);
+// Router logit partials from the planes h16 / h16lo (RMSNorm outputs) and the router rows
+// split into `wsplit` (mx_router_split_bytes) by this call.
+int mx_router_logits_split(const void* h16, const void* h16lo, const void* router_w,
+                           const void* shared_gate_w, int param_dtype, int tokens, int hidden,
+                           int n_experts, int splits, void* wsplit, float* logits, hipStream_t s);
+// Rows per block of mx_gemm_f16x2_slices.
+#define MX_GEMM_SPLIT_BM 256
 
 // Upper bound of the m-tile list for `tokens` tokens at m_blk rows per tile.
 int mx_max_mtiles(int tokens, int top_k, int n_experts, int has_shared, int m_blk);
@@ -16,7 +29,7 @@ int mx_m_blk_for(int tokens, int weight_dtype);
 
 // RMSNorm launch (vectorised when the row fits the register tile).
 int mx_rmsnorm_launch(const float* x, const void* norm_w, int param_dtype, float eps, int tokens,
-                      int hidden, float* h32, void* h16, hipStream_t s);
+                      int hidden, float* h32, void* h16, hipStream_t s, void* h16lo = nullptr);
 
 // Decode router (T <= 64): RMSNorm + logits kernel, then a single-workgroup
 // top-k/dispatch kernel.  mx_router_decode_ok tells whether the shape and the pointer
@@ -81,16 +94,27 @@ struct MxDenseTables {
 int mx_dense_linear(int wdt, int tiled, const MxExpertPtrs* entry, const MxDenseTables& tab,
                     int T, int N, int K, const void* a, float* y, hipStream_t s);
 
-// Dense fp16 GEMM on MFMA (mx_dense_gemm.hip): y_s[M, N_s] (fp32, row stride ldy_s) =
-// a[M, K] (fp16) W_s[N_s, K]^T for up to MX_GEMM_MAX_SEG fp16 weight matrices sharing a.
+// Dense GEMM on MFMA (mx_dense_gemm.hip): y_s[M, N_s] (fp32, row stride ldy_s) =
+// a[M, K] W_s[N_s, K]^T for up to MX_GEMM_MAX_SEG weight matrices sharing a.
 #define MX_GEMM_MAX_SEG 3
 struct MxGemmSeg {
-  const void* w;  // [n, K] fp16, row-major (16-byte aligned)
+  const void* w;  // [n, K] row-major (16-byte aligned), element type of a
   float* y;       // [M, ldy] fp32
   int n;
   int ldy;
+  const void* w_lo = nullptr;  // mx_gemm_f16x2_slices: the low fp16 plane of w
 };
+// fp16 a and W.
 int mx_gemm_f16(const void* a, int M, int K, const MxGemmSeg* segs, int nseg, hipStream_t s);
+// fp32 a and W, full fp32 products; the reduction is cut into slices of kslice columns
+// (a multiple of 16) and slice z writes its partial sums at y_s + z * yslice.
+int mx_gemm_f32_slices(const float* a, int M, int K, const MxGemmSeg* segs, int nseg,
+                       int kslice, long yslice, hipStream_t s);
+// fp32 operands as two fp16 planes each, x = hi + 2^-11 lo (hi = fp16(x), lo = fp16((x -
+// hi) 2^11)): y = a_hi w_hi + 2^-11 (a_hi w_lo + a_lo w_hi), fp32 sums; kslice a multiple
+// of 32, slices as mx_gemm_f32_slices.
+int mx_gemm_f16x2_slices(const void* a_hi, const void* a_lo, int M, int K, const MxGemmSeg* segs,
+                         int nseg, int kslice, long yslice, hipStream_t s);
 
 // Workspace pieces of the dense projections of an attention block (device pointers):
 // expert-table entries (one per projection), single-group m-tile tables and ones[T] for

@@ -53,15 +53,25 @@ bool use_decode_router(const MxMoeDesc* d, const MxMoeWeights* w, int T, const f
   return mx_router_decode_ok(d, w, T, x);
 }
 
+// Workspace pieces outside the views: the dispatch scratch and, for the split-plane router,
+// the low fp16 plane of h and the router rows' planes.
+struct Internal {
+  void* dscratch = nullptr;
+  void* h16lo = nullptr;
+  void* wsplit = nullptr;
+};
+
 int layout(const MxMoeDesc* d, int T, void* ws, MxMoeViews* v, size_t* total,
-           void** dscratch = nullptr) {
+           Internal* in = nullptr) {
   MX_TRY(check_desc(d));
   if (T < 0) return MX_ERR_INVALID;
   const int Tn = T > 0 ? T : 1;
   const size_t H = d->hidden, E = d->n_experts, k = d->top_k;
   const int e1 = d->n_experts + (d->has_shared_gate ? 1 : 0);
   const int has_sh = d->shared_inter > 0;
-  const int S = mx_router_splits_for(Tn, d->hidden, e1);
+  const int S = mx_router_splits_for(Tn, d->hidden, d->n_experts, d->has_shared_gate,
+                                     d->param_dtype, d->weight_dtype);
+  const bool split = mx_router_on_split(Tn, d->hidden, e1, d->weight_dtype);
   const int m_blk = mx_m_blk_for(Tn, d->weight_dtype);
   const size_t P = (size_t)Tn * k;
   const size_t R = P + (has_sh ? Tn : 0);
@@ -95,7 +105,13 @@ int layout(const MxMoeDesc* d, int T, void* ws, MxMoeViews* v, size_t* total,
   size_t dscr = 0;
   MX_TRY(mx_dispatch_scratch_size(Tn, d->top_k, d->n_experts, &dscr));
   void* dispatch_scratch = c.take(dscr);
-  if (dscratch) *dscratch = dispatch_scratch;
+  void* h16lo = split ? c.take((size_t)Tn * H * 2) : nullptr;
+  void* wsplit = split ? c.take(mx_router_split_bytes(d->hidden, e1)) : nullptr;
+  if (in) {
+    in->dscratch = dispatch_scratch;
+    in->h16lo = h16lo;
+    in->wsplit = wsplit;
+  }
   if (v) *v = t;
   if (total) *total = mx_align_up(c.off, 256);
   return MX_OK;
@@ -113,7 +129,8 @@ bool select_in_gate_up(const MxMoeDesc* d, const MxMoeWeights* w, int T, const f
 }
 
 int run_stage(int stage, const MxMoeDesc* d, const MxMoeWeights* w, const float* x, float* out,
-              int T, const MxMoeViews& v, void* dscratch, hipStream_t s, bool sel1) {
+              int T, const MxMoeViews& v, const Internal& in, hipStream_t s, bool sel1) {
+  void* const dscratch = in.dscratch;
   const int has_sh = d->shared_inter > 0;
   const bool decode = use_decode_router(d, w, T, x);
   if (decode && (stage == 0 || stage == 2 || stage == 3)) return MX_OK;  // in stage 1
@@ -121,13 +138,18 @@ int run_stage(int stage, const MxMoeDesc* d, const MxMoeWeights* w, const float*
     case 0:
       if (!x || !w->norm_w) return MX_ERR_INVALID;
       return mx_rmsnorm_launch(x, w->norm_w, d->param_dtype, d->eps, T, d->hidden, v.h32, v.h16,
-                               s);
+                               s, in.h16lo);
     case 1:
       if (decode)
         return mx_router_decode_launch(d, w, T, x, v.h32, v.h16, v.logits, v.topk_ids, v.topk_w,
                                        v.shared_w, v.m_blk, v.counts, v.offsets, v.sorted_tok,
                                        v.sorted_w, v.pair_pos, v.g_expert, v.g_start, v.g_count,
                                        v.n_groups, v.mt_group, v.mt_row0, v.n_mtiles, s, sel1);
+      if (in.h16lo)
+        return mx_router_logits_split(v.h16, in.h16lo, w->router_w,
+                                      d->has_shared_gate ? w->shared_gate_w : nullptr,
+                                      d->param_dtype, T, d->hidden, d->n_experts, v.router_splits,
+                                      in.wsplit, v.logits, s);
       return mx_router_logits(v.h32, w->router_w, d->has_shared_gate ? w->shared_gate_w : nullptr,
                               d->param_dtype, T, d->hidden, d->n_experts, v.router_splits,
                               v.logits, s);
@@ -203,13 +225,13 @@ int forward(const MxMoeDesc* d, const MxMoeWeights* w, const float* x, float* ou
   if (T == 0) return MX_OK;
   MxMoeViews v;
   size_t need = 0;
-  void* dscratch = nullptr;
-  MX_TRY(layout(d, T, ws, &v, &need, &dscratch));
+  Internal in;
+  MX_TRY(layout(d, T, ws, &v, &need, &in));
   if (ws_bytes < need) return MX_ERR_WORKSPACE;
   const bool sel1 = select_in_gate_up(d, w, T, x, st_begin, st_end);
   for (int st = st_begin; st < st_end; ++st) {
     if (events) MX_TRY(mx_status(hipEventRecord((hipEvent_t)events[st], s)));
-    MX_TRY(run_stage(st, d, w, x, out, T, v, dscratch, s, sel1));
+    MX_TRY(run_stage(st, d, w, x, out, T, v, in, s, sel1));
   }
   if (events) MX_TRY(mx_status(hipEventRecord((hipEvent_t)events[MX_N_STAGES], s)));
   return MX_OK;

@@ -13,7 +13,9 @@
 // ------------------------------------------------------------------------------------
 // RMSNorm: one 256-thread block per token.  h = w * (x / sqrt(mean(x^2) + eps)).
 // VEC: each thread keeps its float4 slices of the row in registers (H <= 256 * 4 * RN_V),
-// so all loads of a row are in flight together.
+// so all loads of a row are in flight together.  Outputs: h32 (fp32), h16 = fp16(h) and,
+// for the split-plane router GEMM, h16lo = fp16((h - h16) * 2^11) (h - h16 is exact in
+// fp32, and so is the power-of-two scaling).
 // ------------------------------------------------------------------------------------
 #define RN_V 8
 
@@ -21,11 +23,13 @@ template <bool VEC>
 __global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x,
                                                  const void* __restrict__ w, int wdt,
                                                  float eps, int H, float* __restrict__ h32,
-                                                 half_t* __restrict__ h16) {
+                                                 half_t* __restrict__ h16,
+                                                 half_t* __restrict__ h16lo) {
   const int t = blockIdx.x;
   const float* xr = x + (size_t)t * H;
   float* hr = h32 + (size_t)t * H;
   half_t* hr16 = h16 ? h16 + (size_t)t * H : nullptr;
+  half_t* hrlo = h16lo ? h16lo + (size_t)t * H : nullptr;
   __shared__ float red[4];
   if constexpr (VEC) {
     float4 v[RN_V];
@@ -59,7 +63,13 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x,
         *(float4*)(hr + c) = o;
         if (hr16) {
           typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-          *(h4*)(hr16 + c) = (h4){(half_t)o.x, (half_t)o.y, (half_t)o.z, (half_t)o.w};
+          const h4 hi = (h4){(half_t)o.x, (half_t)o.y, (half_t)o.z, (half_t)o.w};
+          *(h4*)(hr16 + c) = hi;
+          if (hrlo)
+            *(h4*)(hrlo + c) = (h4){(half_t)((o.x - (float)hi[0]) * 2048.f),
+                                    (half_t)((o.y - (float)hi[1]) * 2048.f),
+                                    (half_t)((o.z - (float)hi[2]) * 2048.f),
+                                    (half_t)((o.w - (float)hi[3]) * 2048.f)};
         }
       }
     }
@@ -77,22 +87,28 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x,
     for (int i = threadIdx.x; i < H; i += 256) {
       float v = mx_load_param(w, wdt, i) * (xr[i] / rms);
       hr[i] = v;
-      if (hr16) hr16[i] = (half_t)v;
+      if (hr16) {
+        const half_t hi = (half_t)v;
+        hr16[i] = hi;
+        if (hrlo) hrlo[i] = (half_t)((v - (float)hi) * 2048.f);
+      }
     }
   }
 }
 
 int mx_rmsnorm_launch(const float* x, const void* norm_w, int param_dtype, float eps, int tokens,
-                      int hidden, float* h32, void* h16, hipStream_t s) {
+                      int hidden, float* h32, void* h16, hipStream_t s, void* h16lo) {
+  if (h16lo && !h16) return MX_ERR_INVALID;
   const bool vec = hidden % 4 == 0 && hidden <= 256 * 4 * RN_V && mx_aligned16(x) &&
-                   mx_aligned16(h32) && (!h16 || ((uintptr_t)h16 & 7u) == 0);
+                   mx_aligned16(h32) && (!h16 || ((uintptr_t)h16 & 7u) == 0) &&
+                   (!h16lo || ((uintptr_t)h16lo & 7u) == 0);
   mx_clear_error();
   if (vec)
     hipLaunchKernelGGL(k_rmsnorm<true>, dim3(tokens), dim3(256), 0, s, x, norm_w, param_dtype, eps,
-                       hidden, h32, (half_t*)h16);
+                       hidden, h32, (half_t*)h16, (half_t*)h16lo);
   else
     hipLaunchKernelGGL(k_rmsnorm<false>, dim3(tokens), dim3(256), 0, s, x, norm_w, param_dtype,
-                       eps, hidden, h32, (half_t*)h16);
+                       eps, hidden, h32, (half_t*)h16, (half_t*)h16lo);
   return mx_launch_status();
 }
 
@@ -243,16 +259,67 @@ k_router_logits(const float* __restrict__ h32, const WT* __restrict__ wr,
     }
 }
 
+// Router logits of long inputs run on the LDS-staged GEMM (mx_dense_gemm.hip), the
+// reduction cut into slices over gridDim.y:
+//  * RT_SPLIT: inside the MoE block, where h16 = fp16(h) exists: h and the router rows as
+//    two fp16 planes each (mx_gemm_f16x2_slices; the block's RMSNorm writes the low plane of
+//    h, mx_router_split_weights the planes of the router rows and the shared-expert gate
+//    row, one [E1, H] matrix); 256 x 128 tiles, one block per CU, slices of a multiple of
+//    32 columns.
+//  * RT_GEMM32: fp32 router rows otherwise (mx_gemm_f32_slices; the routed rows and the
+//    gate row as two weight segments); 128 x 128 tiles, two blocks per CU, slices of a
+//    multiple of 16 columns.
+// Other inputs run k_router_logits above (slices of RT_KCH columns).
+#ifndef RT_GEMM_MIN_TOKENS
+#define RT_GEMM_MIN_TOKENS 65
+#endif
+#ifndef RT_USE_SPLIT
+#define RT_USE_SPLIT 1
+#endif
+#ifndef RT_SPLIT_FILL
+#define RT_SPLIT_FILL 256  // blocks of one round of the split-plane GEMM (one per CU)
+#endif
+static bool router_on_gemm(int tokens, int hidden, int e1, int param_dtype) {
+  return param_dtype == MX_DT_F32 && tokens >= RT_GEMM_MIN_TOKENS && hidden % 16 == 0 &&
+         (long)tokens * hidden * 4 < (1l << 31) && (long)e1 * hidden * 4 < (1l << 31);
+}
+bool mx_router_on_split(int tokens, int hidden, int e1, int weight_dtype) {
+  return RT_USE_SPLIT && weight_dtype != MX_DT_F32 && tokens >= RT_GEMM_MIN_TOKENS &&
+         hidden % 32 == 0 && (long)tokens * hidden * 2 < (1l << 31) &&
+         (long)e1 * hidden * 2 < (1l << 31);
+}
+
 // Number of H-slices the router uses for T tokens (a pure function of the shape), at most
-// one slice per RT_KCH columns and at most 16.
-int mx_router_splits_for(int tokens, int hidden, int e1) {
-  const int tiles = mx_ceil_div(tokens > 0 ? tokens : 1, RT_BT) * mx_ceil_div(e1, RT_BE);
-  const int kch = mx_ceil_div(hidden, RT_KCH);
-  // Largest slice count whose blocks fit one round at 4 waves per SIMD (1024 blocks of 4
-  // waves on 256 CUs).  Qwen3-Next, 4096 tokens: 3 slices (816 blocks) against 4 (1088,
-  // a second round of 64 blocks): router + top-k 149 -> 145 us.
+// 16 and at most one per RT_KCH columns (k_router_logits), per 16 columns (RT_GEMM32) or
+// per 32 columns (RT_SPLIT; weight_dtype < 0: outside the MoE block, no split planes).
+int mx_router_splits_for(int tokens, int hidden, int n_experts, int has_shared_gate,
+                         int param_dtype, int weight_dtype) {
+  const int t = tokens > 0 ? tokens : 1;
+  const int e1 = n_experts + (has_shared_gate ? 1 : 0);
+  long tiles, fill;
+  int kch;
+  if (weight_dtype >= 0 && mx_router_on_split(t, hidden, e1, weight_dtype)) {
+    // Largest slice count whose blocks fit one round at one block per CU.  Qwen3-Next,
+    // 4096 tokens: 16 x 5 tiles x 3 slices; GLM-4.7, 2048 tokens: 8 x 2 x 16.
+    tiles = (long)mx_ceil_div(t, MX_GEMM_SPLIT_BM) * mx_ceil_div(e1, 128);
+    fill = RT_SPLIT_FILL;
+    kch = hidden / 32;
+  } else if (router_on_gemm(t, hidden, e1, param_dtype)) {
+    // Largest slice count whose blocks fit one round at two blocks per CU.  Qwen3-Next,
+    // 4096 tokens: 32 x (4 + 1) tiles x 3 slices; GLM-4.7, 2048 tokens: 16 x 2 x 16.
+    tiles = (long)mx_ceil_div(t, 128) *
+            (mx_ceil_div(n_experts, 128) + (has_shared_gate ? 1 : 0));
+    fill = 512;
+    kch = hidden / 16;
+  } else {
+    // Largest slice count whose blocks fit one round at 4 waves per SIMD (1024 blocks of 4
+    // waves on 256 CUs).
+    tiles = (long)mx_ceil_div(t, RT_BT) * mx_ceil_div(e1, RT_BE);
+    fill = 1024;
+    kch = mx_ceil_div(hidden, RT_KCH);
+  }
   int s = 1;
-  while (tiles * (s + 1) <= 1024 && s + 1 <= kch && s < 16) ++s;
+  while (tiles * (s + 1) <= fill && s + 1 <= kch && s < 16) ++s;
   const int per = mx_ceil_div(kch, s);
   return mx_ceil_div(kch, per);
 }
@@ -260,6 +327,46 @@ int mx_router_splits_for(int tokens, int hidden, int e1) {
 static int router_kslice(int hidden, int splits) {
   int kch = mx_ceil_div(hidden, RT_KCH);
   return mx_ceil_div(kch, splits) * RT_KCH;
+}
+
+// Router rows (and the shared-expert gate row as row E) as two fp16 planes [E1, H]:
+// hi = fp16(w), lo = fp16((w - hi) * 2^11).  fp16 rows are exact in hi (lo = 0).
+__global__ __launch_bounds__(256) void k_router_split_weights(const void* __restrict__ wr,
+                                                              const void* __restrict__ wsg,
+                                                              int pdt, int E, int H, long n,
+                                                              half_t* __restrict__ whi,
+                                                              half_t* __restrict__ wlo) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int e = (int)(i / H), k = (int)(i - (long)e * H);
+  const float v = e < E ? mx_load_param(wr, pdt, e * H + k) : mx_load_param(wsg, pdt, k);
+  const half_t hi = (half_t)v;
+  whi[i] = hi;
+  wlo[i] = (half_t)((v - (float)hi) * 2048.f);
+}
+
+size_t mx_router_split_bytes(int hidden, int e1) { return mx_align_up((size_t)e1 * hidden * 2, 256) * 2; }
+
+int mx_router_logits_split(const void* h16, const void* h16lo, const void* router_w,
+                           const void* shared_gate_w, int param_dtype, int tokens, int hidden,
+                           int n_experts, int splits, void* wsplit, float* logits, hipStream_t s) {
+  if (!h16 || !h16lo || !router_w || !wsplit || !logits || tokens <= 0 || hidden <= 0 ||
+      n_experts <= 0 || splits < 1)
+    return MX_ERR_INVALID;
+  const int e1 = n_experts + (shared_gate_w ? 1 : 0);
+  if (!mx_router_on_split(tokens, hidden, e1, MX_DT_F16)) return MX_ERR_UNSUPPORTED;
+  const int kslice = mx_ceil_div(hidden / 32, splits) * 32;
+  if (mx_ceil_div(hidden, kslice) != splits) return MX_ERR_INVALID;
+  half_t* whi = (half_t*)wsplit;
+  half_t* wlo = (half_t*)((char*)wsplit + mx_align_up((size_t)e1 * hidden * 2, 256));
+  const long n = (long)e1 * hidden;
+  mx_clear_error();
+  hipLaunchKernelGGL(k_router_split_weights, dim3((unsigned)mx_ceil_div(n, 256)), dim3(256), 0, s,
+                     router_w, shared_gate_w, param_dtype, n_experts, hidden, n, whi, wlo);
+  MX_TRY(mx_launch_status());
+  MxGemmSeg g{whi, logits, e1, e1};
+  g.w_lo = wlo;
+  return mx_gemm_f16x2_slices(h16, h16lo, tokens, hidden, &g, 1, kslice, (long)tokens * e1, s);
 }
 
 extern "C" int mx_router_logits(const float* h32, const void* router_w, const void* shared_gate_w,
@@ -276,12 +383,20 @@ extern "C" int mx_router_logits(const float* h32, const void* router_w, const vo
       ((uintptr_t)h32 & 15u))
     return MX_ERR_ALIGNMENT;
   if (tokens == 0) return MX_OK;
+  const int e1 = n_experts + (shared_gate_w ? 1 : 0);
+  hipStream_t s = (hipStream_t)stream;
+  if (router_on_gemm(tokens, hidden, e1, param_dtype)) {
+    const int kslice = mx_ceil_div(hidden / 16, splits) * 16;
+    if (mx_ceil_div(hidden, kslice) != splits) return MX_ERR_INVALID;
+    const MxGemmSeg g[2] = {{router_w, logits, n_experts, e1},
+                            {shared_gate_w, logits + n_experts, 1, e1}};
+    return mx_gemm_f32_slices(h32, tokens, hidden, g, shared_gate_w ? 2 : 1, kslice,
+                              (long)tokens * e1, s);
+  }
   const int kslice = router_kslice(hidden, splits);
   if (mx_ceil_div(hidden, kslice) != splits) return MX_ERR_INVALID;
-  const int e1 = n_experts + (shared_gate_w ? 1 : 0);
   dim3 grid(mx_ceil_div(tokens, RT_BT), mx_ceil_div(e1, RT_BE), splits);
   mx_clear_error();
-  hipStream_t s = (hipStream_t)stream;
   if (param_dtype == MX_DT_F16)
     hipLaunchKernelGGL(k_router_logits<half_t>, grid, dim3(256), 0, s, h32,
                        (const half_t*)router_w, (const half_t*)shared_gate_w, (int)tokens,
