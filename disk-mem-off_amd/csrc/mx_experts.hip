@@ -446,15 +446,22 @@ __global__ __launch_bounds__(256) void k_expert(const ExpertParams p, const Sele
 #ifndef MX_LDS_RB
 #define MX_LDS_RB 4
 #endif
-// Nontemporal hint on the prefill kernel's weight loads, per projection; both off.  The
-// sibling m-tiles of hot experts share weight lines through L2 (GLM-4.7 Zipf prefill with
-// nt: gate/up 1.109 -> 1.361 ms, down 671 -> 690 us); single-tile experts gain a little
-// from it (Qwen3-Next 4096 tokens: gate/up 497 -> 480 us, down 340 -> 333 us).
+// Nontemporal hint on the prefill kernel's weight loads of multi-tile groups, per
+// projection; both off.  The sibling m-tiles of hot experts share weight lines through L2
+// (GLM-4.7 Zipf prefill with nt for every block: gate/up 1.117 -> 1.336 ms).
 #ifndef MX_LDS_NT_GU
 #define MX_LDS_NT_GU 0
 #endif
 #ifndef MX_LDS_NT_DN
 #define MX_LDS_NT_DN 0
+#endif
+// Nontemporal weight loads for the blocks of single-tile groups (no sibling tile reads
+// their weights): a uniform branch per block between two copies of the tile body, no
+// spills (250-252 VGPRs).  Same box, interleaved: Qwen3-Next 4096 tokens gate/up 497 ->
+// 479 us, down 341 -> 335 us; GLM-4.7 2048-token Zipf prefill gate/up 1117 -> 1085 us,
+// down 684 -> 639 us.
+#ifndef MX_LDS_NT_SINGLE
+#define MX_LDS_NT_SINGLE 1
 #endif
 #ifndef MX_LDS_RA
 #define MX_LDS_RA 4
@@ -466,18 +473,24 @@ __global__ __launch_bounds__(256) void k_expert(const ExpertParams p, const Sele
 #define MX_LDS_RB_KM2 2
 #endif
 
+#ifndef MX_LDS_OCC_F16
+#define MX_LDS_OCC_F16 2  // 4-wave fp16 blocks per CU
+#endif
+#ifndef MX_LDS_8W
+#define MX_LDS_8W 1  // 8-wave fp16 blocks where lds_eight_waves picks them
+#endif
 template <int WF>
 struct LdsShape {
   // fp16 fits two 4-wave blocks per CU; the int8 variant (conversion temporaries, 64-
   // column stages) needs the full register file of one block per CU to avoid spills.
-  static constexpr int OCC = WF == MX_DT_F16 ? 2 : 1;
+  static constexpr int OCC = WF == MX_DT_F16 ? MX_LDS_OCC_F16 : 1;
   // MFMA k-steps per stage: each weight row is read KM * 64 contiguous bytes per stage.
   static constexpr int KM = WF == MX_DT_F16 ? MX_LDS_KM_F16 : 1;
 };
 
 // One block's work: MB = 16 * MTX rows (from `base` of group g) x NW waves of 16 * NBIX
 // columns (x 2 for gate and up) starting at column n0b.
-template <int WF, bool GU, int MTX, int NBIX, int NW>
+template <int WF, bool GU, int MTX, int NBIX, int NW, bool NT>
 __device__ __forceinline__ void expert_lds_tile(const ExpertParams& p, char* lds, int g,
                                                 int base, int trows, int n0b) {
   using Tr = WTr<WF>;
@@ -557,7 +570,7 @@ __device__ __forceinline__ void expert_lds_tile(const ExpertParams& p, char* lds
 #pragma unroll
       for (int f = 0; f < NF; ++f) {
         const int fi = GU ? (f % NBIX) : f;
-        br[km][f] = mx_ldw16<GU ? MX_LDS_NT_GU : MX_LDS_NT_DN>((GU && f >= NBIX) ? rb1 : rb0,
+        br[km][f] = mx_ldw16<NT>((GU && f >= NBIX) ? rb1 : rb0,
                                                                 kin ? boff[fi] + kb : MX_OOB);
       }
     }
@@ -691,7 +704,9 @@ __device__ __forceinline__ void expert_lds_tile(const ExpertParams& p, char* lds
 // Qwen3-Next gate/up, K = 2048: 531 -> 499 us) and lose outside (GLM-4.7 gate/up,
 // K = 5120: 1111 -> 1170 us; Qwen3-Next down, K = 512: 369 -> 477 us, where a lone block's
 // pipeline fill and epilogue are no longer hidden behind a second block on the CU).
-static bool lds_eight_waves(int wdt, int K) { return wdt == MX_DT_F16 && K >= 1024 && K <= 3072; }
+static bool lds_eight_waves(int wdt, int K) {
+  return MX_LDS_8W && wdt == MX_DT_F16 && K >= 1024 && K <= 3072;
+}
 
 template <int WF, bool GU, int NW>
 __global__ __launch_bounds__((64 * NW), (LdsShape<WF>::OCC * 4 / NW)) void k_expert_lds(
@@ -711,7 +726,12 @@ __global__ __launch_bounds__((64 * NW), (LdsShape<WF>::OCC * 4 / NW)) void k_exp
   const int N = p.g_expert[g] == p.E ? p.N_s : p.N_r;
   const int n0b = nb * NW * 16 * NBI;
   if (n0b >= N) return;  // whole block past this expert's columns
-  expert_lds_tile<WF, GU, 8, NBI, NW>(p, lds, g, row0, min(MB, p.g_count[g] - row0), n0b);
+  const int trows = min(MB, p.g_count[g] - row0);
+  if (MX_LDS_NT_SINGLE && p.g_count[g] <= MB)
+    expert_lds_tile<WF, GU, 8, NBI, NW, true>(p, lds, g, row0, trows, n0b);
+  else
+    expert_lds_tile<WF, GU, 8, NBI, NW, GU ? MX_LDS_NT_GU : MX_LDS_NT_DN>(p, lds, g, row0, trows,
+                                                                          n0b);
 }
 
 // ------------------------------------------------------------------------------------
