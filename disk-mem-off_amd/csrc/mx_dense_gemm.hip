@@ -39,6 +39,7 @@
 // r = 0..3.
 #include "mx_common.h"
 #include "mx_internal.h"
+#include "mx_lds_copy.h"
 
 namespace {
 
@@ -76,27 +77,6 @@ constexpr int STAGE_BYTES = 64;  // bytes of each row per stage (16 B per lane q
 #endif
 
 
-
-typedef __attribute__((address_space(3))) void lds_void;
-
-// One 16-byte piece per lane from global memory into LDS: lane l's piece lands at
-// dst + 16 l (the buffer load's LDS mode).
-__device__ __forceinline__ void copy_to_lds16(rsrc_t r, char* dst, uint32_t off) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)dst, 16, off, 0, 0, 0);
-}
-
-// Wait until at most n (< 16) vector memory operations of this wave are outstanding, then
-// meet the other waves at a barrier.  No memory fence on the way in (a release fence on
-// LDS would wait for every copy into LDS still in flight); the acquire fence after the
-// barrier keeps the compiler from moving the next LDS reads above it.
-template <int N>
-__device__ __forceinline__ void wait_copies_and_barrier() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
 
 template <typename ET, bool SPLIT, int BM, int BN, int WM, int WN, int NS, int OCC>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, OCC) void k_gemm_nt(
@@ -183,7 +163,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, OCC) void k_gemm_nt(
 #pragma unroll
     for (int i = 0; i < DPW; ++i) {
       const int f = wave + i * NW;
-      copy_to_lds16(rsrc_of(i), slot + f * 1024, goff[i] + (uint32_t)st * STAGE_BYTES);
+      mx_copy_to_lds16(rsrc_of(i), slot + f * 1024, goff[i] + (uint32_t)st * STAGE_BYTES);
     }
   };
 
@@ -212,9 +192,9 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, OCC) void k_gemm_nt(
     // flight), then every wave's are, and every wave has finished computing stage st - 1,
     // whose slot the next copies overwrite.
     if (st + NS - 1 <= nst)
-      wait_copies_and_barrier<(NS - 2) * DPW>();
+      mx_wait_copies_and_barrier<(NS - 2) * DPW>();
     else
-      wait_copies_and_barrier<0>();
+      mx_wait_copies_and_barrier<0>();
     if (st + NS - 1 < nst) issue(st + NS - 1);
     const char* slot = lds + (st % NS) * SLOT;
     int4_t af[MF], bf[NF];
