@@ -460,6 +460,9 @@ __global__ __launch_bounds__(256) void k_expert(const ExpertParams p, const Sele
 // spills (250-252 VGPRs).  Same box, interleaved: Qwen3-Next 4096 tokens gate/up 497 ->
 // 479 us, down 341 -> 335 us; GLM-4.7 2048-token Zipf prefill gate/up 1117 -> 1085 us,
 // down 684 -> 639 us.
+#ifndef MX_LDS_XCD_REAL
+#define MX_LDS_XCD_REAL 1  // XCD runs over the actual m-tiles (else over the mt_max bound)
+#endif
 #ifndef MX_LDS_NT_SINGLE
 #define MX_LDS_NT_SINGLE 1
 #endif
@@ -716,11 +719,21 @@ __global__ __launch_bounds__((64 * NW), (LdsShape<WF>::OCC * 4 / NW)) void k_exp
   constexpr int MB = 128;
   __shared__ __align__(16) char lds[2 * MB * (KS * 2 + 16)];
 
+  // The grid is sized for mt_max (an upper bound of the m-tile count); the blocks of the
+  // actual n_mtiles x nblk tiles are dealt to the 8 XCDs (hardware block b runs on XCD
+  // b % 8) in 8 equal contiguous runs, so every XCD gets the same share of the work and the
+  // blocks of one run walk the m-tiles of a column slab in order.
   const int b = blockIdx.x;
-  const int logical = (b & 7) * (gridDim.x >> 3) + (b >> 3);
-  const int nb = logical / mt_max;
-  const int mt = logical - nb * mt_max;
-  if (nb >= nblk || mt >= mt_max || mt >= *p.n_mtiles) return;
+  const int nmt = min(*p.n_mtiles, mt_max);
+  const int real = nmt * nblk;
+  const int per = (real + 7) >> 3;
+  const int logical = MX_LDS_XCD_REAL ? (b & 7) * per + (b >> 3)
+                                      : (b & 7) * (gridDim.x >> 3) + (b >> 3);
+  const int span = MX_LDS_XCD_REAL ? nmt : mt_max;
+  if (MX_LDS_XCD_REAL && (b >> 3) >= per) return;
+  const int nb = logical / span;
+  const int mt = logical - nb * span;
+  if (nb >= nblk || mt >= nmt) return;
   const int g = p.mt_group[mt];
   const int row0 = p.mt_row0[mt];
   const int N = p.g_expert[g] == p.E ? p.N_s : p.N_r;
