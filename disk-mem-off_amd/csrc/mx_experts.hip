@@ -702,13 +702,18 @@ __device__ __forceinline__ void expert_lds_tile(const ExpertParams& p, char* lds
 }
 
 // Waves per block of the prefill kernel: 4 (two blocks per CU) or 8 (fp16 only; one block
-// per CU, one staged activation tile for twice the columns).  Measured on MI355X: 8 waves
-// win for reductions of 1024-3072 columns (GLM-4.7 down, K = 1536: 731 -> 692 us;
-// Qwen3-Next gate/up, K = 2048: 531 -> 499 us) and lose outside (GLM-4.7 gate/up,
-// K = 5120: 1111 -> 1170 us; Qwen3-Next down, K = 512: 369 -> 477 us, where a lone block's
-// pipeline fill and epilogue are no longer hidden behind a second block on the CU).
+// per CU, one staged activation tile for twice the columns).  Measured on MI355X with the
+// work dealt evenly over the XCDs: 8 waves win for reductions of 1024 columns and more
+// (GLM-4.7 gate/up, K = 5120: 1050 -> 983 us; down, K = 1536: 652 -> 621 us; Qwen3-Next
+// gate/up, K = 2048: equal) and tie for the Qwen3-Next down, K = 512 (333 -> 334 us).
+#ifndef MX_LDS_8W_KMIN
+#define MX_LDS_8W_KMIN 1024
+#endif
+#ifndef MX_LDS_8W_KMAX
+#define MX_LDS_8W_KMAX (1 << 30)
+#endif
 static bool lds_eight_waves(int wdt, int K) {
-  return MX_LDS_8W && wdt == MX_DT_F16 && K >= 1024 && K <= 3072;
+  return MX_LDS_8W && wdt == MX_DT_F16 && K >= MX_LDS_8W_KMIN && K <= MX_LDS_8W_KMAX;
 }
 
 template <int WF, bool GU, int NW>
