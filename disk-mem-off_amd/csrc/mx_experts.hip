@@ -460,6 +460,15 @@ __global__ __launch_bounds__(256) void k_expert(const ExpertParams p, const Sele
 // spills (250-252 VGPRs).  Same box, interleaved: Qwen3-Next 4096 tokens gate/up 497 ->
 // 479 us, down 341 -> 335 us; GLM-4.7 2048-token Zipf prefill gate/up 1117 -> 1085 us,
 // down 684 -> 639 us.
+// Block order inside an XCD run: 0 slab-major (a column slab's m-tiles in a row), 1 tile-
+// major (an m-tile's column slabs in a row), 2 expert-major (a group's blocks in a row,
+// slabs outer, its m-tiles inner: single-tile groups reuse their staged activation rows
+// across slabs through L2, sibling m-tiles of a hot expert read each weight slab
+// together).  Same box, interleaved, order 0 / 1 / 2: Qwen3-Next 4096 tokens 978 / 954 /
+// 957 us, GLM-4.7 Zipf prefill 1830 / 1865 / 1807 us.
+#ifndef MX_LDS_ORDER
+#define MX_LDS_ORDER 2
+#endif
 #ifndef MX_LDS_XCD_REAL
 #define MX_LDS_XCD_REAL 1  // XCD runs over the actual m-tiles (else over the mt_max bound)
 #endif
@@ -736,8 +745,27 @@ __global__ __launch_bounds__((64 * NW), (LdsShape<WF>::OCC * 4 / NW)) void k_exp
                                       : (b & 7) * (gridDim.x >> 3) + (b >> 3);
   const int span = MX_LDS_XCD_REAL ? nmt : mt_max;
   if (MX_LDS_XCD_REAL && (b >> 3) >= per) return;
-  const int nb = logical / span;
-  const int mt = logical - nb * span;
+  int nb, mt;
+  if (MX_LDS_ORDER == 1 && MX_LDS_XCD_REAL) {
+    // tile-major: one m-tile's column slabs in a row
+    mt = logical / nblk;
+    nb = logical - mt * nblk;
+    if (mt >= nmt) return;
+  } else if (MX_LDS_ORDER == 2 && MX_LDS_XCD_REAL) {
+    // expert-major: one group's blocks in a row, column slabs outer and its m-tiles inner
+    // (the m-tiles of a group are consecutive in the list; row0 = 128 x tile index).
+    const int mtp = logical / nblk;
+    if (mtp >= nmt) return;
+    const int gg = p.mt_group[mtp];
+    const int t0 = mtp - p.mt_row0[mtp] / MB;
+    const int ntg = (p.g_count[gg] + MB - 1) / MB;
+    const int local = logical - nblk * t0;
+    nb = local / ntg;
+    mt = t0 + (local - nb * ntg);
+  } else {
+    nb = logical / span;
+    mt = logical - nb * span;
+  }
   if (nb >= nblk || mt >= nmt) return;
   const int g = p.mt_group[mt];
   const int row0 = p.mt_row0[mt];
