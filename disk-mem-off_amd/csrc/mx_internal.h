@@ -13,8 +13,8 @@ int mx_router_splits_for(int tokens, int hidden, int n_experts, int has_shared_g
 // writes the low plane of h16, and its workspace holds the router rows' planes).
 bool mx_router_on_split(int tokens, int hidden, int e1, int weight_dtype);
 size_t mx_router_split_bytes(int hidden, int e1);
-// Router logit partials from the planes h16 / h16lo (RMSNorm outputs) and the router rows
-// split into `wsplit` (mx_router_split_bytes) by this call.
+// Router logit partials from the planes h16 / h16lo and the router rows' planes in
+// `wsplit` (mx_router_split_bytes), all written by the block's RMSNorm launch.
 int mx_router_logits_split(const void* h16, const void* h16lo, const void* router_w,
                            const void* shared_gate_w, int param_dtype, int tokens, int hidden,
                            int n_experts, int splits, void* wsplit, float* logits, hipStream_t s);
@@ -28,8 +28,22 @@ int mx_max_mtiles(int tokens, int top_k, int n_experts, int has_shared, int m_bl
 int mx_m_blk_for(int tokens, int weight_dtype);
 
 // RMSNorm launch (vectorised when the row fits the register tile).
+// The router rows' fp16 planes [E1, H] (hi, lo) that the RMSNorm launch writes for the
+// split-plane router GEMM.
+struct MxRouterSplitW {
+  const void* wr;   // router rows [E, H]
+  const void* wsg;  // shared-expert gate row [H] (row E when E1 > E)
+  int pdt;
+  int E, E1;
+  _Float16* whi;
+  _Float16* wlo;
+};
+// The planes' place in a workspace region of mx_router_split_bytes.
+MxRouterSplitW mx_router_split_planes(const void* router_w, const void* shared_gate_w,
+                                      int param_dtype, int n_experts, int hidden, void* wsplit);
 int mx_rmsnorm_launch(const float* x, const void* norm_w, int param_dtype, float eps, int tokens,
-                      int hidden, float* h32, void* h16, hipStream_t s, void* h16lo = nullptr);
+                      int hidden, float* h32, void* h16, hipStream_t s, void* h16lo = nullptr,
+                      const MxRouterSplitW* rsw = nullptr);
 
 // Decode router (T <= 64): RMSNorm + logits kernel, then a single-workgroup
 // top-k/dispatch kernel.  mx_router_decode_ok tells whether the shape and the pointer

@@ -137,8 +137,15 @@ int run_stage(int stage, const MxMoeDesc* d, const MxMoeWeights* w, const float*
   switch (stage) {
     case 0:
       if (!x || !w->norm_w) return MX_ERR_INVALID;
+      if (in.h16lo) {  // the split-plane router's planes of h and of the router rows
+        const MxRouterSplitW rsw = mx_router_split_planes(
+            w->router_w, d->has_shared_gate ? w->shared_gate_w : nullptr, d->param_dtype,
+            d->n_experts, d->hidden, in.wsplit);
+        return mx_rmsnorm_launch(x, w->norm_w, d->param_dtype, d->eps, T, d->hidden, v.h32,
+                                 v.h16, s, in.h16lo, &rsw);
+      }
       return mx_rmsnorm_launch(x, w->norm_w, d->param_dtype, d->eps, T, d->hidden, v.h32, v.h16,
-                               s, in.h16lo);
+                               s);
     case 1:
       if (decode)
         return mx_router_decode_launch(d, w, T, x, v.h32, v.h16, v.logits, v.topk_ids, v.topk_w,

@@ -15,7 +15,10 @@
 // VEC: each thread keeps its float4 slices of the row in registers (H <= 256 * 4 * RN_V),
 // so all loads of a row are in flight together.  Outputs: h32 (fp32), h16 = fp16(h) and,
 // for the split-plane router GEMM, h16lo = fp16((h - h16) * 2^11) (h - h16 is exact in
-// fp32, and so is the power-of-two scaling).
+// fp32, and so is the power-of-two scaling).  With the split-plane router the launch has
+// E1 x ceil(H / 1024) more blocks, dispatched first, each writing the planes hi = fp16(w),
+// lo = fp16((w - hi) * 2^11) of 1024 elements of one router row (row E = the shared-expert
+// gate row) for the router GEMM.
 // ------------------------------------------------------------------------------------
 #define RN_V 8
 
@@ -24,8 +27,34 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x,
                                                  const void* __restrict__ w, int wdt,
                                                  float eps, int H, float* __restrict__ h32,
                                                  half_t* __restrict__ h16,
-                                                 half_t* __restrict__ h16lo) {
-  const int t = blockIdx.x;
+                                                 half_t* __restrict__ h16lo, int nsplit,
+                                                 MxRouterSplitW rs) {
+  if ((int)blockIdx.x < nsplit) {  // 1024 elements of one router row's planes
+    const int pieces = (H + 1023) >> 10;
+    const int e = blockIdx.x / pieces;
+    const int c0 = (blockIdx.x - e * pieces) * 1024;
+    const void* src = e < rs.E ? rs.wr : rs.wsg;
+    const int base = e < rs.E ? e * H : 0;
+    half_t* hi = rs.whi + (size_t)e * H;
+    half_t* lo = rs.wlo + (size_t)e * H;
+    float v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = c0 + threadIdx.x + 256 * u;
+      v[u] = i < H ? mx_load_param(src, rs.pdt, base + i) : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = c0 + threadIdx.x + 256 * u;
+      if (i < H) {
+        const half_t vh = (half_t)v[u];
+        hi[i] = vh;
+        lo[i] = (half_t)((v[u] - (float)vh) * 2048.f);
+      }
+    }
+    return;
+  }
+  const int t = blockIdx.x - nsplit;
   const float* xr = x + (size_t)t * H;
   float* hr = h32 + (size_t)t * H;
   half_t* hr16 = h16 ? h16 + (size_t)t * H : nullptr;
@@ -97,18 +126,27 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x,
 }
 
 int mx_rmsnorm_launch(const float* x, const void* norm_w, int param_dtype, float eps, int tokens,
-                      int hidden, float* h32, void* h16, hipStream_t s, void* h16lo) {
+                      int hidden, float* h32, void* h16, hipStream_t s, void* h16lo,
+                      const MxRouterSplitW* rsw) {
   if (h16lo && !h16) return MX_ERR_INVALID;
+  MxRouterSplitW rs{};
+  if (rsw) {
+    rs = *rsw;
+    if (!rs.wr || !rs.whi || !rs.wlo || rs.E1 < rs.E || (rs.E1 > rs.E && !rs.wsg))
+      return MX_ERR_INVALID;
+  }
+  const int nsplit = rsw ? rs.E1 * ((hidden + 1023) >> 10) : 0;
+  const unsigned grid = (unsigned)tokens + (unsigned)nsplit;
   const bool vec = hidden % 4 == 0 && hidden <= 256 * 4 * RN_V && mx_aligned16(x) &&
                    mx_aligned16(h32) && (!h16 || ((uintptr_t)h16 & 7u) == 0) &&
                    (!h16lo || ((uintptr_t)h16lo & 7u) == 0);
   mx_clear_error();
   if (vec)
-    hipLaunchKernelGGL(k_rmsnorm<true>, dim3(tokens), dim3(256), 0, s, x, norm_w, param_dtype, eps,
-                       hidden, h32, (half_t*)h16, (half_t*)h16lo);
+    hipLaunchKernelGGL(k_rmsnorm<true>, dim3(grid), dim3(256), 0, s, x, norm_w, param_dtype, eps,
+                       hidden, h32, (half_t*)h16, (half_t*)h16lo, nsplit, rs);
   else
-    hipLaunchKernelGGL(k_rmsnorm<false>, dim3(tokens), dim3(256), 0, s, x, norm_w, param_dtype,
-                       eps, hidden, h32, (half_t*)h16, (half_t*)h16lo);
+    hipLaunchKernelGGL(k_rmsnorm<false>, dim3(grid), dim3(256), 0, s, x, norm_w, param_dtype,
+                       eps, hidden, h32, (half_t*)h16, (half_t*)h16lo, nsplit, rs);
   return mx_launch_status();
 }
 
@@ -329,23 +367,21 @@ static int router_kslice(int hidden, int splits) {
   return mx_ceil_div(kch, splits) * RT_KCH;
 }
 
-// Router rows (and the shared-expert gate row as row E) as two fp16 planes [E1, H]:
-// hi = fp16(w), lo = fp16((w - hi) * 2^11).  fp16 rows are exact in hi (lo = 0).
-__global__ __launch_bounds__(256) void k_router_split_weights(const void* __restrict__ wr,
-                                                              const void* __restrict__ wsg,
-                                                              int pdt, int E, int H, long n,
-                                                              half_t* __restrict__ whi,
-                                                              half_t* __restrict__ wlo) {
-  const long i = (long)blockIdx.x * 256 + threadIdx.x;
-  if (i >= n) return;
-  const int e = (int)(i / H), k = (int)(i - (long)e * H);
-  const float v = e < E ? mx_load_param(wr, pdt, e * H + k) : mx_load_param(wsg, pdt, k);
-  const half_t hi = (half_t)v;
-  whi[i] = hi;
-  wlo[i] = (half_t)((v - (float)hi) * 2048.f);
-}
-
 size_t mx_router_split_bytes(int hidden, int e1) { return mx_align_up((size_t)e1 * hidden * 2, 256) * 2; }
+
+MxRouterSplitW mx_router_split_planes(const void* router_w, const void* shared_gate_w,
+                                      int param_dtype, int n_experts, int hidden, void* wsplit) {
+  const int e1 = n_experts + (shared_gate_w ? 1 : 0);
+  MxRouterSplitW r{};
+  r.wr = router_w;
+  r.wsg = shared_gate_w;
+  r.pdt = param_dtype;
+  r.E = n_experts;
+  r.E1 = e1;
+  r.whi = (half_t*)wsplit;
+  r.wlo = (half_t*)((char*)wsplit + mx_align_up((size_t)e1 * hidden * 2, 256));
+  return r;
+}
 
 int mx_router_logits_split(const void* h16, const void* h16lo, const void* router_w,
                            const void* shared_gate_w, int param_dtype, int tokens, int hidden,
@@ -357,15 +393,10 @@ int mx_router_logits_split(const void* h16, const void* h16lo, const void* route
   if (!mx_router_on_split(tokens, hidden, e1, MX_DT_F16)) return MX_ERR_UNSUPPORTED;
   const int kslice = mx_ceil_div(hidden / 32, splits) * 32;
   if (mx_ceil_div(hidden, kslice) != splits) return MX_ERR_INVALID;
-  half_t* whi = (half_t*)wsplit;
-  half_t* wlo = (half_t*)((char*)wsplit + mx_align_up((size_t)e1 * hidden * 2, 256));
-  const long n = (long)e1 * hidden;
-  mx_clear_error();
-  hipLaunchKernelGGL(k_router_split_weights, dim3((unsigned)mx_ceil_div(n, 256)), dim3(256), 0, s,
-                     router_w, shared_gate_w, param_dtype, n_experts, hidden, n, whi, wlo);
-  MX_TRY(mx_launch_status());
-  MxGemmSeg g{whi, logits, e1, e1};
-  g.w_lo = wlo;
+  const MxRouterSplitW r =
+      mx_router_split_planes(router_w, shared_gate_w, param_dtype, n_experts, hidden, wsplit);
+  MxGemmSeg g{r.whi, logits, e1, e1};
+  g.w_lo = r.wlo;
   return mx_gemm_f16x2_slices(h16, h16lo, tokens, hidden, &g, 1, kslice, (long)tokens * e1, s);
 }
 
