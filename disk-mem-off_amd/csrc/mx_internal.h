@@ -28,19 +28,26 @@ int mx_max_mtiles(int tokens, int top_k, int n_experts, int has_shared, int m_bl
 int mx_m_blk_for(int tokens, int weight_dtype);
 
 // RMSNorm launch (vectorised when the row fits the register tile).
-// The router rows' fp16 planes [E1, H] (hi, lo) that the RMSNorm launch writes for the
-// split-plane router GEMM.
+// What the RMSNorm launch writes for the split-plane router GEMM: the router rows' fp16
+// planes [E, H] (hi, lo) and, with a shared-expert gate row, that row's logit per token
+// (an fp32 dot product with h, into column E of logit slice 0; 0 into the other slices).
 struct MxRouterSplitW {
   const void* wr;   // router rows [E, H]
-  const void* wsg;  // shared-expert gate row [H] (row E when E1 > E)
   int pdt;
-  int E, E1;
+  int E;
   _Float16* whi;
   _Float16* wlo;
+  const void* wsg;  // shared-expert gate row [H] or null
+  float* gate_out;  // logits + E: row stride gate_ld, slice stride gate_slice
+  int gate_ld;
+  long gate_slice;
+  int S;
 };
-// The planes' place in a workspace region of mx_router_split_bytes.
+// The planes' place in a workspace region of mx_router_split_bytes, and the gate logit's
+// place in the logit slices [S, T, E + 1].
 MxRouterSplitW mx_router_split_planes(const void* router_w, const void* shared_gate_w,
-                                      int param_dtype, int n_experts, int hidden, void* wsplit);
+                                      int param_dtype, int n_experts, int hidden, int tokens,
+                                      int splits, void* wsplit, float* logits);
 int mx_rmsnorm_launch(const float* x, const void* norm_w, int param_dtype, float eps, int tokens,
                       int hidden, float* h32, void* h16, hipStream_t s, void* h16lo = nullptr,
                       const MxRouterSplitW* rsw = nullptr);

@@ -140,7 +140,7 @@ int run_stage(int stage, const MxMoeDesc* d, const MxMoeWeights* w, const float*
       if (in.h16lo) {  // the split-plane router's planes of h and of the router rows
         const MxRouterSplitW rsw = mx_router_split_planes(
             w->router_w, d->has_shared_gate ? w->shared_gate_w : nullptr, d->param_dtype,
-            d->n_experts, d->hidden, in.wsplit);
+            d->n_experts, d->hidden, T, v.router_splits, in.wsplit, v.logits);
         return mx_rmsnorm_launch(x, w->norm_w, d->param_dtype, d->eps, T, d->hidden, v.h32,
                                  v.h16, s, in.h16lo, &rsw);
       }

@@ -16,11 +16,27 @@
 // so all loads of a row are in flight together.  Outputs: h32 (fp32), h16 = fp16(h) and,
 // for the split-plane router GEMM, h16lo = fp16((h - h16) * 2^11) (h - h16 is exact in
 // fp32, and so is the power-of-two scaling).  With the split-plane router the launch has
-// E1 x ceil(H / 1024) more blocks, dispatched first, each writing the planes hi = fp16(w),
-// lo = fp16((w - hi) * 2^11) of 1024 elements of one router row (row E = the shared-expert
-// gate row) for the router GEMM.
+// E x ceil(H / 1024) more blocks, dispatched first, each writing the planes hi = fp16(w),
+// lo = fp16((w - hi) * 2^11) of 1024 elements of one router row for the router GEMM, and
+// with a shared-expert gate row (qwen3_next.py:328) each token's block also writes the
+// gate logit h . w_sg (fp32 products and sums) into column E of the logit slices, so the
+// GEMM does not spend a 128-column tile on that one row.
 // ------------------------------------------------------------------------------------
 #define RN_V 8
+
+// Block sum of the per-thread gate partials (after the block's use of red for the sum of
+// squares), then token t's gate logit into slice 0 and zeros into the other slices.
+__device__ __forceinline__ void gate_logit_store(const MxRouterSplitW& rs, int t, float gdot,
+                                                 float* red) {
+  gdot = mx_wave_sum(gdot);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = gdot;
+  __syncthreads();
+  if (threadIdx.x < rs.S) {
+    const float g = threadIdx.x == 0 ? (red[0] + red[1]) + (red[2] + red[3]) : 0.f;
+    rs.gate_out[threadIdx.x * rs.gate_slice + (long)t * rs.gate_ld] = g;
+  }
+}
 
 template <bool VEC>
 __global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x,
@@ -33,8 +49,8 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x,
     const int pieces = (H + 1023) >> 10;
     const int e = blockIdx.x / pieces;
     const int c0 = (blockIdx.x - e * pieces) * 1024;
-    const void* src = e < rs.E ? rs.wr : rs.wsg;
-    const int base = e < rs.E ? e * H : 0;
+    const void* src = rs.wr;
+    const int base = e * H;
     half_t* hi = rs.whi + (size_t)e * H;
     half_t* lo = rs.wlo + (size_t)e * H;
     float v[4];
@@ -80,6 +96,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x,
     __syncthreads();
     ss = (red[0] + red[1]) + (red[2] + red[3]);
     const float rms = sqrtf(ss / (float)H + eps);
+    float gdot = 0.f;
 #pragma unroll
     for (int i = 0; i < RN_V; ++i) {
       const int c = (threadIdx.x + 256 * i) * 4;
@@ -90,6 +107,12 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x,
         o.z = mx_load_param(w, wdt, c + 2) * (v[i].z / rms);
         o.w = mx_load_param(w, wdt, c + 3) * (v[i].w / rms);
         *(float4*)(hr + c) = o;
+        if (rs.gate_out) {
+          gdot = fmaf(o.x, mx_load_param(rs.wsg, rs.pdt, c + 0), gdot);
+          gdot = fmaf(o.y, mx_load_param(rs.wsg, rs.pdt, c + 1), gdot);
+          gdot = fmaf(o.z, mx_load_param(rs.wsg, rs.pdt, c + 2), gdot);
+          gdot = fmaf(o.w, mx_load_param(rs.wsg, rs.pdt, c + 3), gdot);
+        }
         if (hr16) {
           typedef _Float16 h4 __attribute__((ext_vector_type(4)));
           const h4 hi = (h4){(half_t)o.x, (half_t)o.y, (half_t)o.z, (half_t)o.w};
@@ -102,6 +125,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x,
         }
       }
     }
+    if (rs.gate_out) gate_logit_store(rs, t, gdot, red);
   } else {
     float ss = 0.f;
     for (int i = threadIdx.x; i < H; i += 256) {
@@ -113,15 +137,18 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x,
     __syncthreads();
     ss = (red[0] + red[1]) + (red[2] + red[3]);
     const float rms = sqrtf(ss / (float)H + eps);
+    float gdot = 0.f;
     for (int i = threadIdx.x; i < H; i += 256) {
       float v = mx_load_param(w, wdt, i) * (xr[i] / rms);
       hr[i] = v;
+      if (rs.gate_out) gdot = fmaf(v, mx_load_param(rs.wsg, rs.pdt, i), gdot);
       if (hr16) {
         const half_t hi = (half_t)v;
         hr16[i] = hi;
         if (hrlo) hrlo[i] = (half_t)((v - (float)hi) * 2048.f);
       }
     }
+    if (rs.gate_out) gate_logit_store(rs, t, gdot, red);
   }
 }
 
@@ -132,10 +159,10 @@ int mx_rmsnorm_launch(const float* x, const void* norm_w, int param_dtype, float
   MxRouterSplitW rs{};
   if (rsw) {
     rs = *rsw;
-    if (!rs.wr || !rs.whi || !rs.wlo || rs.E1 < rs.E || (rs.E1 > rs.E && !rs.wsg))
+    if (!rs.wr || !rs.whi || !rs.wlo || rs.E < 1 || (rs.gate_out && (!rs.wsg || rs.S < 1)))
       return MX_ERR_INVALID;
   }
-  const int nsplit = rsw ? rs.E1 * ((hidden + 1023) >> 10) : 0;
+  const int nsplit = rsw ? rs.E * ((hidden + 1023) >> 10) : 0;
   const unsigned grid = (unsigned)tokens + (unsigned)nsplit;
   const bool vec = hidden % 4 == 0 && hidden <= 256 * 4 * RN_V && mx_aligned16(x) &&
                    mx_aligned16(h32) && (!h16 || ((uintptr_t)h16 & 7u) == 0) &&
@@ -370,16 +397,22 @@ static int router_kslice(int hidden, int splits) {
 size_t mx_router_split_bytes(int hidden, int e1) { return mx_align_up((size_t)e1 * hidden * 2, 256) * 2; }
 
 MxRouterSplitW mx_router_split_planes(const void* router_w, const void* shared_gate_w,
-                                      int param_dtype, int n_experts, int hidden, void* wsplit) {
+                                      int param_dtype, int n_experts, int hidden, int tokens,
+                                      int splits, void* wsplit, float* logits) {
   const int e1 = n_experts + (shared_gate_w ? 1 : 0);
   MxRouterSplitW r{};
   r.wr = router_w;
-  r.wsg = shared_gate_w;
   r.pdt = param_dtype;
   r.E = n_experts;
-  r.E1 = e1;
   r.whi = (half_t*)wsplit;
   r.wlo = (half_t*)((char*)wsplit + mx_align_up((size_t)e1 * hidden * 2, 256));
+  if (shared_gate_w) {
+    r.wsg = shared_gate_w;
+    r.gate_out = logits + n_experts;
+    r.gate_ld = e1;
+    r.gate_slice = (long)tokens * e1;
+    r.S = splits;
+  }
   return r;
 }
 
@@ -393,9 +426,11 @@ int mx_router_logits_split(const void* h16, const void* h16lo, const void* route
   if (!mx_router_on_split(tokens, hidden, e1, MX_DT_F16)) return MX_ERR_UNSUPPORTED;
   const int kslice = mx_ceil_div(hidden / 32, splits) * 32;
   if (mx_ceil_div(hidden, kslice) != splits) return MX_ERR_INVALID;
-  const MxRouterSplitW r =
-      mx_router_split_planes(router_w, shared_gate_w, param_dtype, n_experts, hidden, wsplit);
-  MxGemmSeg g{r.whi, logits, e1, e1};
+  const MxRouterSplitW r = mx_router_split_planes(router_w, shared_gate_w, param_dtype,
+                                                  n_experts, hidden, tokens, splits, wsplit,
+                                                  logits);
+  // Routed rows only: the shared-expert gate logit (column E) comes from the RMSNorm launch.
+  MxGemmSeg g{r.whi, logits, n_experts, e1};
   g.w_lo = r.wlo;
   return mx_gemm_f16x2_slices(h16, h16lo, tokens, hidden, &g, 1, kslice, (long)tokens * e1, s);
 }
