@@ -9,6 +9,8 @@
 // rows (slot order), adds its shared row and the residual.  No atomics: fixed order.
 #include "mx_common.h"
 
+typedef float f4v __attribute__((ext_vector_type(4)));
+
 template <bool VEC4>
 __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ x,
                                                  const float* __restrict__ y,
@@ -20,13 +22,17 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ x,
   const int* pp = pair_pos + (size_t)t * k;
   if constexpr (VEC4) {
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-    // Slots in groups of 8: all loads of a group are issued before the ordered adds.
+    // Slots in groups of 8: all loads of a group are issued before the ordered adds.  Rows
+    // of y are read once, with the nontemporal hint (Qwen3-Next 4096 tokens: 89 -> 68 us;
+    // GLM-4.7 2048 tokens: 88 -> 74 us).
     for (int j0 = 0; j0 < k; j0 += 8) {
       float4 v[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const int p = (j0 + u < k) ? pp[j0 + u] : -1;
-        v[u] = p >= 0 ? *(const float4*)(y + (size_t)p * H + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const f4v r = p >= 0 ? __builtin_nontemporal_load((const f4v*)(y + (size_t)p * H + c))
+                             : (f4v){0.f, 0.f, 0.f, 0.f};
+        v[u] = make_float4(r[0], r[1], r[2], r[3]);
       }
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
