@@ -429,14 +429,14 @@ __global__ __launch_bounds__(256) void k_expert(const ExpertParams p, const Sele
 // k-chunk (gate/up: 2 gate + 2 up column blocks; down: 4 column blocks), so every A
 // fragment read from LDS feeds 4 MFMAs, and each wave owns a 128-row x 4-fragment tile.
 //
-// Blocks are numbered so that consecutive logical ids run on the same XCD: hardware
-// block b goes to XCD b % 8, logical id = (b % 8) * (grid / 8) + b / 8.  Logical ids walk
-// the m-tiles of one column slab before moving to the next slab.  (Sharing an expert's
-// weights between its m-tiles, through L2 or by 256-row tiles, measured slower on
-// MI355X: the sibling tiles drift apart; a taller tile per wave doubles the LDS reads, and
-// 256-row blocks that pass weight fragments between wave pairs through LDS stage as many
-// activation bytes as weight bytes and cannot share a launch with the 128-row tiles
-// without spilling.)
+// Block order: hardware block b runs on XCD b % 8; the blocks of the actual m-tiles x column
+// slabs are dealt to the 8 XCDs in equal contiguous runs, and inside a run a group's blocks
+// come together (slabs outer, its m-tiles inner), so the sibling m-tiles of a hot expert
+// read each weight slab at about the same time through their XCD's L2 and a single-tile
+// group's activation rows are staged from L2 for every slab after the first (see
+// k_expert_lds).  (256-row tiles, through wave pairs exchanging weight fragments in LDS,
+// measured slower on MI355X: they stage as many activation bytes as weight bytes and
+// cannot share a launch with the 128-row tiles without spilling.)
 // ------------------------------------------------------------------------------------
 // Tunables (compile-time; the defaults are the measured best on MI355X).
 //   MX_LDS_RB:      weight stages in flight per wave (even).
