@@ -501,10 +501,17 @@ struct LdsShape {
 };
 
 // One block's work: MB = 16 * MTX rows (from `base` of group g) x NW waves of 16 * NBIX
-// columns (x 2 for gate and up) starting at column n0b.
-template <int WF, bool GU, int MTX, int NBIX, int NW, bool NT>
+// columns (x 2 for gate and up) starting at column n0b; with CH > 1 (down projection), the
+// `items` consecutive column slabs of NW * 16 * NBIX columns from n0b one after the other,
+// the next slab's first weights and activations loaded while the last stage of the
+// previous one computes, and its epilogue run with those loads in flight (the tile's
+// routing weights come from LDS, `wrow`, so the epilogue issues no global load that would
+// wait for them).
+template <int WF, bool GU, int MTX, int NBIX, int NW, bool NT, int CH = 1>
 __device__ __forceinline__ void expert_lds_tile(const ExpertParams& p, char* lds, int g,
-                                                int base, int trows, int n0b) {
+                                                int base, int trows, int n0b, int items = 1,
+                                                const float* wrow = nullptr) {
+  static_assert(CH == 1 || (!GU && WF == MX_DT_F16), "slab chains: fp16 down projection");
   using Tr = WTr<WF>;
   constexpr int EPL = Tr::EPL, ESZ = Tr::ESZ;
   constexpr int KM = LdsShape<WF>::KM;
@@ -540,8 +547,14 @@ __device__ __forceinline__ void expert_lds_tile(const ExpertParams& p, char* lds
 #pragma unroll
   for (int f = 0; f < NBIX; ++f) {
     const int n = n0 + 16 * f + j;
-    boff[f] = (wact && n < N) ? mx_bfrag_base<EPL, ESZ>(p.tiled, n0 + 16 * f, j, q, K) : MX_OOB;
+    boff[f] = (wact && n < N) ? mx_bfrag_base<EPL, ESZ>(p.tiled, n0 + 16 * f, j, q, K)
+                              : MX_OOB;
   }
+  // Slab chains: weight bytes from one slab to the next (the fragment base is linear in
+  // the first column of a 16-row block).
+  constexpr int SLABW = NW * 16 * NBIX;
+  const uint32_t dslab = p.tiled ? (uint32_t)(SLABW / 16) * (uint32_t)(K / (4 * EPL)) * 1024u
+                                 : (uint32_t)SLABW * rowb;
 
   // Activation chunks this thread stages: fixed rows of the tile, advancing columns.
   const mx_rsrc_t ra = mx_rsrc(p.a, p.a_bytes);
@@ -574,16 +587,18 @@ __device__ __forceinline__ void expert_lds_tile(const ExpertParams& p, char* lds
     for (int i = 0; i < ACH; ++i)
       ar[i] = mx_ld16(ra, (k0 + acol[i] < K) ? agoff[i] + (uint32_t)k0 * 2 : MX_OOB);
   };
-  auto load_b = [&](int st, int4_t (&br)[KM][NF]) {
+  // sb: byte offset of the slab in a slab chain (0 otherwise).
+  auto load_b = [&](int st, int4_t (&br)[KM][NF], uint32_t sb = 0) {
 #pragma unroll
     for (int km = 0; km < KM; ++km) {
       const bool kin = st * KS + km * 4 * EPL + q * EPL < K;
-      const uint32_t kb = ((uint32_t)st * KM + km) * bstep;
+      const uint32_t kb = ((uint32_t)st * KM + km) * bstep + sb;
 #pragma unroll
       for (int f = 0; f < NF; ++f) {
         const int fi = GU ? (f % NBIX) : f;
+        // (this exact form: a temporary for the offset makes the compiler spill)
         br[km][f] = mx_ldw16<NT>((GU && f >= NBIX) ? rb1 : rb0,
-                                                                kin ? boff[fi] + kb : MX_OOB);
+                                 kin ? boff[fi] + kb : MX_OOB);
       }
     }
   };
@@ -639,6 +654,73 @@ __device__ __forceinline__ void expert_lds_tile(const ExpertParams& p, char* lds
   const int nst_pad = (nst + RB - 1) / RB * RB;
   int4_t aring[RA][ACH];
   int4_t bring[RB][KM][NF];
+  if constexpr (CH > 1) {
+    // Slab chain: the same pipeline over `items` slabs in turn.  In the last ring turn of a
+    // slab the loads that run ahead (weights RB - 1 stages, activations RA stages) fetch the
+    // next slab's first stages: the same activation rows, the weights one slab delta
+    // further.  Past the last slab they fetch memory nobody reads (inside the matrix, or
+    // out of range and zero), so no load needs a slab check.  Slab widths divide N (the
+    // launch checks it), so every lane's columns are inside N.
+#pragma unroll
+    for (int u = 0; u < RA; ++u) load_a(u, aring[u]);
+#pragma unroll
+    for (int u = 0; u < RB - 1; ++u) load_b(u, bring[u]);
+    store_a(0, aring[0]);
+    __syncthreads();
+    const int orow = __builtin_amdgcn_readfirstlane(gstart + base);
+    const int trs = __builtin_amdgcn_readfirstlane(trows);
+    for (int ci = 0; ci < items; ++ci) {
+      const uint32_t sb_cur = (uint32_t)ci * dslab, sb_next = sb_cur + dslab;
+      for (int s0 = 0; s0 < nst_pad; s0 += RB) {
+        const bool last = s0 + RB == nst_pad;
+#pragma unroll
+        for (int u = 0; u < RB; ++u) {
+          const int sbn = s0 + u + RB - 1, san = s0 + u + RA;
+          const bool bx = last && sbn >= nst_pad, ax = last && san >= nst_pad;
+          load_b(bx ? sbn - nst_pad : sbn, bring[(u + RB - 1) % RB], bx ? sb_next : sb_cur);
+          compute(u % 2, bring[u]);
+          store_a((u + 1) % 2, aring[(u + 1) % RA]);
+          load_a(ax ? san - nst_pad : san, aring[u % RA]);
+          __syncthreads();
+        }
+      }
+      // Epilogue of slab ci (the down epilogue below, routing weights from LDS).  The
+      // row stride, row count and weight index go through empty asm statements so the
+      // compiler recomputes the addresses here instead of hoisting all 32 rows' addresses
+      // out of the slab loop (where they spill).
+      // Stores through a buffer descriptor of y: 32-bit offsets (the launch checks that y
+      // is under 2 GiB).
+      // (The lane index is recomputed here, by mbcnt in an asm statement the compiler
+      // cannot hoist, so no register holds it across the slab.)
+      int ln;
+      asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
+      int ldo = p.ldo, tr = trs, orw = orow, q4 = (ln >> 4) * 4, cj = ln & 15;
+      asm volatile("" : "+s"(ldo), "+s"(tr), "+s"(orw));
+      const int n0c = n0 + ci * SLABW;
+      if (n0c < N) {
+        const mx_rsrc_t ry = mx_rsrc(p.out, 0x7fffffffu);
+        const uint32_t yb = ((uint32_t)(orw + q4) * (uint32_t)ldo + (uint32_t)(n0c + cj)) * 4u;
+#pragma unroll
+        for (int mi = 0; mi < MTX; ++mi)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int m = 16 * mi + q4 + r;
+            if (m >= tr) continue;
+            const uint32_t yo = yb + (uint32_t)(16 * mi + r) * (uint32_t)ldo * 4u;
+            const float w = wrow[m];
+#pragma unroll
+            for (int f = 0; f < NBIX; ++f)
+              __builtin_amdgcn_raw_buffer_store_b32(
+                  __builtin_bit_cast(int, w * (acc[mi][f][r] * 1.f)), ry, yo + 64u * f, 0, 0);
+          }
+      }
+#pragma unroll
+      for (int mi = 0; mi < MTX; ++mi)
+#pragma unroll
+        for (int f = 0; f < NF; ++f) acc[mi][f] = (float4_t){0.f, 0.f, 0.f, 0.f};
+    }
+    return;
+  }
 #pragma unroll
   for (int u = 0; u < RA; ++u) load_a(u, aring[u]);
 #pragma unroll
@@ -725,13 +807,40 @@ static bool lds_eight_waves(int wdt, int K) {
   return MX_LDS_8W && wdt == MX_DT_F16 && K >= MX_LDS_8W_KMIN && K <= MX_LDS_8W_KMAX;
 }
 
-template <int WF, bool GU, int NW>
+// Slab chains for the fp16 down projection of short reductions (few stages per slab, so a
+// block's pipeline fill and epilogue are a large part of its life).
+#ifndef MX_LDS_CHAIN
+#define MX_LDS_CHAIN 2
+#endif
+#ifndef MX_LDS_CHAIN_KMAX
+#define MX_LDS_CHAIN_KMAX 512
+#endif
+// The chained epilogue stores whole slabs (64 columns per wave) through 32-bit
+// offsets, so every expert's N must be a multiple of 256 and y below 2 GiB.
+#ifndef MX_LDS_CHAIN8
+#define MX_LDS_CHAIN8 1  // slab chains for 8-wave blocks too
+#endif
+static int lds_slab_chain(bool gu, int wdt, int nw, const ExpertParams& p, int mt_max) {
+  if (gu || wdt != MX_DT_F16 || MX_LDS_CHAIN < 2) return 1;
+  if (nw != 4 && !(nw == 8 && MX_LDS_CHAIN8)) return 1;
+  if (nw == 4 && (p.K_r > MX_LDS_CHAIN_KMAX || p.K_s > MX_LDS_CHAIN_KMAX)) return 1;
+  const int slab = nw * 64;
+  if (p.N_r % slab || p.N_s % slab) return 1;
+  if ((long)mt_max * 128 * p.ldo * 4 >= (1l << 31) - 1) return 1;
+  return MX_LDS_CHAIN;
+}
+
+// CH > 1: each block runs up to CH consecutive column slabs of its m-tile in turn
+// (expert_lds_tile's slab chain); nblk counts the slabs, the grid the chains.
+template <int WF, bool GU, int NW, int CH = 1>
 __global__ __launch_bounds__((64 * NW), (LdsShape<WF>::OCC * 4 / NW)) void k_expert_lds(
-    const ExpertParams p, int mt_max, int nblk) {
+    const ExpertParams p, int mt_max, int nslab) {
   constexpr int KS = 4 * WTr<WF>::EPL * LdsShape<WF>::KM;
   constexpr int NBI = GU ? 2 : 4;
   constexpr int MB = 128;
   __shared__ __align__(16) char lds[2 * MB * (KS * 2 + 16)];
+  __shared__ float wrow[CH > 1 ? MB : 1];
+  const int nblk = (nslab + CH - 1) / CH;
 
   // The grid is sized for mt_max (an upper bound of the m-tile count); the blocks of the
   // actual n_mtiles x nblk tiles are dealt to the 8 XCDs (hardware block b runs on XCD
@@ -770,9 +879,19 @@ __global__ __launch_bounds__((64 * NW), (LdsShape<WF>::OCC * 4 / NW)) void k_exp
   const int g = p.mt_group[mt];
   const int row0 = p.mt_row0[mt];
   const int N = p.g_expert[g] == p.E ? p.N_s : p.N_r;
-  const int n0b = nb * NW * 16 * NBI;
+  const int n0b = nb * CH * NW * 16 * NBI;
   if (n0b >= N) return;  // whole block past this expert's columns
   const int trows = min(MB, p.g_count[g] - row0);
+  if constexpr (CH > 1) {
+    const int items = min(CH, nslab - nb * CH);
+    if ((int)threadIdx.x < trows) wrow[threadIdx.x] = p.sorted_w[p.g_start[g] + row0 + threadIdx.x];
+    if (MX_LDS_NT_SINGLE && p.g_count[g] <= MB)
+      expert_lds_tile<WF, GU, 8, NBI, NW, true, CH>(p, lds, g, row0, trows, n0b, items, wrow);
+    else
+      expert_lds_tile<WF, GU, 8, NBI, NW, MX_LDS_NT_DN, CH>(p, lds, g, row0, trows, n0b, items,
+                                                             wrow);
+    return;
+  }
   if (MX_LDS_NT_SINGLE && p.g_count[g] <= MB)
     expert_lds_tile<WF, GU, 8, NBI, NW, true>(p, lds, g, row0, trows, n0b);
   else
@@ -928,10 +1047,20 @@ static int launch_grouped_mt(int wdt, const ExpertParams& p, int mt_max, int m_b
     const int nw = lds_eight_waves(wdt, p.K_r) ? 8 : 4;
     const int cols = nw * 16 * (GU ? 2 : 4);
     const int nblk = mx_ceil_div(nmax, cols);
-    const long blocks = ((long)mt_max * nblk + 7) / 8 * 8;
+    const int ch = lds_slab_chain(GU, wdt, nw, p, mt_max);
+    const long blocks = ((long)mt_max * mx_ceil_div(nblk, ch) + 7) / 8 * 8;
     if (blocks > (1l << 31) - 1) return MX_ERR_UNSUPPORTED;
     mx_clear_error();
-    if (wdt == MX_DT_F16 && nw == 8)
+    if (!GU && ch == 2 && nw == 8 && MX_LDS_CHAIN8)
+      hipLaunchKernelGGL((k_expert_lds<MX_DT_F16, false, 8, 2>), dim3((unsigned)blocks),
+                         dim3(512), 0, s, p, mt_max, nblk);
+    else if (!GU && ch == 2)
+      hipLaunchKernelGGL((k_expert_lds<MX_DT_F16, false, 4, 2>), dim3((unsigned)blocks),
+                         dim3(256), 0, s, p, mt_max, nblk);
+    else if (!GU && ch == 4)
+      hipLaunchKernelGGL((k_expert_lds<MX_DT_F16, false, 4, 4>), dim3((unsigned)blocks),
+                         dim3(256), 0, s, p, mt_max, nblk);
+    else if (wdt == MX_DT_F16 && nw == 8)
       hipLaunchKernelGGL((k_expert_lds<MX_DT_F16, GU, 8>), dim3((unsigned)blocks), dim3(512), 0,
                          s, p, mt_max, nblk);
     else if (wdt == MX_DT_F16)

@@ -37,10 +37,13 @@ def say(msg: str) -> None:
     sys.stdout.flush()
 
 
-def run_device(mi355x, stream, tensors, shape, spec, x):
-    """Forward on the device; returns (out, views dict)."""
+def run_device(mi355x, stream, tensors, shape, spec, x, frag=False):
+    """Forward on the device (expert weights re-laid in MX_LAYOUT_FRAG16 when ``frag``);
+    returns (out, views dict)."""
     dl = DeviceMoeLayer.from_host(mi355x, tensors, stream)
     try:
+        if frag:
+            dl.tile()
         cfg = dl.config(top_k=spec.top_k, router_mode=MODE_CODE[spec.router_mode],
                         routed_scaling=spec.routed_scaling, eps=spec.eps,
                         norm_topk_prob=spec.norm_topk_prob)
@@ -168,6 +171,32 @@ def test_skewed_prefill(mi355x, stream, wdt, T):
     ref = orc.moe_block(x, t, spec)
     assert ref["counts"][:3].min() > 256
     check_routing(views, ref, ref["logits"], bias, spec, f"skew/{wdt}/T={T}", x, t)
+    err = float(np.max(np.abs(out - ref["out"])))
+    say(f"    max abs err {err:.3e}, counts[:3]={ref['counts'][:3].tolist()}")
+    assert err <= LOWP_ABS
+
+
+@pytest.mark.parametrize("frag", [False, True])
+def test_prefill_slab_chains(mi355x, stream, frag):
+    """Short fp16 down reductions run the prefill kernel's slab chains (a block takes two
+    256-column slabs of its m-tile in turn): hidden 768 gives chains of two slabs and of
+    one, reductions of 200 and 136 columns end in partial stages, hot experts span several
+    m-tiles."""
+    say(f"[gpu] prefill slab chains frag16={frag}")
+    inter, shared = (192, 128) if frag else (200, 136)
+    shape = syn.MoeShape(syn.GLM, 768, 24, 4, inter, shared, 2.5, 1e-5)
+    base = syn.make_tensors(shape, 4343)
+    bias = np.zeros(shape.n_experts, np.float32)
+    bias[:3] = [0.8, 0.4, 0.2]
+    base["mlp.gate.e_score_correction_bias"] = bias
+    t = {n: (v.astype(np.float16) if n.startswith(("mlp.experts.", "mlp.shared_experts."))
+             else v) for n, v in base.items()}
+    x = syn.make_inputs(4343, 700, shape.hidden)
+    spec = spec_for(shape, orc.SIGMOID_SELECT_BIAS)
+    out, views = run_device(mi355x, stream, t, shape, spec, x, frag=frag)
+    ref = orc.moe_block(x, t, spec)
+    assert views["m_blk"] == 128 and ref["counts"][:3].min() > 128
+    check_routing(views, ref, ref["logits"], bias, spec, f"slab chains/{frag}", x, t)
     err = float(np.max(np.abs(out - ref["out"])))
     say(f"    max abs err {err:.3e}, counts[:3]={ref['counts'][:3].tolist()}")
     assert err <= LOWP_ABS
