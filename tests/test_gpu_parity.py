@@ -176,15 +176,18 @@ def test_skewed_prefill(mi355x, stream, wdt, T):
     assert err <= LOWP_ABS
 
 
-@pytest.mark.parametrize("frag", [False, True])
-def test_prefill_slab_chains(mi355x, stream, frag):
-    """Short fp16 down reductions run the prefill kernel's slab chains (a block takes two
-    256-column slabs of its m-tile in turn): hidden 768 gives chains of two slabs and of
-    one, reductions of 200 and 136 columns end in partial stages, hot experts span several
-    m-tiles."""
-    say(f"[gpu] prefill slab chains frag16={frag}")
-    inter, shared = (192, 128) if frag else (200, 136)
-    shape = syn.MoeShape(syn.GLM, 768, 24, 4, inter, shared, 2.5, 1e-5)
+@pytest.mark.parametrize("H,inter,shared,frag", [
+    (768, 200, 136, False),    # 4-wave chains of 2 and 1 slabs, partial last stages
+    (768, 192, 128, True),
+    (1536, 1024, 512, True),   # 8-wave chains of 2 and 1 slabs
+])
+def test_prefill_slab_chains(mi355x, stream, H, inter, shared, frag):
+    """fp16 prefill down projections run as slab chains (a block takes two column slabs of
+    its m-tile in turn, the next slab's loads in flight across the epilogue): odd slab
+    counts give chains of two slabs and of one, short reductions end in partial stages,
+    hot experts span several m-tiles."""
+    say(f"[gpu] prefill slab chains H={H} inter={inter} shared={shared} frag16={frag}")
+    shape = syn.MoeShape(syn.GLM, H, 24, 4, inter, shared, 2.5, 1e-5)
     base = syn.make_tensors(shape, 4343)
     bias = np.zeros(shape.n_experts, np.float32)
     bias[:3] = [0.8, 0.4, 0.2]
