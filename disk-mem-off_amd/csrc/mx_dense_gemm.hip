@@ -75,6 +75,9 @@ constexpr int STAGE_BYTES = 64;  // bytes of each row per stage (16 B per lane q
 #ifndef MX_GEMM_NS
 #define MX_GEMM_NS 4  // stage slots in the LDS ring
 #endif
+#ifndef MX_GEMM_GM
+#define MX_GEMM_GM 4  // row blocks per group of the block order (0: one column block at a time)
+#endif
 
 
 
@@ -95,13 +98,27 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, OCC) void k_gemm_nt(
   __shared__ __align__(1024) char lds[NS * SLOT];
 
   // Blocks are numbered so that consecutive logical ids run on one XCD (hardware block b
-  // goes to XCD b % 8); logical ids walk the row blocks of one column block first, so the
-  // blocks sharing a weight slab run together on one XCD.
+  // goes to XCD b % 8).  Logical ids walk groups of MX_GEMM_GM row blocks: the row blocks of
+  // a group for one column block, then for the next, so the blocks an XCD runs at once
+  // share few operand tiles through its L2 (32 blocks: 4 row x 8 column blocks, 12
+  // distinct tiles per stage, where one column block's 16 row blocks and the next's
+  // need 18).
   const int nb_total = gridDim.x;
   const int b = blockIdx.x;
   const int logical = (nb_total % 8 == 0) ? (b & 7) * (nb_total >> 3) + (b >> 3) : b;
-  int rem = logical / p.mblk;
-  const int mb = logical - rem * p.mblk;
+  int rem, mb;
+  if (MX_GEMM_GM > 0) {
+    const int ncol = nb_total / p.mblk;
+    const int grp = logical / (MX_GEMM_GM * ncol);
+    const int first = grp * MX_GEMM_GM;
+    const int gm = min(p.mblk - first, MX_GEMM_GM);
+    const int in = logical - grp * MX_GEMM_GM * ncol;
+    rem = in / gm;
+    mb = first + (in - rem * gm);
+  } else {
+    rem = logical / p.mblk;
+    mb = logical - rem * p.mblk;
+  }
   int si = 0;
 #pragma unroll
   for (int i = 0; i < MX_GEMM_MAX_SEG - 1; ++i)
