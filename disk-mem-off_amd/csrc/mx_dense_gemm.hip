@@ -75,6 +75,11 @@ constexpr int STAGE_BYTES = 64;  // bytes of each row per stage (16 B per lane q
 #ifndef MX_GEMM_NS
 #define MX_GEMM_NS 4  // stage slots in the LDS ring
 #endif
+// Operand fragments read one stage ahead (fp16 256 x 256 tiles; the 128 x 128 tiles at two
+// blocks per CU lose with it: out projection 89 -> 92 us, against qkvz + ba 410 -> 401 us).
+#ifndef MX_GEMM_PF
+#define MX_GEMM_PF 1
+#endif
 #ifndef MX_GEMM_GM
 #define MX_GEMM_GM 4  // row blocks per group of the block order (0: one column block at a time)
 #endif
@@ -204,6 +209,57 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, OCC) void k_gemm_nt(
 #pragma unroll
   for (int s0 = 0; s0 < NS - 1; ++s0)
     if (s0 < nst) issue(s0);
+  if constexpr (!SPLIT && ES == 2 && MX_GEMM_PF && BM == 256) {
+    // Fragments one stage ahead: stage st + 1's operand fragments are read from LDS while
+    // stage st's MFMAs run (two register sets, alternating), so no stage starts with the
+    // MFMA pipe waiting on LDS reads after its barrier.  Stage st + 1's copies must have
+    // landed before that read: the barrier of iteration st waits for them, leaving the
+    // copies of the stages after st + 1 in flight.  The slot the copies of iteration st
+    // overwrite held stage st - 1, whose fragments every wave consumed in iteration st - 1.
+    auto wait_landed = [&](int ahead) {  // ahead: stages issued after the awaited one
+      if (ahead >= 2) mx_wait_copies_and_barrier<2 * DPW>();
+      else if (ahead == 1) mx_wait_copies_and_barrier<DPW>();
+      else mx_wait_copies_and_barrier<0>();
+    };
+    auto read_frags = [&](int st, int4_t (&af)[MF], int4_t (&bf)[NF]) {
+      const char* slot = lds + (st % NS) * SLOT;
+#pragma unroll
+      for (int ni = 0; ni < NF; ++ni)
+        bf[ni] = *(const int4_t*)(slot + (FA + wn * NF + ni) * 1024 + rpos);
+#pragma unroll
+      for (int mi = 0; mi < MF; ++mi)
+        af[mi] = *(const int4_t*)(slot + (wm * MF + mi) * 1024 + rpos);
+    };
+    auto mfmas = [&](const int4_t (&af)[MF], const int4_t (&bf)[NF]) {
+#pragma unroll
+      for (int mi = 0; mi < MF; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < NF; ++ni)
+          acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              __builtin_bit_cast(half8_t, bf[ni]), __builtin_bit_cast(half8_t, af[mi]),
+              acc[mi][ni], 0, 0, 0);
+    };
+    // Every step waits, meets the barrier and reads (the last one reads a slot whose copies
+    // have all landed and whose fragments nobody uses), so the LDS-read counter is in the
+    // same state on every path and the MFMAs wait only for the older fragment set.
+    auto step = [&](int st, const int4_t (&ca)[MF], const int4_t (&cb)[NF], int4_t (&na)[MF],
+                    int4_t (&nb)[NF]) {
+      wait_landed(min(NS - 3, nst - st - 2));
+      if (st + NS - 1 < nst) issue(st + NS - 1);
+      read_frags(st + 1, na, nb);
+      __builtin_amdgcn_sched_barrier(0);  // the reads go out before the MFMAs
+      mfmas(ca, cb);
+    };
+    int4_t fa0[MF], fb0[NF], fa1[MF], fb1[NF];
+    if (nst > 0) {
+      wait_landed(min(NS - 2, nst - 1));
+      read_frags(0, fa0, fb0);
+    }
+    for (int st = 0; st < nst; st += 2) {
+      step(st, fa0, fb0, fa1, fb1);
+      if (st + 1 < nst) step(st + 1, fa1, fb1, fa0, fb0);
+    }
+  } else
   for (int st = 0; st < nst; ++st) {
     // This wave's copies of stage st are done (the NS - 2 later stages may still be in
     // flight), then every wave's are, and every wave has finished computing stage st - 1,
