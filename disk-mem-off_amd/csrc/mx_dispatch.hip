@@ -147,12 +147,21 @@ __global__ __launch_bounds__(1024) void k_dispatch_scan(
   int* gid = off + E;
   int* mtb = gid + E;
   __shared__ int s_tot[3];
+  // Per expert, the chunk counts are read 16 at a time (all loads of a batch in flight
+  // together, then the in-place prefix), not one dependent round trip per chunk.
   for (int e = threadIdx.x; e < E; e += blockDim.x) {
     int run = 0;
-    for (int c = 0; c < nch; ++c) {
-      const int n = chunk_counts[(size_t)c * E + e];
-      chunk_counts[(size_t)c * E + e] = run;
-      run += n;
+    for (int c0 = 0; c0 < nch; c0 += 16) {
+      int n[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        n[u] = c0 + u < nch ? chunk_counts[(size_t)(c0 + u) * E + e] : 0;
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        if (c0 + u < nch) {
+          chunk_counts[(size_t)(c0 + u) * E + e] = run;
+          run += n[u];
+        }
     }
     tot[e] = run;
     counts[e] = run;
