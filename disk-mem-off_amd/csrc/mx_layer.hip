@@ -141,7 +141,10 @@ int run_stage(int stage, const MxMoeDesc* d, const MxMoeWeights* w, const float*
         const MxRouterSplitW rsw = mx_router_split_planes(
             w->router_w, d->has_shared_gate ? w->shared_gate_w : nullptr, d->param_dtype,
             d->n_experts, d->hidden, T, v.router_splits, in.wsplit, v.logits);
-        return mx_rmsnorm_launch(x, w->norm_w, d->param_dtype, d->eps, T, d->hidden, v.h32,
+        // The router reads the planes and the experts h16 (the split needs fp16 / int8
+        // experts): no later stage reads the fp32 rows, so they are not written (GLM-4.7
+        // 2048-token prefill: RMSNorm 27.5 -> 23.5 us).
+        return mx_rmsnorm_launch(x, w->norm_w, d->param_dtype, d->eps, T, d->hidden, nullptr,
                                  v.h16, s, in.h16lo, &rsw);
       }
       return mx_rmsnorm_launch(x, w->norm_w, d->param_dtype, d->eps, T, d->hidden, v.h32, v.h16,

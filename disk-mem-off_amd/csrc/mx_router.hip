@@ -13,7 +13,9 @@
 // ------------------------------------------------------------------------------------
 // RMSNorm: one 256-thread block per token.  h = w * (x / sqrt(mean(x^2) + eps)).
 // VEC: each thread keeps its float4 slices of the row in registers (H <= 256 * 4 * RN_V),
-// so all loads of a row are in flight together.  Outputs: h32 (fp32), h16 = fp16(h) and,
+// so all loads of a row are in flight together.  (One wave per token, four tokens per
+// block, measured slower for Qwen3-Next's H = 2048: 28 -> 32 us at 4096 tokens.)  Outputs:
+// h32 (fp32; left out when null), h16 = fp16(h) and,
 // for the split-plane router GEMM, h16lo = fp16((h - h16) * 2^11) (h - h16 is exact in
 // fp32, and so is the power-of-two scaling).  With the split-plane router the launch has
 // E x ceil(H / 1024) more blocks, dispatched first, each writing the planes hi = fp16(w),
@@ -72,7 +74,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x,
   }
   const int t = blockIdx.x - nsplit;
   const float* xr = x + (size_t)t * H;
-  float* hr = h32 + (size_t)t * H;
+  float* hr = h32 ? h32 + (size_t)t * H : nullptr;
   half_t* hr16 = h16 ? h16 + (size_t)t * H : nullptr;
   half_t* hrlo = h16lo ? h16lo + (size_t)t * H : nullptr;
   __shared__ float red[4];
@@ -106,7 +108,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x,
         o.y = mx_load_param(w, wdt, c + 1) * (v[i].y / rms);
         o.z = mx_load_param(w, wdt, c + 2) * (v[i].z / rms);
         o.w = mx_load_param(w, wdt, c + 3) * (v[i].w / rms);
-        *(float4*)(hr + c) = o;
+        if (hr) *(float4*)(hr + c) = o;
         if (rs.gate_out) {
           gdot = fmaf(o.x, mx_load_param(rs.wsg, rs.pdt, c + 0), gdot);
           gdot = fmaf(o.y, mx_load_param(rs.wsg, rs.pdt, c + 1), gdot);
@@ -140,7 +142,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x,
     float gdot = 0.f;
     for (int i = threadIdx.x; i < H; i += 256) {
       float v = mx_load_param(w, wdt, i) * (xr[i] / rms);
-      hr[i] = v;
+      if (hr) hr[i] = v;
       if (rs.gate_out) gdot = fmaf(v, mx_load_param(rs.wsg, rs.pdt, i), gdot);
       if (hr16) {
         const half_t hi = (half_t)v;
@@ -162,10 +164,11 @@ int mx_rmsnorm_launch(const float* x, const void* norm_w, int param_dtype, float
     if (!rs.wr || !rs.whi || !rs.wlo || rs.E < 1 || (rs.gate_out && (!rs.wsg || rs.S < 1)))
       return MX_ERR_INVALID;
   }
+  if (!h32 && !h16) return MX_ERR_INVALID;
   const int nsplit = rsw ? rs.E * ((hidden + 1023) >> 10) : 0;
   const unsigned grid = (unsigned)tokens + (unsigned)nsplit;
   const bool vec = hidden % 4 == 0 && hidden <= 256 * 4 * RN_V && mx_aligned16(x) &&
-                   mx_aligned16(h32) && (!h16 || ((uintptr_t)h16 & 7u) == 0) &&
+                   (!h32 || mx_aligned16(h32)) && (!h16 || ((uintptr_t)h16 & 7u) == 0) &&
                    (!h16lo || ((uintptr_t)h16lo & 7u) == 0);
   mx_clear_error();
   if (vec)

@@ -111,7 +111,9 @@ typedef struct MxMoeWeights {
 
 /* Views into a forward workspace (all device pointers), for inspection after a call. */
 typedef struct MxMoeViews {
-  float* h32;          /* [T, H] rms-normalised activations                             */
+  float* h32;          /* [T, H] rms-normalised activations; not written by a forward   */
+                       /* whose router runs on fp16 planes (T >= 65, fp16 / int8        */
+                       /* experts, H a multiple of 32): h16 holds them there            */
   void* h16;           /* [T, H] fp16 copy (NULL for MX_DT_F32 weights)                 */
   float* logits;       /* [S, T, E(+1)] router logit partials (S = router_splits)        */
   int32_t router_splits;
