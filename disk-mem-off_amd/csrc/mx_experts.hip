@@ -114,6 +114,7 @@ struct ExpertParams {
   int N_r, K_r;           // routed expert: output columns, reduction length
   int N_s, K_s;           // shared expert
   int tiled;              // weights in MX_LAYOUT_FRAG16 (else row-major)
+  int y16 = 0;            // down, prefill kernel: y rows stored as fp16 (else fp32)
 };
 
 // One-token selection inside the gate/up launch (used in place of the top-k/dispatch
@@ -507,11 +508,12 @@ struct LdsShape {
 // previous one computes, and its epilogue run with those loads in flight (the tile's
 // routing weights come from LDS, `wrow`, so the epilogue issues no global load that would
 // wait for them).
-template <int WF, bool GU, int MTX, int NBIX, int NW, bool NT, int CH = 1>
+template <int WF, bool GU, int MTX, int NBIX, int NW, bool NT, int CH = 1, bool Y16 = false>
 __device__ __forceinline__ void expert_lds_tile(const ExpertParams& p, char* lds, int g,
                                                 int base, int trows, int n0b, int items = 1,
                                                 const float* wrow = nullptr) {
   static_assert(CH == 1 || (!GU && WF == MX_DT_F16), "slab chains: fp16 down projection");
+  static_assert(!(GU && Y16), "fp16 y rows: down projection");
   using Tr = WTr<WF>;
   constexpr int EPL = Tr::EPL, ESZ = Tr::ESZ;
   constexpr int KM = LdsShape<WF>::KM;
@@ -698,20 +700,27 @@ __device__ __forceinline__ void expert_lds_tile(const ExpertParams& p, char* lds
       asm volatile("" : "+s"(ldo), "+s"(tr), "+s"(orw));
       const int n0c = n0 + ci * SLABW;
       if (n0c < N) {
+        constexpr uint32_t YE = Y16 ? 2u : 4u;  // bytes per element of y
         const mx_rsrc_t ry = mx_rsrc(p.out, 0x7fffffffu);
-        const uint32_t yb = ((uint32_t)(orw + q4) * (uint32_t)ldo + (uint32_t)(n0c + cj)) * 4u;
+        const uint32_t yb = ((uint32_t)(orw + q4) * (uint32_t)ldo + (uint32_t)(n0c + cj)) * YE;
 #pragma unroll
         for (int mi = 0; mi < MTX; ++mi)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int m = 16 * mi + q4 + r;
             if (m >= tr) continue;
-            const uint32_t yo = yb + (uint32_t)(16 * mi + r) * (uint32_t)ldo * 4u;
+            const uint32_t yo = yb + (uint32_t)(16 * mi + r) * (uint32_t)ldo * YE;
             const float w = wrow[m];
 #pragma unroll
-            for (int f = 0; f < NBIX; ++f)
-              __builtin_amdgcn_raw_buffer_store_b32(
-                  __builtin_bit_cast(int, w * (acc[mi][f][r] * 1.f)), ry, yo + 64u * f, 0, 0);
+            for (int f = 0; f < NBIX; ++f) {
+              const float v = w * (acc[mi][f][r] * 1.f);
+              if constexpr (Y16)
+                __builtin_amdgcn_raw_buffer_store_b16(
+                    __builtin_bit_cast(short, (half_t)v), ry, yo + 32u * f, 0, 0);
+              else
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, v), ry,
+                                                      yo + 64u * f, 0, 0);
+            }
           }
       }
 #pragma unroll
@@ -786,7 +795,12 @@ __device__ __forceinline__ void expert_lds_tile(const ExpertParams& p, char* lds
 #pragma unroll
         for (int f = 0; f < NBIX; ++f) {
           const int n = n0 + 16 * f + j;
-          if (n < N) ((float*)p.out)[(size_t)row * p.ldo + n] = w * (acc[mi][f][r] * sd[f]);
+          if (n >= N) continue;
+          const float v = w * (acc[mi][f][r] * sd[f]);
+          if constexpr (Y16)
+            ((half_t*)p.out)[(size_t)row * p.ldo + n] = (half_t)v;
+          else
+            ((float*)p.out)[(size_t)row * p.ldo + n] = v;
         }
       }
   }
@@ -832,7 +846,7 @@ static int lds_slab_chain(bool gu, int wdt, int nw, const ExpertParams& p, int m
 
 // CH > 1: each block runs up to CH consecutive column slabs of its m-tile in turn
 // (expert_lds_tile's slab chain); nblk counts the slabs, the grid the chains.
-template <int WF, bool GU, int NW, int CH = 1>
+template <int WF, bool GU, int NW, int CH = 1, bool Y16 = false>
 __global__ __launch_bounds__((64 * NW), (LdsShape<WF>::OCC * 4 / NW)) void k_expert_lds(
     const ExpertParams p, int mt_max, int nslab) {
   constexpr int KS = 4 * WTr<WF>::EPL * LdsShape<WF>::KM;
@@ -886,17 +900,18 @@ __global__ __launch_bounds__((64 * NW), (LdsShape<WF>::OCC * 4 / NW)) void k_exp
     const int items = min(CH, nslab - nb * CH);
     if ((int)threadIdx.x < trows) wrow[threadIdx.x] = p.sorted_w[p.g_start[g] + row0 + threadIdx.x];
     if (MX_LDS_NT_SINGLE && p.g_count[g] <= MB)
-      expert_lds_tile<WF, GU, 8, NBI, NW, true, CH>(p, lds, g, row0, trows, n0b, items, wrow);
+      expert_lds_tile<WF, GU, 8, NBI, NW, true, CH, Y16>(p, lds, g, row0, trows, n0b, items,
+                                                         wrow);
     else
-      expert_lds_tile<WF, GU, 8, NBI, NW, MX_LDS_NT_DN, CH>(p, lds, g, row0, trows, n0b, items,
-                                                             wrow);
+      expert_lds_tile<WF, GU, 8, NBI, NW, MX_LDS_NT_DN, CH, Y16>(p, lds, g, row0, trows, n0b,
+                                                                  items, wrow);
     return;
   }
   if (MX_LDS_NT_SINGLE && p.g_count[g] <= MB)
-    expert_lds_tile<WF, GU, 8, NBI, NW, true>(p, lds, g, row0, trows, n0b);
+    expert_lds_tile<WF, GU, 8, NBI, NW, true, 1, Y16>(p, lds, g, row0, trows, n0b);
   else
-    expert_lds_tile<WF, GU, 8, NBI, NW, GU ? MX_LDS_NT_GU : MX_LDS_NT_DN>(p, lds, g, row0, trows,
-                                                                          n0b);
+    expert_lds_tile<WF, GU, 8, NBI, NW, GU ? MX_LDS_NT_GU : MX_LDS_NT_DN, 1, Y16>(
+        p, lds, g, row0, trows, n0b);
 }
 
 // ------------------------------------------------------------------------------------
@@ -1039,38 +1054,46 @@ static int dispatch_expert(int wdt, int mt, const ExpertParams& p, int mt_max, i
 
 // Direct-load kernel for m_blk 16/32/64; LDS-staged kernel for m_blk 128 (fp16/int8).
 // mt_max bounds the m-tile list (the kernels read the actual count from p.n_mtiles).
+template <bool GU, bool Y16>
+static int launch_lds(int wdt, const ExpertParams& p, int mt_max, int nmax, hipStream_t s) {
+  const int nw = lds_eight_waves(wdt, p.K_r) ? 8 : 4;
+  const int cols = nw * 16 * (GU ? 2 : 4);
+  const int nblk = mx_ceil_div(nmax, cols);
+  const int ch = lds_slab_chain(GU, wdt, nw, p, mt_max);
+  const long blocks = ((long)mt_max * mx_ceil_div(nblk, ch) + 7) / 8 * 8;
+  if (blocks > (1l << 31) - 1) return MX_ERR_UNSUPPORTED;
+  mx_clear_error();
+  if (!GU && ch == 2 && nw == 8 && MX_LDS_CHAIN8)
+    hipLaunchKernelGGL((k_expert_lds<MX_DT_F16, false, 8, 2, Y16>), dim3((unsigned)blocks),
+                       dim3(512), 0, s, p, mt_max, nblk);
+  else if (!GU && ch == 2)
+    hipLaunchKernelGGL((k_expert_lds<MX_DT_F16, false, 4, 2, Y16>), dim3((unsigned)blocks),
+                       dim3(256), 0, s, p, mt_max, nblk);
+  else if (!GU && ch == 4)
+    hipLaunchKernelGGL((k_expert_lds<MX_DT_F16, false, 4, 4, Y16>), dim3((unsigned)blocks),
+                       dim3(256), 0, s, p, mt_max, nblk);
+  else if (wdt == MX_DT_F16 && nw == 8)
+    hipLaunchKernelGGL((k_expert_lds<MX_DT_F16, GU, 8, 1, Y16>), dim3((unsigned)blocks),
+                       dim3(512), 0, s, p, mt_max, nblk);
+  else if (wdt == MX_DT_F16)
+    hipLaunchKernelGGL((k_expert_lds<MX_DT_F16, GU, 4, 1, Y16>), dim3((unsigned)blocks),
+                       dim3(256), 0, s, p, mt_max, nblk);
+  else
+    hipLaunchKernelGGL((k_expert_lds<MX_DT_I8, GU, 4, 1, Y16>), dim3((unsigned)blocks),
+                       dim3(256), 0, s, p, mt_max, nblk);
+  return mx_launch_status();
+}
+
 template <bool GU>
 static int launch_grouped_mt(int wdt, const ExpertParams& p, int mt_max, int m_blk, int nmax,
                              hipStream_t s) {
   if (m_blk == 128) {
     if (wdt == MX_DT_F32) return MX_ERR_INVALID;
-    const int nw = lds_eight_waves(wdt, p.K_r) ? 8 : 4;
-    const int cols = nw * 16 * (GU ? 2 : 4);
-    const int nblk = mx_ceil_div(nmax, cols);
-    const int ch = lds_slab_chain(GU, wdt, nw, p, mt_max);
-    const long blocks = ((long)mt_max * mx_ceil_div(nblk, ch) + 7) / 8 * 8;
-    if (blocks > (1l << 31) - 1) return MX_ERR_UNSUPPORTED;
-    mx_clear_error();
-    if (!GU && ch == 2 && nw == 8 && MX_LDS_CHAIN8)
-      hipLaunchKernelGGL((k_expert_lds<MX_DT_F16, false, 8, 2>), dim3((unsigned)blocks),
-                         dim3(512), 0, s, p, mt_max, nblk);
-    else if (!GU && ch == 2)
-      hipLaunchKernelGGL((k_expert_lds<MX_DT_F16, false, 4, 2>), dim3((unsigned)blocks),
-                         dim3(256), 0, s, p, mt_max, nblk);
-    else if (!GU && ch == 4)
-      hipLaunchKernelGGL((k_expert_lds<MX_DT_F16, false, 4, 4>), dim3((unsigned)blocks),
-                         dim3(256), 0, s, p, mt_max, nblk);
-    else if (wdt == MX_DT_F16 && nw == 8)
-      hipLaunchKernelGGL((k_expert_lds<MX_DT_F16, GU, 8>), dim3((unsigned)blocks), dim3(512), 0,
-                         s, p, mt_max, nblk);
-    else if (wdt == MX_DT_F16)
-      hipLaunchKernelGGL((k_expert_lds<MX_DT_F16, GU, 4>), dim3((unsigned)blocks), dim3(256), 0,
-                         s, p, mt_max, nblk);
-    else
-      hipLaunchKernelGGL((k_expert_lds<MX_DT_I8, GU, 4>), dim3((unsigned)blocks), dim3(256), 0,
-                         s, p, mt_max, nblk);
-    return mx_launch_status();
+    if constexpr (!GU)
+      if (p.y16) return launch_lds<false, true>(wdt, p, mt_max, nmax, s);
+    return launch_lds<GU, false>(wdt, p, mt_max, nmax, s);
   }
+  if (p.y16) return MX_ERR_INVALID;  // fp16 y rows come from the prefill kernel only
   if (m_blk != 16 && m_blk != 32 && m_blk != 64) return MX_ERR_INVALID;
   return dispatch_expert<GU>(wdt, m_blk / 16, p, mt_max, nmax, s);
 }
@@ -1211,7 +1234,17 @@ extern "C" int mx_expert_down(const MxMoeDesc* desc, const MxExpertPtrs* experts
                               const int32_t* g_start, const int32_t* g_count,
                               const int32_t* mt_group, const int32_t* mt_row0,
                               const int32_t* n_mtiles, int32_t m_blk, float* y, void* stream) {
+  return mx_expert_down_rows(desc, experts, tokens, act, sorted_w, g_expert, g_start, g_count,
+                             mt_group, mt_row0, n_mtiles, m_blk, y, false, (hipStream_t)stream);
+}
+
+int mx_expert_down_rows(const MxMoeDesc* desc, const MxExpertPtrs* experts, int tokens,
+                        const void* act, const float* sorted_w, const int* g_expert,
+                        const int* g_start, const int* g_count, const int* mt_group,
+                        const int* mt_row0, const int* n_mtiles, int m_blk, void* y, bool y16,
+                        hipStream_t stream) {
   MX_TRY(expert_check(desc));
+  if (y16 && m_blk != 128) return MX_ERR_INVALID;
   if (!experts || !act || !sorted_w || !g_expert || !g_start || !g_count || !mt_group ||
       !mt_row0 || !n_mtiles || !y || tokens < 0)
     return MX_ERR_INVALID;
@@ -1245,7 +1278,8 @@ extern "C" int mx_expert_down(const MxMoeDesc* desc, const MxExpertPtrs* experts
   p.N_s = desc->hidden;
   p.K_s = desc->shared_inter;
   p.tiled = desc->weight_layout == MX_LAYOUT_FRAG16;
-  return launch_grouped<false>(desc, p, tokens, m_blk, desc->hidden, (hipStream_t)stream);
+  p.y16 = y16;
+  return launch_grouped<false>(desc, p, tokens, m_blk, desc->hidden, stream);
 }
 
 // ------------------------------------------------------------------------------------

@@ -94,6 +94,15 @@ struct MxOneTokenSelect {
   int* mt_row0;
   int* n_mtiles;
 };
+// mx_expert_down with the y rows as fp16 when y16 (the prefill kernel, m_blk 128, only; the
+// combine then reads them with mx_combine_rows(..., y16 = true)).
+int mx_expert_down_rows(const MxMoeDesc* desc, const MxExpertPtrs* experts, int tokens,
+                        const void* act, const float* sorted_w, const int* g_expert,
+                        const int* g_start, const int* g_count, const int* mt_group,
+                        const int* mt_row0, const int* n_mtiles, int m_blk, void* y, bool y16,
+                        hipStream_t stream);
+int mx_combine_rows(const float* x, const void* y, const int32_t* pair_pos, int tokens,
+                    int hidden, int top_k, int has_shared, float* out, bool y16, hipStream_t s);
 bool mx_one_token_select_ok(const MxMoeDesc* d);
 int mx_expert_gate_up_select(const MxMoeDesc* desc, const MxExpertPtrs* experts, const void* a,
                              void* act, const MxOneTokenSelect& sp, hipStream_t s);

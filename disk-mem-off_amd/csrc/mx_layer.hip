@@ -47,6 +47,14 @@ int check_desc(const MxMoeDesc* d) {
   return MX_OK;
 }
 
+// Prefill batches (128-row m-tiles, fp16 / int8 experts) keep the y rows between the down
+// and combine launches as fp16: half the bytes of that round trip (written once, read once),
+// for one more rounding of each weighted expert row (2^-11 relative) before the fp32 sum.
+#ifndef MX_Y_ROWS_FP16
+#define MX_Y_ROWS_FP16 1
+#endif
+bool y_rows_fp16(const MxMoeViews& v) { return MX_Y_ROWS_FP16 && v.m_blk == 128; }
+
 // Decode-sized batches run the decode router (RMSNorm + logits, then top-k + dispatch in
 // one workgroup) in place of stages 0-3.
 bool use_decode_router(const MxMoeDesc* d, const MxMoeWeights* w, int T, const float* x) {
@@ -101,7 +109,7 @@ int layout(const MxMoeDesc* d, int T, void* ws, MxMoeViews* v, size_t* total,
   t.n_mtiles = (int32_t*)c.take(4);
   t.m_blk = m_blk;
   t.act = c.take(R * imax * aesz);
-  t.y = (float*)c.take(R * H * 4);
+  t.y = c.take(R * H * 4);  // fp32 rows (fp16 rows use the first half)
   size_t dscr = 0;
   MX_TRY(mx_dispatch_scratch_size(Tn, d->top_k, d->n_experts, &dscr));
   void* dispatch_scratch = c.take(dscr);
@@ -215,10 +223,13 @@ int run_stage(int stage, const MxMoeDesc* d, const MxMoeWeights* w, const float*
                                v.sorted_tok, v.g_expert, v.g_start, v.g_count, v.mt_group,
                                v.mt_row0, v.n_mtiles, v.m_blk, v.act, s);
     case 5:
-      return mx_expert_down(d, w->experts, T, v.act, v.sorted_w, v.g_expert, v.g_start, v.g_count,
-                            v.mt_group, v.mt_row0, v.n_mtiles, v.m_blk, v.y, s);
+      return mx_expert_down_rows(d, w->experts, T, v.act, v.sorted_w, v.g_expert, v.g_start,
+                                 v.g_count, v.mt_group, v.mt_row0, v.n_mtiles, v.m_blk, v.y,
+                                 y_rows_fp16(v), s);
     case 6:
-      return mx_combine(x, v.y, v.pair_pos, T, d->hidden, d->top_k, has_sh, out, s);
+      if (!x || !out) return MX_ERR_INVALID;
+      return mx_combine_rows(x, v.y, v.pair_pos, T, d->hidden, d->top_k, has_sh, out,
+                             y_rows_fp16(v), s);
     default:
       return MX_ERR_INVALID;
   }

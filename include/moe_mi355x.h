@@ -134,7 +134,8 @@ typedef struct MxMoeViews {
   int32_t* n_mtiles;   /* [1]                                                           */
   int32_t m_blk;       /* rows per m-tile                                               */
   void* act;           /* [T k + T, max(I, I_s)] silu(gate) * up                        */
-  float* y;            /* [T k + T, H] weighted expert outputs                          */
+  void* y;             /* [T k + T, H] weighted expert outputs: fp32, or fp16 when      */
+                       /* m_blk is 128 (fp16 / int8 experts, T >= 65)                   */
 } MxMoeViews;
 
 /* Static description of the device. */
