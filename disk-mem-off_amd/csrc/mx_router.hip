@@ -12,9 +12,8 @@
 
 // ------------------------------------------------------------------------------------
 // RMSNorm: one 256-thread block per token.  h = w * (x / sqrt(mean(x^2) + eps)).
-// Vector form: each thread keeps its float4 slices of the row in registers (H <= 256 * 4 *
-// RN_V), so all loads of a row are in flight together, with the norm weights' (and gate
-// row's) slices requested before the reduction.  (One wave per token, four tokens per
+// VEC: each thread keeps its float4 slices of the row in registers (H <= 256 * 4 * RN_V),
+// so all loads of a row are in flight together.  (One wave per token, four tokens per
 // block, measured slower for Qwen3-Next's H = 2048: 28 -> 32 us at 4096 tokens.)  Outputs:
 // h32 (fp32; left out when null), h16 = fp16(h) and,
 // for the split-plane router GEMM, h16lo = fp16((h - h16) * 2^11) (h - h16 is exact in
@@ -41,30 +40,13 @@ __device__ __forceinline__ void gate_logit_store(const MxRouterSplitW& rs, int t
   }
 }
 
-// Four parameters (fp32 or fp16 storage) as fp32: one vector load when `vec` (the caller
-// checked the alignment), else four element loads.
-__device__ __forceinline__ float4 load_param4(const void* p, int dtype, int i, bool vec) {
-  if (vec) {
-    if (dtype == MX_DT_F16) {
-      typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-      const h4 h = *(const h4*)((const half_t*)p + i);
-      return make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
-    }
-    return *(const float4*)((const float*)p + i);
-  }
-  return make_float4(mx_load_param(p, dtype, i), mx_load_param(p, dtype, i + 1),
-                     mx_load_param(p, dtype, i + 2), mx_load_param(p, dtype, i + 3));
-}
-
-// NV: float4 slices of the row per thread (H <= 256 * 4 * NV); 0: the element-wise form.
-// pvec: the norm weights (and the shared-gate row) can be read as 4-element vectors.
-template <int NV>
+template <bool VEC>
 __global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x,
                                                  const void* __restrict__ w, int wdt,
                                                  float eps, int H, float* __restrict__ h32,
                                                  half_t* __restrict__ h16,
                                                  half_t* __restrict__ h16lo, int nsplit,
-                                                 MxRouterSplitW rs, int pvec) {
+                                                 MxRouterSplitW rs) {
   if ((int)blockIdx.x < nsplit) {  // 1024 elements of one router row's planes
     const int pieces = (H + 1023) >> 10;
     const int e = blockIdx.x / pieces;
@@ -96,22 +78,16 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x,
   half_t* hr16 = h16 ? h16 + (size_t)t * H : nullptr;
   half_t* hrlo = h16lo ? h16lo + (size_t)t * H : nullptr;
   __shared__ float red[4];
-  if constexpr (NV > 0) {
-    // The row, the norm weights and the gate row are all requested before the reduction,
-    // so the block waits for memory once.
-    float4 v[NV], wv[NV], gv[NV];
+  if constexpr (VEC) {
+    float4 v[RN_V];
     float ss = 0.f;
-    const bool gate = rs.gate_out != nullptr;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
+    for (int i = 0; i < RN_V; ++i) {
       const int c = (threadIdx.x + 256 * i) * 4;
-      const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-      v[i] = c < H ? *(const float4*)(xr + c) : z;
-      wv[i] = c < H ? load_param4(w, wdt, c, pvec) : z;
-      gv[i] = gate && c < H ? load_param4(rs.wsg, rs.pdt, c, pvec) : z;
+      v[i] = c < H ? *(const float4*)(xr + c) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
+    for (int i = 0; i < RN_V; ++i) {
       ss = fmaf(v[i].x, v[i].x, ss);
       ss = fmaf(v[i].y, v[i].y, ss);
       ss = fmaf(v[i].z, v[i].z, ss);
@@ -124,20 +100,20 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x,
     const float rms = sqrtf(ss / (float)H + eps);
     float gdot = 0.f;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
+    for (int i = 0; i < RN_V; ++i) {
       const int c = (threadIdx.x + 256 * i) * 4;
       if (c < H) {
         float4 o;
-        o.x = wv[i].x * (v[i].x / rms);
-        o.y = wv[i].y * (v[i].y / rms);
-        o.z = wv[i].z * (v[i].z / rms);
-        o.w = wv[i].w * (v[i].w / rms);
+        o.x = mx_load_param(w, wdt, c + 0) * (v[i].x / rms);
+        o.y = mx_load_param(w, wdt, c + 1) * (v[i].y / rms);
+        o.z = mx_load_param(w, wdt, c + 2) * (v[i].z / rms);
+        o.w = mx_load_param(w, wdt, c + 3) * (v[i].w / rms);
         if (hr) *(float4*)(hr + c) = o;
-        if (gate) {
-          gdot = fmaf(o.x, gv[i].x, gdot);
-          gdot = fmaf(o.y, gv[i].y, gdot);
-          gdot = fmaf(o.z, gv[i].z, gdot);
-          gdot = fmaf(o.w, gv[i].w, gdot);
+        if (rs.gate_out) {
+          gdot = fmaf(o.x, mx_load_param(rs.wsg, rs.pdt, c + 0), gdot);
+          gdot = fmaf(o.y, mx_load_param(rs.wsg, rs.pdt, c + 1), gdot);
+          gdot = fmaf(o.z, mx_load_param(rs.wsg, rs.pdt, c + 2), gdot);
+          gdot = fmaf(o.w, mx_load_param(rs.wsg, rs.pdt, c + 3), gdot);
         }
         if (hr16) {
           typedef _Float16 h4 __attribute__((ext_vector_type(4)));
@@ -194,20 +170,13 @@ int mx_rmsnorm_launch(const float* x, const void* norm_w, int param_dtype, float
   const bool vec = hidden % 4 == 0 && hidden <= 256 * 4 * RN_V && mx_aligned16(x) &&
                    (!h32 || mx_aligned16(h32)) && (!h16 || ((uintptr_t)h16 & 7u) == 0) &&
                    (!h16lo || ((uintptr_t)h16lo & 7u) == 0);
-  const uintptr_t pal = param_dtype == MX_DT_F16 ? 7u : 15u;
-  const uintptr_t gal = rs.pdt == MX_DT_F16 ? 7u : 15u;
-  const int pvec = !((uintptr_t)norm_w & pal) && !(rs.gate_out && ((uintptr_t)rs.wsg & gal));
-  const int nv = hidden <= 256 * 4 * 2 ? 2 : (hidden <= 256 * 4 * 4 ? 4 : (hidden <= 256 * 4 * 6 ? 6 : 8));
   mx_clear_error();
-#define RN_LAUNCH(NV_)                                                                       \
-  hipLaunchKernelGGL(k_rmsnorm<NV_>, dim3(grid), dim3(256), 0, s, x, norm_w, param_dtype, eps, \
-                     hidden, h32, (half_t*)h16, (half_t*)h16lo, nsplit, rs, pvec)
-  if (!vec) RN_LAUNCH(0);
-  else if (nv == 2) RN_LAUNCH(2);
-  else if (nv == 4) RN_LAUNCH(4);
-  else if (nv == 6) RN_LAUNCH(6);
-  else RN_LAUNCH(8);
-#undef RN_LAUNCH
+  if (vec)
+    hipLaunchKernelGGL(k_rmsnorm<true>, dim3(grid), dim3(256), 0, s, x, norm_w, param_dtype, eps,
+                       hidden, h32, (half_t*)h16, (half_t*)h16lo, nsplit, rs);
+  else
+    hipLaunchKernelGGL(k_rmsnorm<false>, dim3(grid), dim3(256), 0, s, x, norm_w, param_dtype,
+                       eps, hidden, h32, (half_t*)h16, (half_t*)h16lo, nsplit, rs);
   return mx_launch_status();
 }
 
