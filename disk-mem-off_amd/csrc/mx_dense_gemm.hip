@@ -54,6 +54,7 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
 struct GemmSeg {
   const void* w;  // [N, K]
   const void* w_lo;  // SPLIT: the low plane of w
+  const float* res;  // residual added by the epilogue (same layout as y) or null
   float* y;       // [M, ldy] for slice 0; slice z at y + z * yslice
   int n;          // N of the segment
   int ldy;
@@ -327,23 +328,28 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, OCC) void k_gemm_nt(
   }
 
   // Epilogue: fp32 rows of the segment's output, 4 consecutive columns per lane (a
-  // 16-byte store when the row stride and the base allow it).
+  // 16-byte store when the row stride and the base allow it), plus the residual when the
+  // segment has one (read and written by the same lane, so it may alias the output).
   float* const ybase = sg.y + (size_t)blockIdx.y * p.yslice;
-  const bool vec = (sg.ldy & 3) == 0 && ((uintptr_t)ybase & 15) == 0;
+  const bool vec = (sg.ldy & 3) == 0 && ((uintptr_t)ybase & 15) == 0 &&
+                   ((uintptr_t)sg.res & 15) == 0;
 #pragma unroll
   for (int mi = 0; mi < MF; ++mi) {
     const int m = m0 + wm * WM + mi * 16 + j;
     if (m >= M) continue;
     float* yrow = ybase + (size_t)m * sg.ldy;
+    const float* rrow = sg.res ? sg.res + (size_t)m * sg.ldy : nullptr;
 #pragma unroll
     for (int ni = 0; ni < NF; ++ni) {
       const int n = n0 + wn * WN + ni * 16 + 4 * q;
       if (vec && n + 3 < N) {
-        *(float4_t*)(yrow + n) = acc[mi][ni];
+        float4_t v = acc[mi][ni];
+        if (rrow) v += *(const float4_t*)(rrow + n);
+        *(float4_t*)(yrow + n) = v;
       } else {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          if (n + r < N) yrow[n + r] = acc[mi][ni][r];
+          if (n + r < N) yrow[n + r] = rrow ? rrow[n + r] + acc[mi][ni][r] : acc[mi][ni][r];
       }
     }
   }
@@ -385,10 +391,12 @@ int prepare(GemmArgs& args, const void* a, int M, int K, int es, const MxGemmSeg
   for (int i = 0; i < nseg; ++i) {
     const MxGemmSeg& g = segs[i];
     if (!g.w || !g.y || g.n <= 0 || g.ldy < g.n) return MX_ERR_INVALID;
+    if (g.res && kslice != K) return MX_ERR_INVALID;  // a residual needs the whole reduction
     if (!mx_aligned16(g.w)) return MX_ERR_ALIGNMENT;
     if ((long)g.n * K * es >= (1l << 31)) return MX_ERR_UNSUPPORTED;
     args.seg[i].w = g.w;
     args.seg[i].w_lo = g.w_lo;
+    args.seg[i].res = g.res;
     args.seg[i].y = g.y;
     args.seg[i].n = g.n;
     args.seg[i].ldy = g.ldy;

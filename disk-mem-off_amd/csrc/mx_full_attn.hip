@@ -102,62 +102,74 @@ int layout(const MxFullAttnDesc* d, int T, void* ws, FaWork* w, size_t* total) {
 }
 
 // ------------------------------------------------------------------------------------
-// qk-norm + RoPE, in place on the q half of the q projection and on k.  One wave per
-// (token, head row); lane handles dims i = lane + 64 j.  y = (x / rms(x)) * w when the
-// norm weight is given (rms_norm_no_weight then the weight, _common.py:137-140), then on
-// the first rotary_dim dims the rotate-half RoPE of _common.py:105-127: with half =
-// rotary_dim / 2, freq_j = 1 / theta^(j / half) (fp64), angle = fp32(t * freq_j),
-// out_i = y_i cos - y_{i+half} sin (i < half), y_i cos + y_{i-half} sin (half <= i < rd).
-// Each lane recomputes its partner's normalised value from memory (same rms), so there is
-// no cross-lane exchange; all loads precede the reduction, all stores follow it.
-// ------------------------------------------------------------------------------------
+// qk-norm + RoPE, in place on the q half of the q projection and on k.  One block per
+// token; its 4 waves take the token's head rows in turn, lane handling dims i = lane + 64 j.
+// y = (x / rms(x)) * w when the norm weight is given (rms_norm_no_weight then the weight,
+// _common.py:137-140), then on the first rotary_dim dims the rotate-half RoPE of
+// _common.py:105-127: with half = rotary_dim / 2, freq_j = 1 / theta^(j / half) (fp64),
+// angle = fp32(t * freq_j), out_i = y_i cos - y_{i+half} sin (i < half), y_i cos +
+// y_{i-half} sin (half <= i < rd).  The token's cos / sin table (the same for every head)
+// is computed once into LDS, so the fp64 power and the fp32 cos / sin run once per
+// (token, frequency), not once per (token, head, dim).  Each lane recomputes its partner's
+// normalised value from memory (same rms), so there is no cross-lane exchange; all loads of
+// a row precede its reduction, all its stores follow it.
 template <int EPT>
-__global__ __launch_bounds__(64) void k_fa_rope(float* __restrict__ qg, float* __restrict__ kk,
-                                                const void* __restrict__ qn_w,
-                                                const void* __restrict__ kn_w, int pdt,
-                                                FaDims m, double theta, float eps) {
+__global__ __launch_bounds__(256) void k_fa_rope_tok(float* __restrict__ qg,
+                                                     float* __restrict__ kk,
+                                                     const void* __restrict__ qn_w,
+                                                     const void* __restrict__ kn_w, int pdt,
+                                                     FaDims m, double theta, float eps) {
 #pragma clang fp contract(off)
-  const int t = blockIdx.x, slot = blockIdx.y, lane = threadIdx.x;
-  const bool isq = slot < m.nh;
-  float* row = isq ? qg + (size_t)t * m.qw + (size_t)slot * m.hd
-                   : kk + (size_t)t * m.kw + (size_t)(slot - m.nh) * m.hd;
-  const void* nw = isq ? qn_w : kn_w;
+  __shared__ float cs[128], sn[128];  // rotary_dim / 2 <= head_dim / 2 <= 128
+  const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = m.rd / 2;
-  float x[EPT], xp[EPT], w[EPT], wp[EPT];
-#pragma unroll
-  for (int j = 0; j < EPT; ++j) {
-    const int i = lane + 64 * j;
-    const bool valid = i < m.hd;
-    const int ic = valid ? i : 0;
-    const int p = ic < m.rd ? (ic < half ? ic + half : ic - half) : ic;
-    x[j] = valid ? row[ic] : 0.f;
-    xp[j] = valid ? row[p] : 0.f;
-    w[j] = nw ? mx_load_param(nw, pdt, ic) : 1.f;
-    wp[j] = nw ? mx_load_param(nw, pdt, p) : 1.f;
+  if (tid < half) {
+    const double f = 1.0 / pow(theta, (double)tid / (double)half);
+    const float ang = (float)((double)t * f);
+    cs[tid] = cosf(ang);
+    sn[tid] = sinf(ang);
   }
-  float rms = 1.f;
-  if (nw) {
-    float ss = 0.f;
+  __syncthreads();
+  for (int slot = wave; slot < m.nh + m.nkv; slot += 4) {
+    const bool isq = slot < m.nh;
+    float* row = isq ? qg + (size_t)t * m.qw + (size_t)slot * m.hd
+                     : kk + (size_t)t * m.kw + (size_t)(slot - m.nh) * m.hd;
+    const void* nw = isq ? qn_w : kn_w;
+    float x[EPT], xp[EPT], w[EPT], wp[EPT];
 #pragma unroll
-    for (int j = 0; j < EPT; ++j) ss += x[j] * x[j];
-    ss = mx_wave_sum(ss);
-    rms = sqrtf(ss / (float)m.hd + eps);
-  }
-#pragma unroll
-  for (int j = 0; j < EPT; ++j) {
-    const int i = lane + 64 * j;
-    if (i >= m.hd) break;
-    const float y = nw ? (x[j] / rms) * w[j] : x[j];
-    float out = y;
-    if (i < m.rd) {
-      const float yp = nw ? (xp[j] / rms) * wp[j] : xp[j];
-      const int jj = i < half ? i : i - half;
-      const double f = 1.0 / pow(theta, (double)jj / (double)half);
-      const float ang = (float)((double)t * f);
-      const float c = cosf(ang), s = sinf(ang);
-      out = i < half ? y * c - yp * s : y * c + yp * s;
+    for (int j = 0; j < EPT; ++j) {
+      const int i = lane + 64 * j;
+      const bool valid = i < m.hd;
+      const int ic = valid ? i : 0;
+      const int p = ic < m.rd ? (ic < half ? ic + half : ic - half) : ic;
+      x[j] = valid ? row[ic] : 0.f;
+      xp[j] = valid ? row[p] : 0.f;
+      w[j] = nw ? mx_load_param(nw, pdt, ic) : 1.f;
+      wp[j] = nw ? mx_load_param(nw, pdt, p) : 1.f;
     }
-    row[i] = out;
+    float rms = 1.f;
+    if (nw) {
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < EPT; ++j) ss += x[j] * x[j];
+      ss = mx_wave_sum(ss);
+      rms = sqrtf(ss / (float)m.hd + eps);
+    }
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+      const int i = lane + 64 * j;
+      if (i >= m.hd) break;
+      const float y = nw ? (x[j] / rms) * w[j] : x[j];
+      float out = y;
+      if (i < m.rd) {
+        const float yp = nw ? (xp[j] / rms) * wp[j] : xp[j];
+        const int jj = i < half ? i : i - half;
+        const float c = cs[jj], sv = sn[jj];
+        out = i < half ? y * c - yp * sv : y * c + yp * sv;
+      }
+      row[i] = out;
+    }
   }
 }
 
@@ -661,24 +673,30 @@ int run_stage(int st, const MxFullAttnDesc* d, const MxFullAttnWeights* w, const
       if (mx_dense_on_gemm(wdt, T, m.H)) return MX_OK;
       return mx_project(k.dw, 2, wdt, w->v_w, T, m.kw, m.H, h, k.v.v, s);
     case 4: {
-      const dim3 grid(T, m.nh + m.nkv);
+      const dim3 grid(T);
       mx_clear_error();
       if (m.hd <= 64)
-        hipLaunchKernelGGL(k_fa_rope<1>, grid, dim3(64), 0, s, k.v.qg, k.v.k, w->q_norm_w,
+        hipLaunchKernelGGL(k_fa_rope_tok<1>, grid, dim3(256), 0, s, k.v.qg, k.v.k, w->q_norm_w,
                            w->k_norm_w, d->param_dtype, m, d->rope_theta, d->eps);
       else if (m.hd <= 128)
-        hipLaunchKernelGGL(k_fa_rope<2>, grid, dim3(64), 0, s, k.v.qg, k.v.k, w->q_norm_w,
+        hipLaunchKernelGGL(k_fa_rope_tok<2>, grid, dim3(256), 0, s, k.v.qg, k.v.k, w->q_norm_w,
                            w->k_norm_w, d->param_dtype, m, d->rope_theta, d->eps);
       else
-        hipLaunchKernelGGL(k_fa_rope<4>, grid, dim3(64), 0, s, k.v.qg, k.v.k, w->q_norm_w,
+        hipLaunchKernelGGL(k_fa_rope_tok<4>, grid, dim3(256), 0, s, k.v.qg, k.v.k, w->q_norm_w,
                            w->k_norm_w, d->param_dtype, m, d->rope_theta, d->eps);
       return mx_launch_status();
     }
     case 5:
       return attn_launch(k.v.qg, k.v.k, k.v.v, m, T, k.v.act, !f32, k.k16, k.v16t, s);
     case 6:
+      if (mx_dense_on_gemm(wdt, T, m.od)) {  // out = x + act W_o^T in the GEMM epilogue
+        if (!x || !out) return MX_ERR_INVALID;
+        const MxGemmSeg g{w->o_w, out, m.H, m.H, nullptr, x};
+        return mx_gemm_f16(k.v.act, T, m.od, &g, 1, s);
+      }
       return mx_project(k.dw, 3, wdt, w->o_w, T, m.H, m.od, k.v.act, k.v.y, s);
     case 7: {
+      if (mx_dense_on_gemm(wdt, T, m.od)) return MX_OK;  // added in stage 6
       const long n4 = (long)T * m.H / 4;
       mx_clear_error();
       hipLaunchKernelGGL(k_fa_residual, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, x,

@@ -133,6 +133,7 @@ struct MxGemmSeg {
   int n;
   int ldy;
   const void* w_lo = nullptr;  // mx_gemm_f16x2_slices: the low fp16 plane of w
+  const float* res = nullptr;  // mx_gemm_f16: y = res + a W^T (res [M, ldy], may alias y)
 };
 // fp16 a and W.
 int mx_gemm_f16(const void* a, int M, int K, const MxGemmSeg* segs, int nseg, hipStream_t s);

@@ -691,8 +691,14 @@ int run_stage(int st, const MxLinearAttnDesc* d, const MxLinearAttnWeights* w, c
                            f32 ? nullptr : (half_t*)k.v.act);
       return mx_launch_status();
     case 6:
+      if (mx_dense_on_gemm(wdt, T, m.vd)) {  // out = x + act W_out^T in the GEMM epilogue
+        if (!x || !out) return MX_ERR_INVALID;
+        const MxGemmSeg g{w->out_w, out, m.H, m.H, nullptr, x};
+        return mx_gemm_f16(k.v.act, T, m.vd, &g, 1, s);
+      }
       return mx_project(k.dw, 2, wdt, w->out_w, T, m.H, m.vd, k.v.act, k.v.y, s);
     case 7: {
+      if (mx_dense_on_gemm(wdt, T, m.vd)) return MX_OK;  // added in stage 6
       const long n4 = (long)T * m.H / 4;
       mx_clear_error();
       hipLaunchKernelGGL(k_la_residual, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, x,
