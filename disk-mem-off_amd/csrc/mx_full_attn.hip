@@ -102,15 +102,17 @@ int layout(const MxFullAttnDesc* d, int T, void* ws, FaWork* w, size_t* total) {
 }
 
 // ------------------------------------------------------------------------------------
-// qk-norm + RoPE, in place on the q half of the q projection and on k.  One block per
-// token; its 4 waves take the token's head rows in turn, lane handling dims i = lane + 64 j.
+// qk-norm + RoPE, in place on the q half of the q projection and on k.  A block per
+// (token, rpb head rows), its 4 waves taking the rows in turn, lane handling dims i = lane +
+// 64 j (rpb = all the token's rows for long inputs, 4 for short ones, whose few blocks would
+// otherwise run the rows of a token one after another).
 // y = (x / rms(x)) * w when the norm weight is given (rms_norm_no_weight then the weight,
 // _common.py:137-140), then on the first rotary_dim dims the rotate-half RoPE of
 // _common.py:105-127: with half = rotary_dim / 2, freq_j = 1 / theta^(j / half) (fp64),
 // angle = fp32(t * freq_j), out_i = y_i cos - y_{i+half} sin (i < half), y_i cos +
 // y_{i-half} sin (half <= i < rd).  The token's cos / sin table (the same for every head)
-// is computed once into LDS, so the fp64 power and the fp32 cos / sin run once per
-// (token, frequency), not once per (token, head, dim).  Each lane recomputes its partner's
+// is computed once per block into LDS, so the fp64 power and the fp32 cos / sin run once
+// per (block, frequency), not once per (token, head, dim).  Each lane recomputes its partner's
 // normalised value from memory (same rms), so there is no cross-lane exchange; all loads of
 // a row precede its reduction, all its stores follow it.
 template <int EPT>
@@ -118,7 +120,8 @@ __global__ __launch_bounds__(256) void k_fa_rope_tok(float* __restrict__ qg,
                                                      float* __restrict__ kk,
                                                      const void* __restrict__ qn_w,
                                                      const void* __restrict__ kn_w, int pdt,
-                                                     FaDims m, double theta, float eps) {
+                                                     FaDims m, double theta, float eps,
+                                                     int rpb) {
 #pragma clang fp contract(off)
   __shared__ float cs[128], sn[128];  // rotary_dim / 2 <= head_dim / 2 <= 128
   const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
@@ -131,7 +134,8 @@ __global__ __launch_bounds__(256) void k_fa_rope_tok(float* __restrict__ qg,
     sn[tid] = sinf(ang);
   }
   __syncthreads();
-  for (int slot = wave; slot < m.nh + m.nkv; slot += 4) {
+  const int slot_end = min(m.nh + m.nkv, (int)(blockIdx.y + 1) * rpb);
+  for (int slot = blockIdx.y * rpb + wave; slot < slot_end; slot += 4) {
     const bool isq = slot < m.nh;
     float* row = isq ? qg + (size_t)t * m.qw + (size_t)slot * m.hd
                      : kk + (size_t)t * m.kw + (size_t)(slot - m.nh) * m.hd;
@@ -673,17 +677,20 @@ int run_stage(int st, const MxFullAttnDesc* d, const MxFullAttnWeights* w, const
       if (mx_dense_on_gemm(wdt, T, m.H)) return MX_OK;
       return mx_project(k.dw, 2, wdt, w->v_w, T, m.kw, m.H, h, k.v.v, s);
     case 4: {
-      const dim3 grid(T);
+      // Long inputs: one block per token (4096 tokens: 34 us against 41 us with 4 rows per
+      // block); short ones: 4 rows per block (one token: 6.8 us against 11.7 us).
+      const int rows = m.nh + m.nkv, rpb = T >= 1024 ? rows : 4;
+      const dim3 grid(T, mx_ceil_div(rows, rpb));
       mx_clear_error();
       if (m.hd <= 64)
         hipLaunchKernelGGL(k_fa_rope_tok<1>, grid, dim3(256), 0, s, k.v.qg, k.v.k, w->q_norm_w,
-                           w->k_norm_w, d->param_dtype, m, d->rope_theta, d->eps);
+                           w->k_norm_w, d->param_dtype, m, d->rope_theta, d->eps, rpb);
       else if (m.hd <= 128)
         hipLaunchKernelGGL(k_fa_rope_tok<2>, grid, dim3(256), 0, s, k.v.qg, k.v.k, w->q_norm_w,
-                           w->k_norm_w, d->param_dtype, m, d->rope_theta, d->eps);
+                           w->k_norm_w, d->param_dtype, m, d->rope_theta, d->eps, rpb);
       else
         hipLaunchKernelGGL(k_fa_rope_tok<4>, grid, dim3(256), 0, s, k.v.qg, k.v.k, w->q_norm_w,
-                           w->k_norm_w, d->param_dtype, m, d->rope_theta, d->eps);
+                           w->k_norm_w, d->param_dtype, m, d->rope_theta, d->eps, rpb);
       return mx_launch_status();
     }
     case 5:
