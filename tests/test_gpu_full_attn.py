@@ -183,3 +183,34 @@ def test_in_place_and_argument_errors(mi355x, stream):
     finally:
         mi355x.free_device(xb)
         layer.close()
+
+
+def test_in_place_fp16_long_input(mi355x, stream):
+    """fp16 weights and more than 64 tokens: the residual rides in the o projection's GEMM
+    epilogue (out = x + act W_o^T), which must also hold in place (out aliasing x) and give
+    the out-of-place output bit for bit."""
+    s = syn.FullAttnShape(256, 4, 2, 64, 0.5, 10000.0, 1e-6)
+    t = syn.make_full_attn_tensors(s, 11, weight_dtype=np.float16)
+    T = 100
+    x = syn.make_inputs(12, T, s.hidden)
+    say(f"[gpu] full attention in place, fp16 weights, T={T}")
+    layer = _layer(mi355x, stream, s, t)
+    lib = _lib.load()
+    xb = mi355x.alloc_device(x.nbytes)
+    try:
+        mi355x.copy_h2d_ptr_async(xb.handle, x.ctypes.data, x.nbytes, stream)
+        desc, w = layer.desc(s.eps), layer.weights()
+        layer.runner.reserve(desc, T, io=False)
+        ws = layer.runner._ws
+        _lib.check(lib.mx_full_attn_forward(ctypes.byref(desc), ctypes.byref(w), xb.handle,
+                                            xb.handle, T, ws.handle, ws.nbytes, stream))
+        got = read_device(mi355x, xb.handle, np.float32, x.size, stream).reshape(x.shape)
+        sep = layer.forward_numpy(x, s.eps)
+    finally:
+        mi355x.free_device(xb)
+        layer.close()
+    assert np.array_equal(got, sep)
+    ref = fa.full_attn_block(x, t, spec_of(s))["out"]
+    mabs = float(np.max(np.abs(got - ref)))
+    say(f"    max abs err {mabs:.2e}")
+    assert mabs <= 2e-2

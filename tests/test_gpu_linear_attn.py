@@ -227,3 +227,33 @@ def test_in_place_and_argument_errors(mi355x, stream):
     finally:
         mi355x.free_device(xb)
         layer.close()
+
+
+def test_in_place_fp16_long_input(mi355x, stream):
+    """fp16 weights and more than 64 tokens: the residual rides in the out projection's GEMM
+    epilogue (out = x + act W_out^T), which must also hold in place (out aliasing x) and give
+    the out-of-place output bit for bit."""
+    shape = syn.LinearAttnShape(256, 4, 32, 32, 4, 1e-6)
+    t = syn.make_linear_attn_tensors(shape, 13, weight_dtype=np.float16)
+    T = 100
+    x = syn.make_inputs(14, T, shape.hidden)
+    say(f"[gpu] linear attention in place, fp16 weights, T={T}")
+    layer = DeviceLinearAttnLayer.from_host(mi355x, t, stream)
+    lib = _lib.load()
+    xb = upload(mi355x, stream, x)
+    try:
+        desc, w = layer.desc(shape.eps), layer.weights()
+        layer.runner.reserve(desc, T, io=False)
+        ws = layer.runner._ws
+        _lib.check(lib.mx_linear_attn_forward(ctypes.byref(desc), ctypes.byref(w), xb.handle,
+                                              xb.handle, T, ws.handle, ws.nbytes, stream))
+        got = read_device(mi355x, xb.handle, np.float32, x.size, stream).reshape(x.shape)
+        sep = layer.forward_numpy(x, shape.eps)
+    finally:
+        mi355x.free_device(xb)
+        layer.close()
+    assert np.array_equal(got, sep)
+    ref = la.linear_attn_block(x, t, spec_of(shape))["out"]
+    mabs = float(np.max(np.abs(got - ref)))
+    say(f"    max abs err {mabs:.2e}")
+    assert mabs <= 2e-2
