@@ -362,8 +362,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, FA_WPE))
 // row-major per key/value head, values transposed per 32-key tile with the keys of a
 // tile in k-slot order (below), so staging a tile is a straight 16-byte copy.
 //
-// k_fa_attn_h: block = NW waves, one query head, 16 NW queries (16 per wave); tiles of
-// 32 S32 keys, the next tile's 16-byte pieces loaded into registers while a tile computes.
+// k_fa_attn_h: block = NW waves, one query head, 16 QS NW queries (QS sets of 16 per
+// wave); tiles of 32 S32 keys, the next tile's 16-byte pieces loaded into registers while a
+// tile computes.
 // Each XCD runs whole heads, consecutive ones, so the heads of a key/value head read its
 // packed keys and values through one XCD's L2 (Qwen3-Next, 16 heads over 2 key/value
 // heads at 4096 tokens: 393 -> 250 us against blocks dealt round-robin over all heads).
@@ -411,7 +412,7 @@ __global__ __launch_bounds__(256) void k_fa_pack_kv(const float* __restrict__ kk
 #define FA_H_XCD 1  // XCD-aware head runs in k_fa_attn_h
 #endif
 
-template <int NC, int NW, int S32>
+template <int NC, int NW, int S32, int QS>
 __global__ __launch_bounds__(64 * NW) void k_fa_attn_h(const float* __restrict__ qg,
                                                        const half_t* __restrict__ k16,
                                                        const half_t* __restrict__ v16t,
@@ -424,11 +425,12 @@ __global__ __launch_bounds__(64 * NW) void k_fa_attn_h(const float* __restrict__
   constexpr int NT = 64 * NW;          // threads
   constexpr int KCH = KT * DP / 8;     // 16-byte pieces of a K tile (= of a V^T tile)
   constexpr int PPT = (KCH + NT - 1) / NT;  // pieces of each per thread
+  constexpr int WQ = 16 * QS;          // queries per wave (QS sets of 16)
   __shared__ __align__(16) half_t sk[KT * KR];
   __shared__ __align__(16) half_t svt[S32 * DP * VR];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int QB = 16 * NW;
+  const int QB = WQ * NW;
   const int nqb = gridDim.x;
   int h = blockIdx.y, qx = blockIdx.x;  // qx = 0: the longest query block (the last one)
   if (FA_H_XCD) {
@@ -443,37 +445,43 @@ __global__ __launch_bounds__(64 * NW) void k_fa_attn_h(const float* __restrict__
     }
   }
   const int q0 = (nqb - 1 - qx) * QB;
-  const int qw0 = q0 + wave * 16;
+  const int qw0 = q0 + wave * WQ;
   const int kvh = h / (m.nh / m.nkv);
   const int ql = lane & 15, g = lane >> 4;
-  const int qi = qw0 + ql;
-  const int qc = min(qi, T - 1);
+  int qi[QS];
+#pragma unroll
+  for (int u = 0; u < QS; ++u) qi[u] = qw0 + 16 * u + ql;
 
-  half8_t qf[NC];
-  const float* qrow = qg + (size_t)qc * m.qw + (size_t)h * m.hd;
-  {
+  half8_t qf[QS][NC];
+#pragma unroll
+  for (int u = 0; u < QS; ++u) {
+    const float* qrow = qg + (size_t)min(qi[u], T - 1) * m.qw + (size_t)h * m.hd;
     // Loads at clamped (in-row) offsets first, all in flight together; pad dims zeroed after.
     float4 qv[2 * NC];
 #pragma unroll
-    for (int u = 0; u < 2 * NC; ++u)
-      qv[u] = *(const float4*)(qrow + min(32 * (u >> 1) + 8 * g + 4 * (u & 1), m.hd - 4));
+    for (int i = 0; i < 2 * NC; ++i)
+      qv[i] = *(const float4*)(qrow + min(32 * (i >> 1) + 8 * g + 4 * (i & 1), m.hd - 4));
 #pragma unroll
     for (int c = 0; c < NC; ++c)
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float4 v = qv[2 * c + (e >> 2)];
         const float x = (e & 3) == 0 ? v.x : (e & 3) == 1 ? v.y : (e & 3) == 2 ? v.z : v.w;
-        qf[c][e] = (half_t)(32 * c + 8 * g + e < m.hd ? x : 0.f);
+        qf[u][c][e] = (half_t)(32 * c + 8 * g + e < m.hd ? x : 0.f);
       }
   }
-  float4_t oacc[2 * NC];
+  float4_t oacc[QS][2 * NC];
 #pragma unroll
-  for (int f = 0; f < 2 * NC; ++f) oacc[f] = (float4_t){0.f, 0.f, 0.f, 0.f};
-  float mrun = -INFINITY, lrun = 0.f;
+  for (int u = 0; u < QS; ++u)
+#pragma unroll
+    for (int f = 0; f < 2 * NC; ++f) oacc[u][f] = (float4_t){0.f, 0.f, 0.f, 0.f};
+  float mrun[QS], lrun[QS];
+#pragma unroll
+  for (int u = 0; u < QS; ++u) mrun[u] = -INFINITY, lrun[u] = 0.f;
 
   const int kend = min(T, q0 + QB);
   const int ntile = (kend + KT - 1) / KT;
-  const int wq_last = min(qw0 + 15, T - 1);
+  const int wq_last = min(qw0 + WQ - 1, T - 1);
   const half_t* kb = k16 + (size_t)kvh * Tp * DP;
   const half_t* vb = v16t + (size_t)kvh * Tp * DP;  // Tp / KT tiles of DP x KT
   // Scores in the base-2 domain: s2 = (q.k) log2(e) / sqrt(head_dim), p = 2^(s2 - max).
@@ -518,82 +526,112 @@ __global__ __launch_bounds__(64 * NW) void k_fa_attn_h(const float* __restrict__
     // Only tiles reaching past the wave's first query or past T need the mask.
     const bool need_mask = k0 + KT - 1 > qw0 || k0 + KT > T;
 
-    float sv[2 * S32][4];
-    float mt = -INFINITY;
+    // S^T sub-tiles: each K fragment read from LDS feeds the QS query sets.
+    float sv[QS][2 * S32][4];
 #pragma unroll
     for (int b = 0; b < 2 * S32; ++b) {
-      float4_t sc = (float4_t){0.f, 0.f, 0.f, 0.f};
+      float4_t sc[QS];
+#pragma unroll
+      for (int u = 0; u < QS; ++u) sc[u] = (float4_t){0.f, 0.f, 0.f, 0.f};
       const half_t* krow = sk + (16 * b + ql) * KR + 8 * g;
 #pragma unroll
-      for (int c = 0; c < NC; ++c)
-        sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const half8_t*)(krow + 32 * c), qf[c], sc,
-                                                    0, 0, 0);
+      for (int c = 0; c < NC; ++c) {
+        const half8_t kf = *(const half8_t*)(krow + 32 * c);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sv[b][r] = sc[r] * rs;
+        for (int u = 0; u < QS; ++u)
+          sc[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[u][c], sc[u], 0, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < QS; ++u)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sv[u][b][r] = sc[u][r] * rs;
       if (need_mask) {
 #pragma unroll
+        for (int u = 0; u < QS; ++u)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int key = k0 + 16 * b + 4 * g + r;
+            if (key > qi[u] || key >= T) sv[u][b][r] = -INFINITY;
+          }
+      }
+    }
+    half8_t pf[QS][S32];
+#pragma unroll
+    for (int u = 0; u < QS; ++u) {
+      float mt = -INFINITY;
+#pragma unroll
+      for (int b = 0; b < 2 * S32; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mt = fmaxf(mt, sv[u][b][r]);
+      mt = fmaxf(mt, __shfl_xor(mt, 16));
+      mt = fmaxf(mt, __shfl_xor(mt, 32));
+      // A set whose queries all precede the tile sees only -inf here and keeps its max
+      // (finite from tile 0 on), so its probabilities are 0 and alpha is 1.
+      const float mnew = fmaxf(mrun[u], mt);
+      const float alpha = __builtin_amdgcn_exp2f(mrun[u] - mnew);  // 0 on the first tile
+      float ps = 0.f;
+#pragma unroll
+      for (int b = 0; b < 2 * S32; ++b)
+#pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int key = k0 + 16 * b + 4 * g + r;
-          if (key > qi || key >= T) sv[b][r] = -INFINITY;
+          const float pv2 = __builtin_amdgcn_exp2f(sv[u][b][r] - mnew);
+          ps += pv2;
+          pf[u][b >> 1][4 * (b & 1) + r] = (half_t)pv2;
         }
+      lrun[u] = lrun[u] * alpha + ps;
+      const bool grow = mnew > mrun[u];
+      mrun[u] = mnew;
+      if (__builtin_amdgcn_ballot_w64(grow)) {
+#pragma unroll
+        for (int f = 0; f < 2 * NC; ++f) oacc[u][f] *= alpha;
       }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) mt = fmaxf(mt, sv[b][r]);
     }
-    mt = fmaxf(mt, __shfl_xor(mt, 16));
-    mt = fmaxf(mt, __shfl_xor(mt, 32));
-    const float mnew = fmaxf(mrun, mt);
-    const float alpha = __builtin_amdgcn_exp2f(mrun - mnew);  // 0 on the first tile
-    half8_t pf[S32];
-    float ps = 0.f;
-#pragma unroll
-    for (int b = 0; b < 2 * S32; ++b)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float pv2 = __builtin_amdgcn_exp2f(sv[b][r] - mnew);
-        ps += pv2;
-        pf[b >> 1][4 * (b & 1) + r] = (half_t)pv2;
-      }
-    lrun = lrun * alpha + ps;
-    const bool grow = mnew > mrun;
-    mrun = mnew;
-    if (__builtin_amdgcn_ballot_w64(grow)) {
-#pragma unroll
-      for (int f = 0; f < 2 * NC; ++f) oacc[f] *= alpha;
-    }
+    // O^T += V^T P: each V^T fragment read from LDS feeds the QS query sets.
 #pragma unroll
     for (int s32 = 0; s32 < S32; ++s32)
 #pragma unroll
-      for (int f = 0; f < 2 * NC; ++f)
-        oacc[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-            *(const half8_t*)(svt + (s32 * DP + 16 * f + ql) * VR + 8 * g), pf[s32], oacc[f], 0,
-            0, 0);
+      for (int f = 0; f < 2 * NC; ++f) {
+        const half8_t vf = *(const half8_t*)(svt + (s32 * DP + 16 * f + ql) * VR + 8 * g);
+#pragma unroll
+        for (int u = 0; u < QS; ++u)
+          oacc[u][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[u][s32], oacc[u][f], 0, 0, 0);
+      }
   }
-  float l = lrun + __shfl_xor(lrun, 16);
-  l = l + __shfl_xor(l, 32);
-  if (qi >= T) return;
-  const float* gate = qg + (size_t)qi * m.qw + (size_t)m.od + (size_t)h * m.hd;
-  const size_t orow = (size_t)qi * m.od + (size_t)h * m.hd;
-  float4 gv[2 * NC];  // gate loads first (clamped offsets), then the math and 8-byte stores
 #pragma unroll
-  for (int f = 0; f < 2 * NC; ++f)
-    gv[f] = *(const float4*)(gate + min(16 * f + 4 * g, m.hd - 4));
-  const float il = 1.f / l;
+  for (int u = 0; u < QS; ++u) {
+    float l = lrun[u] + __shfl_xor(lrun[u], 16);
+    l = l + __shfl_xor(l, 32);
+    if (qi[u] >= T) continue;
+    const float* gate = qg + (size_t)qi[u] * m.qw + (size_t)m.od + (size_t)h * m.hd;
+    const size_t orow = (size_t)qi[u] * m.od + (size_t)h * m.hd;
+    float4 gv[2 * NC];  // gate loads first (clamped offsets), then the math and 8-byte stores
 #pragma unroll
-  for (int f = 0; f < 2 * NC; ++f) {
-    const int d = 16 * f + 4 * g;
-    if (d >= m.hd) continue;
-    typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
-    const half4_t o = {(half_t)(oacc[f][0] * il * mx_sigmoid(gv[f].x)),
-                       (half_t)(oacc[f][1] * il * mx_sigmoid(gv[f].y)),
-                       (half_t)(oacc[f][2] * il * mx_sigmoid(gv[f].z)),
-                       (half_t)(oacc[f][3] * il * mx_sigmoid(gv[f].w))};
-    *(half4_t*)(act16 + orow + d) = o;
+    for (int f = 0; f < 2 * NC; ++f)
+      gv[f] = *(const float4*)(gate + min(16 * f + 4 * g, m.hd - 4));
+    const float il = 1.f / l;
+#pragma unroll
+    for (int f = 0; f < 2 * NC; ++f) {
+      const int d = 16 * f + 4 * g;
+      if (d >= m.hd) continue;
+      typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+      const half4_t o = {(half_t)(oacc[u][f][0] * il * mx_sigmoid(gv[f].x)),
+                         (half_t)(oacc[u][f][1] * il * mx_sigmoid(gv[f].y)),
+                         (half_t)(oacc[u][f][2] * il * mx_sigmoid(gv[f].z)),
+                         (half_t)(oacc[u][f][3] * il * mx_sigmoid(gv[f].w))};
+      *(half4_t*)(act16 + orow + d) = o;
+    }
   }
 }
 
 #ifndef FA_H_NW
-#define FA_H_NW 8  // waves (16 queries each) per block of the fp16 attention
+#define FA_H_NW 8  // waves per block of the fp16 attention
+#endif
+#ifndef FA_H_QS
+// Sets of 16 queries per wave of the fp16 attention.  Two sets read each K / V^T fragment
+// from LDS once for two MFMAs, but their registers (256 VGPRs + 206 AGPRs) allow one wave
+// per SIMD: with 4-wave blocks the Qwen3-Next 4096-token attention took 330 us against
+// 250 us for one set in 8-wave blocks (2 waves per SIMD, 194 VGPRs).
+#define FA_H_QS 1
 #endif
 
 template <int NC>
@@ -605,9 +643,9 @@ int launch_attn_h(const float* qg, const float* kk, const float* vv, const FaDim
   hipLaunchKernelGGL(k_fa_pack_kv, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, s, kk,
                      vv, m, T, Tp, DP, k16, v16t);
   MX_TRY(mx_launch_status());
-  const dim3 grid(mx_ceil_div(T, 16 * FA_H_NW), m.nh);
+  const dim3 grid(mx_ceil_div(T, 16 * FA_H_QS * FA_H_NW), m.nh);
   const float sqrt_hd = (float)sqrt((double)m.hd);
-  hipLaunchKernelGGL((k_fa_attn_h<NC, FA_H_NW, FA_H_S32>), grid, dim3(64 * FA_H_NW), 0, s, qg,
+  hipLaunchKernelGGL((k_fa_attn_h<NC, FA_H_NW, FA_H_S32, FA_H_QS>), grid, dim3(64 * FA_H_NW), 0, s, qg,
                      k16, v16t, m, T, Tp, sqrt_hd, (half_t*)act);
   return mx_launch_status();
 }
