@@ -406,6 +406,10 @@ int prepare(GemmArgs& args, const void* a, int M, int K, int es, const MxGemmSeg
 
 }  // namespace
 
+#ifndef MX_GEMM_TAIL
+#define MX_GEMM_TAIL 1  // leftover columns of a partial last round on 128 x 128 tiles
+#endif
+
 int mx_gemm_f16(const void* a, int M, int K, const MxGemmSeg* segs, int nseg, hipStream_t s) {
   GemmArgs args;
   MX_TRY(prepare(args, a, M, K, 2, segs, nseg, K, 0));
@@ -414,9 +418,44 @@ int mx_gemm_f16(const void* a, int M, int K, const MxGemmSeg* segs, int nseg, hi
   // 256 x 256 tiles while they give at least two rounds of blocks on 256 CUs; 128 x 128
   // (four waves, two blocks per CU) otherwise.
   const long big = (long)mx_ceil_div(M, 256) * mx_ceil_div((int)cols, 256);
-  if (big >= 512)
-    return launch<half_t, false, 256, 256, 128, 64, MX_GEMM_NS, 1>(args, segs, nseg, 1, s);
-  return launch<half_t, false, 128, 128, 64, 64, MX_GEMM_NS, 2>(args, segs, nseg, 1, s);
+  if (big < 512)
+    return launch<half_t, false, 128, 128, 64, 64, MX_GEMM_NS, 2>(args, segs, nseg, 1, s);
+  if (MX_GEMM_TAIL && big % 256) {
+    // One 256 x 256 block per CU: the blocks past the last whole round would run as a
+    // partial round as long as a full one.  The whole rounds take whole 256-column tiles
+    // of the segments in order; the columns left over (partial tiles, later segments) go
+    // to a second launch on 128 x 128 tiles, which spreads them over all CUs.  Each output
+    // element is still computed by one block over the whole reduction.
+    int budget = (int)(big / 256 * 256 / mx_ceil_div(M, 256));  // 256-column tiles
+    MxGemmSeg head[MX_GEMM_MAX_SEG], tail[MX_GEMM_MAX_SEG];
+    int nh = 0, nt = 0;
+    for (int i = 0; i < nseg; ++i) {
+      const MxGemmSeg& g = segs[i];
+      const int take = budget < g.n / 256 ? budget : g.n / 256;
+      budget -= take;
+      const int n0 = take * 256;
+      if (n0 > 0) {
+        head[nh] = g;
+        head[nh++].n = n0;
+      }
+      if (n0 < g.n) {
+        MxGemmSeg t = g;
+        t.w = (const char*)g.w + (size_t)n0 * K * 2;
+        t.y = g.y + n0;
+        if (g.res) t.res = g.res + n0;
+        t.n = g.n - n0;
+        tail[nt++] = t;
+      }
+    }
+    if (nh > 0 && nt > 0) {
+      GemmArgs ah, at;
+      MX_TRY(prepare(ah, a, M, K, 2, head, nh, K, 0));
+      MX_TRY(prepare(at, a, M, K, 2, tail, nt, K, 0));
+      MX_TRY((launch<half_t, false, 256, 256, 128, 64, MX_GEMM_NS, 1>(ah, head, nh, 1, s)));
+      return launch<half_t, false, 128, 128, 64, 64, MX_GEMM_NS, 2>(at, tail, nt, 1, s);
+    }
+  }
+  return launch<half_t, false, 256, 256, 128, 64, MX_GEMM_NS, 1>(args, segs, nseg, 1, s);
 }
 
 int mx_gemm_f32_slices(const float* a, int M, int K, const MxGemmSeg* segs, int nseg,
