@@ -406,6 +406,9 @@ int prepare(GemmArgs& args, const void* a, int M, int K, int es, const MxGemmSeg
 
 }  // namespace
 
+#ifndef MX_GEMM_MID
+#define MX_GEMM_MID 1  // 256 x 128 tiles for products that fill whole rounds with them
+#endif
 #ifndef MX_GEMM_TAIL
 #define MX_GEMM_TAIL 1  // leftover columns of a partial last round on 128 x 128 tiles
 #endif
@@ -418,8 +421,14 @@ int mx_gemm_f16(const void* a, int M, int K, const MxGemmSeg* segs, int nseg, hi
   // 256 x 256 tiles while they give at least two rounds of blocks on 256 CUs; 128 x 128
   // (four waves, two blocks per CU) otherwise.
   const long big = (long)mx_ceil_div(M, 256) * mx_ceil_div((int)cols, 256);
-  if (big < 512)
+  if (big < 512) {
+    // 256 x 128 tiles (8 waves of 64 x 64, one block per CU) when they fill whole rounds
+    long mid = 0;
+    for (int i = 0; i < nseg; ++i) mid += (long)mx_ceil_div(M, 256) * mx_ceil_div(segs[i].n, 128);
+    if (MX_GEMM_MID && mid >= 256 && mid % 256 == 0)
+      return launch<half_t, false, 256, 128, 64, 64, MX_GEMM_NS, 1>(args, segs, nseg, 1, s);
     return launch<half_t, false, 128, 128, 64, 64, MX_GEMM_NS, 2>(args, segs, nseg, 1, s);
+  }
   if (MX_GEMM_TAIL && big % 256) {
     // One 256 x 256 block per CU: the blocks past the last whole round would run as a
     // partial round as long as a full one.  The whole rounds take whole 256-column tiles
