@@ -75,5 +75,14 @@ __device__ __forceinline__ float mx_silu(float x) { return x / (1.0f + expf(-x))
 // Reference sigmoid: 1 / (1 + exp(-x))  (qwen3_next.py:31-32).
 __device__ __forceinline__ float mx_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+// fp32 -> fp16 for the intermediates the expert kernels keep in fp16 (activation rows,
+// prefill y rows): values beyond the fp16 range saturate to +-65504 instead of becoming
+// infinities; NaN stays NaN (both comparisons are false).
+__device__ __forceinline__ half_t mx_f16_sat(float v) {
+  v = v > 65504.0f ? 65504.0f : v;
+  v = v < -65504.0f ? -65504.0f : v;
+  return (half_t)v;
+}
+
 static inline int mx_ceil_div(int a, int b) { return (a + b - 1) / b; }
 static inline size_t mx_align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }

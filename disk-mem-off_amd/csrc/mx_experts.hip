@@ -384,7 +384,7 @@ __global__ __launch_bounds__(256) void k_expert(const ExpertParams p, const Sele
             if constexpr (WF == MX_DT_F32)
               ((float*)p.out)[o] = av;
             else
-              ((half_t*)p.out)[o] = (half_t)av;
+              ((half_t*)p.out)[o] = mx_f16_sat(av);
           }
         }
     }
@@ -716,7 +716,7 @@ __device__ __forceinline__ void expert_lds_tile(const ExpertParams& p, char* lds
               const float v = w * (acc[mi][f][r] * 1.f);
               if constexpr (Y16)
                 __builtin_amdgcn_raw_buffer_store_b16(
-                    __builtin_bit_cast(short, (half_t)v), ry, yo + 32u * f, 0, 0);
+                    __builtin_bit_cast(short, mx_f16_sat(v)), ry, yo + 32u * f, 0, 0);
               else
                 __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, v), ry,
                                                       yo + 64u * f, 0, 0);
@@ -768,7 +768,7 @@ __device__ __forceinline__ void expert_lds_tile(const ExpertParams& p, char* lds
           if (m < trows) {
             const float gv = acc[mi][f][r] * sg;
             const float uv = acc[mi][NBIX + f][r] * su;
-            ((half_t*)p.out)[(size_t)(orow + m) * p.ldo + n] = (half_t)(mx_silu(gv) * uv);
+            ((half_t*)p.out)[(size_t)(orow + m) * p.ldo + n] = mx_f16_sat(mx_silu(gv) * uv);
           }
         }
     }
@@ -798,7 +798,7 @@ __device__ __forceinline__ void expert_lds_tile(const ExpertParams& p, char* lds
           if (n >= N) continue;
           const float v = w * (acc[mi][f][r] * sd[f]);
           if constexpr (Y16)
-            ((half_t*)p.out)[(size_t)row * p.ldo + n] = (half_t)v;
+            ((half_t*)p.out)[(size_t)row * p.ldo + n] = mx_f16_sat(v);
           else
             ((float*)p.out)[(size_t)row * p.ldo + n] = v;
         }

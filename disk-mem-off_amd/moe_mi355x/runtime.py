@@ -209,10 +209,14 @@ class OffloadRuntime:
         pinned.view[: host_weights.nbytes] = host_weights.view[: host_weights.nbytes]
         return pinned
 
-    def _wait_copy(self, rec: _Inflight) -> None:
-        sync = getattr(self.backend, "event_synchronize", None)
-        if sync is not None:
-            sync(rec.copied)
+    def _release_staging(self, rec: _Inflight) -> None:
+        """Hand a pinned staging buffer back with the event of the copy that reads it (the
+        pool owns the event from then on and waits on it before lending the buffer again);
+        otherwise destroy that event."""
+        if rec.staged is not rec.host and self._pinned_pool is not None:
+            self._pinned_pool.release(rec.staged, copy_event=rec.copied)
+        else:
+            self.backend.destroy_event(rec.copied)
 
     # -- one layer's transfer --
     def _issue(self, index: int, layer_id: int, metrics: RuntimeMetrics) -> _Inflight:
@@ -351,10 +355,7 @@ class OffloadRuntime:
                 done = self.backend.record_event(self.compute_stream) if self._timing else None
                 self._free_device(rec.device, done)
                 self.storage.release(layer_id)
-                if rec.staged is not rec.host and self._pinned_pool is not None:
-                    self._wait_copy(rec)
-                    self._pinned_pool.release(rec.staged)
-                self.backend.destroy_event(rec.copied)
+                self._release_staging(rec)
                 timings.append((rec.lm, rec.t_start, rec.t_end, c_start, c_end,
                                 rec.extra_copies))
                 metrics.layer_metrics.append(rec.lm)
@@ -368,9 +369,7 @@ class OffloadRuntime:
                 rec = inflight.popleft()
                 self.backend.synchronize_stream(self.transfer_stream)
                 self._free_device(rec.device, None)
-                if rec.staged is not rec.host and self._pinned_pool is not None:
-                    self._pinned_pool.release(rec.staged)
-                self.backend.destroy_event(rec.copied)
+                self._release_staging(rec)
             self.backend.synchronize_stream(self.transfer_stream)
             self.backend.synchronize_stream(self.compute_stream)
             self._flush_deferred(force=True)

@@ -213,8 +213,10 @@ int mx_moe_forward_profiled(const MxMoeDesc* desc, const MxMoeWeights* weights,
  * hipMalloc.  The same computation, without the workspace arguments: the stages run out of
  * a scratch array of MX_NOALLOC_MAX_WORKSPACE bytes that the library holds on every device
  * it runs on until the process ends.  Nothing is allocated and no memset is issued.
- * Returns MX_ERR_WORKSPACE when mx_moe_workspace_size(desc, tokens) exceeds that size
- * (16 MiB: GLM-4.7 shapes up to 64 tokens, Qwen3-Next shapes up to 128).  Every call on
+ * Returns MX_ERR_WORKSPACE when mx_moe_workspace_size(desc, tokens) exceeds that size;
+ * size batches from that function, not from the token count alone (from 65 tokens the
+ * prefill-path buffers join the workspace).  With 16 MiB: GLM-4.7 shapes up to 64 tokens
+ * (62 with fp32 experts), Qwen3-Next shapes up to 83 (108 with fp32 experts).  Every call on
  * one device shares that device's scratch: calls that overlap on one device (other
  * streams, other host threads) race and must be serialised by the caller; calls on one
  * stream are ordered by it.                                                            */
@@ -358,10 +360,16 @@ typedef struct MxLinearAttnViews {
   float* decay;  /* [T, n] exp(g)                                                       */
   float* o;      /* [T, n dv] recurrence output                                         */
   void* act;     /* [T, n dv] rms_norm(o) * silu(z), fp16 (fp32 for F32 weights)        */
-  float* y;      /* [T, H] act W_out^T                                                  */
+  float* y;      /* [T, H] act W_out^T; not written on the fused-GEMM path (below)      */
 } MxLinearAttnViews;
 
-#define MX_LA_N_STAGES 8 /* rmsnorm, qkvz, ba, conv+gates, scan, gated norm, out, residual */
+/* Stages: rmsnorm, qkvz, ba, conv+gates, scan, gated norm, out, residual.  With fp16
+ * weights, T >= 65 and H (for qkvz / ba) or n dv (for out) a multiple of 32 the
+ * projections run on the dense MFMA GEMM: ba is computed in the qkvz launch (stage 2 is
+ * then empty, and the _profiled events report ba's time under qkvz), and out = x +
+ * act W_out^T is formed in the out launch's epilogue (stage 7 is empty and the view y is
+ * not written).                                                                        */
+#define MX_LA_N_STAGES 8
 
 int mx_linear_attn_workspace_size(const MxLinearAttnDesc* desc, int32_t tokens,
                                   size_t* nbytes);
@@ -422,10 +430,16 @@ typedef struct MxFullAttnViews {
   float* k;    /* [T, n_kv_heads head_dim] k, normalised and rotated in place           */
   float* v;    /* [T, n_kv_heads head_dim]                                              */
   void* act;   /* [T, n_heads head_dim] attn * sigmoid(gate), fp16 (fp32 for F32 weights) */
-  float* y;    /* [T, H] act W_o^T                                                      */
+  float* y;    /* [T, H] act W_o^T; not written on the fused-GEMM path (below)          */
 } MxFullAttnViews;
 
-#define MX_FA_N_STAGES 8 /* rmsnorm, q, k, v, qk-norm+rope, attention, o, residual */
+/* Stages: rmsnorm, q, k, v, qk-norm+rope, attention, o, residual.  With fp16 weights,
+ * T >= 65 and H (for q / k / v) or n_heads head_dim (for o) a multiple of 32 the
+ * projections run on the dense MFMA GEMM: k and v are computed in the q launch (stages 2
+ * and 3 are then empty, and the _profiled events report their time under q), and out =
+ * x + act W_o^T is formed in the o launch's epilogue (stage 7 is empty and the view y is
+ * not written).                                                                        */
+#define MX_FA_N_STAGES 8
 
 int mx_full_attn_workspace_size(const MxFullAttnDesc* desc, int32_t tokens, size_t* nbytes);
 int mx_full_attn_views(const MxFullAttnDesc* desc, int32_t tokens, void* workspace,

@@ -6,7 +6,7 @@ import pytest
 
 from moe_mi355x import _lib
 from moe_mi355x import synthetic as syn
-from null_backend import NullBackend
+from host_backend import HostArenaBackend
 from moe_mi355x.executors import GLM4MoeExecutor, Qwen3NextExecutor
 from moe_mi355x.layout import make_layer_spec, pack_tensors
 
@@ -42,7 +42,7 @@ def test_run_layer_requires_the_rocm_backend():
     shape = syn.MoeShape(syn.GLM, 32, 4, 2, 16, 16, 2.5, 1e-5)
     raw, meta = pack_tensors(syn.make_tensors(shape, 1), align=16)
     layer = make_layer_spec(0, meta, len(raw))
-    be = NullBackend()
+    be = HostArenaBackend()
     buf = be.alloc_device(len(raw))
     ex = GLM4MoeExecutor(shape.config())
     with pytest.raises(RuntimeError, match="MI355X backend"):
@@ -55,7 +55,7 @@ def test_attention_layers_need_an_attention_callable():
     t["self_attn.q_proj.weight"] = np.zeros((32, 32), np.float32)
     raw, meta = pack_tensors(t, align=16)
     layer = make_layer_spec(0, meta, len(raw))
-    be = NullBackend()
+    be = HostArenaBackend()
     ex = GLM4MoeExecutor(shape.config())
     with pytest.raises(NotImplementedError, match="attention"):
         ex.run_layer(layer, np.zeros((2, 32), np.float32), be.alloc_device(len(raw)), be, None)
@@ -92,8 +92,8 @@ def _attention_layer(seed=5):
     return t, buf, make_layer_spec(0, meta, len(buf))
 
 
-class _PtrBackend(NullBackend):
-    """NullBackend with pointer D2H copies over one numpy array; logs the byte counts."""
+class _PtrBackend(HostArenaBackend):
+    """HostArenaBackend with pointer D2H copies over one numpy array; logs the byte counts."""
 
     def __init__(self, data):
         super().__init__()
@@ -120,7 +120,7 @@ def test_read_layer_tensors_copies_only_non_mlp_ranges():
     want = sum(t[n].nbytes for n in got)
     assert want <= sum(be.copied) < len(buf) // 4
     # the whole-layer fallback of backends without pointer copies gives the same tensors
-    nb = NullBackend()
+    nb = HostArenaBackend()
     d2 = nb.alloc_device(len(buf))
     from moe_mi355x.types import HostBuffer
     nb.copy_h2d_async(d2, HostBuffer(view=memoryview(buf)), None)

@@ -7,7 +7,7 @@ from typing import Any
 
 import pytest
 
-from null_backend import NullBackend
+from host_backend import HostArenaBackend
 from moe_mi355x.quantize import CompositeDequantizer, Int8Dequantizer
 from moe_mi355x.runtime import OffloadRuntime, RuntimeMetrics
 from moe_mi355x.scheduler import LookaheadScheduler
@@ -30,7 +30,7 @@ class RecordingExecutor:
 
     def run_layer(self, layer, activations, device_weights, backend, stream):
         self.executed.append(layer.layer_id)
-        self.payloads.append(bytes(backend._buffers[int(device_weights.handle)]))
+        self.payloads.append(backend.device_bytes(device_weights))
         return activations
 
 
@@ -43,7 +43,7 @@ def storage(n: int, nbytes: int = 16) -> InMemoryStorage:
 
 
 def runtime(n=3, lookahead=1, **kw) -> OffloadRuntime:
-    backend = kw.pop("backend", NullBackend())
+    backend = kw.pop("backend", HostArenaBackend())
     return OffloadRuntime(layers=layers(n), backend=backend, storage=storage(n),
                           scheduler=LookaheadScheduler(lookahead=lookahead),
                           executor=kw.pop("executor", SumExecutor()), **kw)
@@ -71,9 +71,9 @@ def test_unknown_layer_raises():
 
 
 def test_device_buffers_freed():
-    backend = NullBackend()
+    backend = HostArenaBackend()
     runtime(3, 2, backend=backend).run_inference([0, 1, 2], inputs=0)
-    assert len(backend._buffers) == 0
+    assert len(backend.allocations) == 0
 
 
 def test_per_layer_metrics():
@@ -97,15 +97,17 @@ def test_metric_formulas():
 
 
 def test_buffer_pool_and_pinned_staging():
-    backend = NullBackend()
+    backend = HostArenaBackend()
     with runtime(3, 2, backend=backend, use_buffer_pool=True, use_pinned_staging=True) as rt:
         out, m = rt.run_inference([0, 1, 2], inputs=0)
         assert out == 3 and m.transferred_bytes == 48
-    assert len(backend._buffers) == 0
+    # every device buffer, pinned staging buffer and event is released at close
+    assert len(backend.allocations) == 0 and len(backend.pinned) == 0
+    assert backend.live_events == 0
 
 
 def test_pinned_staging_skipped_when_unsupported():
-    class NoPinned(NullBackend):
+    class NoPinned(HostArenaBackend):
         @property
         def supports_pinned_host(self) -> bool:
             return False
@@ -118,7 +120,7 @@ def test_quantized_transfer_accounting():
     lay = [LayerSpec(0, "L0", 4, {"dtype": "int8", "scale": 1.0}),
            LayerSpec(1, "L1", 4, {"dtype": "int8", "scale": 1.0})]
     st = InMemoryStorage({0: struct.pack("4b", 1, 2, 3, 4), 1: struct.pack("4b", 5, 6, 7, 8)})
-    rt = OffloadRuntime(lay, NullBackend(), st, LookaheadScheduler(1), SumExecutor(),
+    rt = OffloadRuntime(lay, HostArenaBackend(), st, LookaheadScheduler(1), SumExecutor(),
                         dequantizer=Int8Dequantizer())
     out, m = rt.run_inference([0, 1], inputs=0)
     assert out == 1 and m.transferred_bytes == 32 and m.compressed_bytes == 8
@@ -128,7 +130,7 @@ def test_quantized_transfer_accounting():
 def test_quantized_mixed_layers():
     lay = [LayerSpec(0, "L0", 16), LayerSpec(1, "L1", 4, {"dtype": "int8", "scale": 1.0})]
     st = InMemoryStorage({0: b"\x00" * 16, 1: struct.pack("4b", 1, 2, 3, 4)})
-    rt = OffloadRuntime(lay, NullBackend(), st, LookaheadScheduler(1), SumExecutor(),
+    rt = OffloadRuntime(lay, HostArenaBackend(), st, LookaheadScheduler(1), SumExecutor(),
                         dequantizer=CompositeDequantizer())
     _, m = rt.run_inference([0, 1], inputs=0)
     assert m.transferred_bytes == 32 and m.compressed_bytes == 4
@@ -147,7 +149,7 @@ def test_transfers_issued_ahead_of_compute():
     runs (the reference enqueues copy i right before compute i)."""
     events: list[str] = []
 
-    class Spy(NullBackend):
+    class Spy(HostArenaBackend):
         def copy_h2d_async(self, dst, src, stream):
             events.append(f"copy{src.view.tobytes()[0]}")
             super().copy_h2d_async(dst, src, stream)
@@ -163,7 +165,7 @@ def test_transfers_issued_ahead_of_compute():
 
 
 def test_expert_granular_needs_capable_executor_and_backend():
-    from null_backend import NullBackend
+    from host_backend import HostArenaBackend
     from moe_mi355x.runtime import OffloadRuntime
     from moe_mi355x.scheduler import LookaheadScheduler
     from moe_mi355x.storage import InMemoryStorage
@@ -180,8 +182,8 @@ def test_expert_granular_needs_capable_executor_and_backend():
             return [], []
 
     with pytest.raises(ValueError, match="run_layer_granular"):
-        OffloadRuntime([], NullBackend(), InMemoryStorage({}), LookaheadScheduler(1), Plain(),
+        OffloadRuntime([], HostArenaBackend(), InMemoryStorage({}), LookaheadScheduler(1), Plain(),
                        expert_granular=True)
     with pytest.raises(ValueError, match="pointer copies"):
-        OffloadRuntime([], NullBackend(), InMemoryStorage({}), LookaheadScheduler(1), Granular(),
+        OffloadRuntime([], HostArenaBackend(), InMemoryStorage({}), LookaheadScheduler(1), Granular(),
                        expert_granular=True)

@@ -2,7 +2,8 @@
 allocation) against mx_moe_forward with a caller workspace: identical outputs, bit for
 bit, on two calls in a row, the second with fewer tokens (the scratch keeps the first
 call's contents), for a GLM-style layer (one-token selection path included) and a
-Qwen3-Next-style layer (512 experts, gated shared expert)."""
+Qwen3-Next-style layer (512 experts, gated shared expert) at decode and at prefill sizes
+(T >= 65: split-plane router, 128-row tiles and fp16 y rows inside the scratch)."""
 from __future__ import annotations
 
 import ctypes
@@ -29,6 +30,10 @@ CASES = {
             _lib.MX_ROUTER_SIGMOID_SELECT_BIAS, (64, 1)),
     "qwen": (syn.MoeShape(syn.QWEN, 1024, 512, 10, 256, 256, 1.0, 1e-6, has_bias=False,
                           has_shared_gate=True), _lib.MX_ROUTER_SOFTMAX, (48, 3)),
+    # from 65 tokens: the split-plane router, 128-row m-tiles and fp16 y rows, carved out
+    # of the scratch array
+    "qwen_prefill": (syn.MoeShape(syn.QWEN, 1024, 512, 10, 256, 256, 1.0, 1e-6, has_bias=False,
+                                  has_shared_gate=True), _lib.MX_ROUTER_SOFTMAX, (150, 70)),
 }
 
 
