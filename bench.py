@@ -43,7 +43,8 @@ from moe_mi355x.backends import MI355XBackend  # noqa: E402
 from moe_mi355x.device_layer import DeviceMoeLayer  # noqa: E402
 from moe_mi355x.moe import read_device  # noqa: E402
 from moe_mi355x.workloads import (HBM_PEAK, MFMA_F16_PEAK, MFMA_F32_PEAK, call_traffic,  # noqa: E402
-                                  host_router_logits, synthetic_host_params, zipf_bias)
+                                  host_router_logits, synthetic_host_params, zipf_bias,
+                                  zipf_summary)
 
 METRIC = "MoE-layer tokens/s at decode (HBM GB/s %peak) and prefill (MFMA %peak), 1 GPU"
 SEED = 2026
@@ -551,8 +552,11 @@ def main() -> int:
                 hp = synthetic_host_params(G, SEED)
                 logits = host_router_logits(x, np.ones(G.hidden, np.float32),
                                             hp["mlp.gate.weight"], G.eps)
-                bias, loads, c = zipf_bias(logits, G.top_k, 1.1, seed=SEED,
-                                           base_bias=hp["mlp.gate.e_score_correction_bias"])
+                bias, loads, zinfo = zipf_bias(logits, G.top_k, 1.1, seed=SEED,
+                                               base_bias=hp["mlp.gate.e_score_correction_bias"])
+                zhost = zipf_summary(loads, zinfo["target"], T, G.top_k)
+                if not zhost["ok"]:
+                    raise RuntimeError(f"Zipf(1.1) workload not realised: {zhost}")
                 off = layer.layout.offset("mlp.gate.e_score_correction_bias")
                 bb = np.ascontiguousarray(bias, np.float32)
                 backend.copy_h2d_ptr_async(layer.buf.handle + off, bb.ctypes.data, bb.nbytes, stream)
@@ -561,9 +565,12 @@ def main() -> int:
                 r = Case(backend, stream, [layer], G, "float16", T, mode, x).run(
                     min(args.steps, 20), 3)
                 s = summarize(r, name, "float16")
-                cnt = np.sort(r["counts"])[::-1]
-                s["zipf"] = {"c": c, "max_load": int(cnt[0]), "min_load": int(cnt[-1]),
-                             "median_load": int(np.median(cnt)), "top5": cnt[:5].tolist()}
+                # loads the device routed (its dispatch counts), against the capped and
+                # renormalised Zipf(1.1) targets: all experts active, the hottest at >= 95 %
+                # of the tokens, L1 distance <= 10 % of the routed pairs
+                s["zipf"] = zipf_summary(r["counts"], zinfo["target"], T, G.top_k)
+                if not s["zipf"]["ok"]:
+                    raise RuntimeError(f"device loads miss the Zipf(1.1) targets: {s['zipf']}")
                 sweep[name] = s
                 log(f"{name}: {s['tokens_per_s']} tok/s, mfma {s['layer_mfma_frac']}")
         for lay in layers:

@@ -63,34 +63,96 @@ def host_router_logits(x: np.ndarray, norm_w: np.ndarray, router_w: np.ndarray,
     return h @ router_w.T
 
 
-def zipf_bias(logits: np.ndarray, top_k: int, alpha: float = 1.1, seed: int = 0,
-              base_bias: np.ndarray | None = None) -> tuple[np.ndarray, np.ndarray, float]:
-    """Correction bias that skews sigmoid-select routing towards Zipf(alpha) expert loads.
+def zipf_targets(tokens: int, n_experts: int, top_k: int, alpha: float = 1.1) -> np.ndarray:
+    """Per-rank expert loads of a Zipf(alpha) skew over ``tokens * top_k`` routed pairs.
 
-    Experts get ranks from a seeded permutation; bias_e = c * log(p_rank(e)) with
-    p_r ∝ r^-alpha.  ``c`` is chosen on a grid to minimise the L1 distance between the
-    realised per-rank loads and the Zipf targets capped at T (a token picks an expert at
-    most once).  Returns (bias, realised loads by expert id, c)."""
+    p_r ∝ r^-alpha over ranks 1..E.  A token picks an expert at most once, so no load can
+    exceed ``tokens``: loads above it are capped and the excess is shared among the
+    uncapped ranks in proportion to p (repeated until no rank exceeds the cap).  The loads
+    are then rounded to integers summing to ``tokens * top_k`` (largest remainders first).
+    """
+    E, total = n_experts, tokens * top_k
+    if top_k > E:
+        raise ValueError("top_k exceeds the expert count")
+    p = np.arange(1, E + 1, dtype=np.float64) ** -alpha
+    p /= p.sum()
+    capped = np.zeros(E, dtype=bool)
+    t = p * total
+    while True:
+        over = (t > tokens) & ~capped
+        if not over.any():
+            break
+        capped |= over
+        rest = total - tokens * int(capped.sum())
+        t = np.where(capped, float(tokens), p / p[~capped].sum() * rest)
+    loads = np.floor(t).astype(np.int64)
+    frac = np.where(loads < tokens, t - loads, -1.0)
+    loads[np.argsort(-frac, kind="stable")[: total - int(loads.sum())]] += 1
+    return loads
+
+
+def zipf_bias(logits: np.ndarray, top_k: int, alpha: float = 1.1, seed: int = 0,
+              base_bias: np.ndarray | None = None, max_iters: int = 400
+              ) -> tuple[np.ndarray, np.ndarray, dict]:
+    """Per-expert correction bias that makes sigmoid-select routing of these tokens give
+    Zipf(alpha) expert loads (``zipf_targets``, capped and renormalised).
+
+    Experts get Zipf ranks from a seeded permutation.  With s = sigmoid(logits), token t
+    selects expert e iff s[t, e] + b[e] is among its ``top_k`` largest keys, i.e. iff
+    b[e] > theta[t, e] = (the k-th largest key of t among the other experts) - s[t, e].
+    Given the other biases, the b[e] that gives expert e exactly its target load n_e lies
+    between the n_e-th and (n_e + 1)-th smallest theta[:, e]; each sweep moves every b[e]
+    halfway to the midpoint of that interval (all experts at once) and keeps the bias
+    with the smallest L1 distance between realised and target loads.  Midpoints keep the
+    selection away from the tie boundaries, so device logits (fp32 sums in another order)
+    route the same way.  Returns (bias fp32, realised loads by expert id, info) with
+    ``info`` = {"target": loads by expert id, "l1": L1 distance, "iters": sweeps run}.
+    """
     T, E = logits.shape
+    k = top_k
     rng = np.random.default_rng(seed)
     rank_of = np.empty(E, dtype=np.int64)
     rank_of[rng.permutation(E)] = np.arange(E)
-    p = (np.arange(1, E + 1, dtype=np.float64)) ** -alpha
-    p /= p.sum()
-    target = np.minimum(p * T * top_k, T)
-    scores = 1.0 / (1.0 + np.exp(-logits.astype(np.float64)))
-    b0 = np.zeros(E) if base_bias is None else base_bias.astype(np.float64)
+    target = zipf_targets(T, E, k, alpha)[rank_of]
+    s = 1.0 / (1.0 + np.exp(-logits.astype(np.float64)))
+    b = np.zeros(E) if base_bias is None else base_bias.astype(np.float64).copy()
+    cols = np.arange(E)
     best = None
-    for c in np.linspace(0.0, 0.3, 61):
-        bias = b0 + c * np.log(p[rank_of])
-        key = scores + bias
-        ids = np.argpartition(-key, top_k, axis=-1)[:, :top_k]
-        loads = np.bincount(ids.ravel(), minlength=E)
-        err = np.abs(loads[np.argsort(rank_of)] - target).sum()
-        if best is None or err < best[0]:
-            best = (err, bias, loads, c)
-    _, bias, loads, c = best
-    return bias.astype(np.float32), loads, float(c)
+    it = 0
+    for it in range(max_iters):
+        bias32 = b.astype(np.float32)
+        key = s + bias32.astype(np.float64)
+        part = np.partition(-key, (k - 1, k), axis=1)
+        kth, k1th = -part[:, k - 1], -part[:, k]
+        chosen = key >= kth[:, None]
+        loads = chosen.sum(axis=0)
+        l1 = int(np.abs(loads - target).sum())
+        if best is None or l1 < best[0]:
+            best = (l1, bias32, loads)
+        if l1 == 0:
+            break
+        theta = np.sort(np.where(chosen, k1th[:, None], kth[:, None]) - s, axis=0)
+        lo = np.where(target > 0, theta[np.clip(target - 1, 0, T - 1), cols], theta[0] - 1e-3)
+        hi = np.where(target < T, theta[np.clip(target, 0, T - 1), cols], theta[-1] + 1e-3)
+        b += 0.5 * (0.5 * (lo + hi) - b)
+    l1, bias32, loads = best
+    return bias32, loads, {"target": target, "l1": l1, "iters": it + 1}
+
+
+def zipf_summary(loads: np.ndarray, target: np.ndarray, tokens: int, top_k: int) -> dict:
+    """Realised loads against the Zipf targets, with the workload's acceptance checks:
+    every expert active, the hottest at >= 95 % of the token count, L1 distance <= 10 %
+    of the routed pairs."""
+    loads = np.asarray(loads, dtype=np.int64)
+    srt = np.sort(loads)[::-1]
+    l1 = int(np.abs(loads - np.asarray(target)).sum())
+    out = {"n_active": int((loads > 0).sum()), "max_load": int(srt[0]),
+           "min_load": int(srt[-1]), "median_load": float(np.median(srt)),
+           "top5": srt[:5].tolist(), "target_top5": np.sort(target)[::-1][:5].tolist(),
+           "l1": l1, "l1_frac": l1 / float(tokens * top_k)}
+    out["ok"] = bool(out["n_active"] == loads.size and srt[0] >= 0.95 * tokens
+                     and out["l1_frac"] <= 0.10)
+    return out
 
 
 def synthetic_host_params(shape: MoeShape, seed: int) -> dict[str, np.ndarray]:

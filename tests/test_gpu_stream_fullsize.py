@@ -1,6 +1,7 @@
-"""The layer stream at full size: per-row int8 GLM-4.7 layers (3.8 GB each) in pinned host
-memory, streamed through OffloadRuntime with a lookahead-2 scheduler, the device buffer
-pool and the MI355X GLM4-MoE executor, both with whole-layer copies and with the
+"""The layer stream at full size: eight per-row int8 GLM-4.7 layers (3.8 GB each) in pinned
+host memory, streamed through OffloadRuntime with a lookahead-2 scheduler, the device
+buffer pool (three 3.8 GB buffers, each reused while copies into the others are in
+flight) and the MI355X GLM4-MoE executor, both with whole-layer copies and with the
 expert-granular transfer (non-expert bytes ahead, each layer's routed experts after its
 router ran), at 1 and 16 tokens (runtime.py:121-198, lookahead.py:6-23).
 
@@ -32,7 +33,7 @@ from oracle import moe_oracle as orc
 
 pytestmark = pytest.mark.gpu
 
-N_LAYERS = 3
+N_LAYERS = 8  # the streaming benchmark's chain: 8 layers, 3 pooled device buffers reused
 LOWP_ABS = 2e-2
 SEED = 2126  # the streaming benchmark's first layer seed
 PROJ = ("gate_proj", "up_proj", "down_proj")
@@ -101,6 +102,7 @@ def int8_stream(mi355x, stream):
                 layers.append(dl.layer)
             finally:
                 dl.close()
+            say(f"    layer {i} in pinned memory ({dl.layer.nbytes / 1e9:.2f} GB)")
         yield layers, blobs
     finally:
         for pin in blobs.values():
@@ -124,6 +126,9 @@ def test_int8_layer_stream_matches_oracle(mi355x, int8_stream, T):
                             expert_granular=mode == "experts")
         try:
             out, metrics = rt.run_inference(list(range(N_LAYERS)), x)
+            # lookahead 2: three layer buffers in use at once, each later layer reuses one
+            # whose previous layer's compute may still run when its copy is enqueued
+            assert (rt._pool.misses, rt._pool.hits) == (3, N_LAYERS - 3)
         finally:
             rt.close()
             ex.ex.close()
