@@ -450,6 +450,73 @@ def stream_case(backend, shape: syn.MoeShape, tokens: tuple[int, ...], n_layers:
     return out
 
 
+def dropin_case(backend, stream, dlayers: list[DeviceMoeLayer], shape: syn.MoeShape,
+                mode: int, tokens: tuple[int, ...], layout_name: str, steps: int,
+                prefix: str) -> dict[str, dict]:
+    """The drop-in path on resident layers: OffloadRuntime (DeviceResidentStorage, nothing
+    copied) driving the package's executor through ``run_layer``, as the reference runtime
+    drives its executors (runtime.py:169-180), against the block alone (``Case``) on the
+    same layers.  Two executor modes: NumPy activations in and out of every layer (the
+    reference contract) and activations kept on the device between layers
+    (``device_activations=True``).  Per layer: device time (two events around the whole
+    chain on the runtime's compute stream, divided by the layer calls) and host wall time
+    (the chain ends with one synchronisation)."""
+    from moe_mi355x.executors import GLM4MoeExecutor, Qwen3NextExecutor
+    from moe_mi355x.runtime import OffloadRuntime
+    from moe_mi355x.scheduler import LookaheadScheduler
+    from moe_mi355x.storage import DeviceResidentStorage
+    from moe_mi355x.types import LayerSpec
+
+    b = backend
+    specs = [LayerSpec(dl.layer.layer_id, dl.layer.name, dl.layer.nbytes,
+                       {**dl.layer.metadata, "weight_layout": layout_name, "is_moe": True})
+             for dl in dlayers]
+    storage = DeviceResidentStorage({sp.layer_id: dl.buf for sp, dl in zip(specs, dlayers)})
+    ids = [sp.layer_id for sp in specs]
+    make = GLM4MoeExecutor if shape.arch == syn.GLM else Qwen3NextExecutor
+    out: dict[str, dict] = {}
+    for T in tokens:
+        x = syn.make_inputs(SEED + 77 + T, T, shape.hidden)
+        block = Case(b, stream, dlayers, shape, "float16", T, mode, x).run(steps, 5)
+        row = {"workload": f"{prefix}_t{T}_{layout_name}", "tokens": T,
+               "layers": len(ids), "weight_layout": layout_name,
+               "block_ms": round(block["ms_per_step"], 4)}
+        outs = {}
+        for act in ("numpy", "device"):
+            ex = make(shape.config(), router_mode=mode, max_tokens=T,
+                      device_activations=act == "device")
+            rt = OffloadRuntime(specs, b, storage, LookaheadScheduler(2), ex, event_timing=False)
+            try:
+                rt.run_inference(ids, x)  # warm-up: workspace, pointer tables
+                order = ids * max(1, steps // len(ids))
+                e0, e1 = b.create_timing_event(), b.create_timing_event()
+                b.synchronize_stream(rt.compute_stream)
+                b.record(e0, rt.compute_stream)
+                t0 = time.perf_counter()
+                y, _ = rt.run_inference(order, x)
+                wall = time.perf_counter() - t0
+                b.record(e1, rt.compute_stream)
+                b.event_synchronize(e1)
+                dev_ms = b.elapsed_ms(e0, e1) / len(order)
+                b.destroy_event(e0)
+                b.destroy_event(e1)
+            finally:
+                rt.close()
+                ex.close()
+            outs[act] = y
+            row[f"{act}_device_ms_per_layer"] = round(dev_ms, 4)
+            row[f"{act}_wall_ms_per_layer"] = round(wall * 1e3 / len(order), 4)
+        row["equal_outputs"] = bool(np.array_equal(outs["numpy"], outs["device"]))
+        row["device_over_block"] = round(row["device_device_ms_per_layer"] / row["block_ms"], 3)
+        row["numpy_over_block"] = round(row["numpy_device_ms_per_layer"] / row["block_ms"], 3)
+        out[row["workload"]] = row
+        log(f"{row['workload']}: block {row['block_ms']} ms; run_layer per layer "
+            f"device-activations {row['device_device_ms_per_layer']} ms (wall "
+            f"{row['device_wall_ms_per_layer']}), NumPy {row['numpy_device_ms_per_layer']} ms "
+            f"(wall {row['numpy_wall_ms_per_layer']})")
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -489,7 +556,8 @@ def main() -> int:
     def want(name: str) -> bool:
         return only is None or only == name
 
-    def build_layers(shape: syn.MoeShape, wdt: str, n: int) -> list[DeviceMoeLayer]:
+    def build_layers(shape: syn.MoeShape, wdt: str, n: int,
+                     layout: str | None = None) -> list[DeviceMoeLayer]:
         """Layer 0 from SEED (the layer the parity checks and the single-layer workloads
         use), layers 1.. from other seeds (other routing, other weights)."""
         t0 = time.perf_counter()
@@ -498,7 +566,7 @@ def main() -> int:
             lay = DeviceMoeLayer.synthetic(backend, shape, SEED + LAYER_SEED_STEP * i, stream,
                                            weight_dtype=wdt, param_dtype="float32",
                                            layer_id=i)
-            if args.weight_layout == "frag16":
+            if (layout or args.weight_layout) == "frag16":
                 lay.tile()
             out.append(lay)
         log(f"{shape.arch} {wdt}: {n} layer(s) of {out[0].layer.nbytes / 1e9:.2f} GB built on "
@@ -610,6 +678,27 @@ def main() -> int:
             log(f"{name}: {sweep[name]['tokens_per_s']} tok/s")
         for lay in layers:
             lay.close()
+
+    # ---- the drop-in path: OffloadRuntime + executors on resident layers ---------------------
+    if not args.no_sweep and (only is None or only.startswith("dropin")):
+        k = min(args.steps, 40)
+        for lay_name in ("frag16", "rows"):
+            if only is not None and not only.endswith(lay_name):
+                continue
+            if only is None or only.startswith("dropin_glm47"):
+                layers = build_layers(G, "float16", nl, layout=lay_name)
+                sweep.update(dropin_case(backend, stream, layers, G,
+                                         _lib.MX_ROUTER_SIGMOID_SELECT_BIAS, (1, 32), lay_name,
+                                         k, "dropin_glm47_fp16"))
+                for lay in layers:
+                    lay.close()
+            if lay_name == "frag16" and (only is None or only.startswith("dropin_qwen3next")):
+                Q = syn.QWEN3_NEXT
+                layers = build_layers(Q, "float16", nl, layout=lay_name)
+                sweep.update(dropin_case(backend, stream, layers, Q, _lib.MX_ROUTER_SOFTMAX,
+                                         (1, 32), lay_name, k, "dropin_qwen3next_fp16"))
+                for lay in layers:
+                    lay.close()
 
     # ---- Qwen3-Next linear-attention (Gated DeltaNet) block -------------------------------------
     if not args.no_sweep and (only is None or only.startswith("qwen3next_linattn")):

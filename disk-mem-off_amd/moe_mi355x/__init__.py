@@ -3,6 +3,7 @@
 Compute runs only in ``libmoe_mi355x.so`` (HIP kernels, C ABI, see include/moe_mi355x.h);
 this package is the host side: backend, pools, runtime, layer layout and executors.
 """
+from .activations import DeviceActivations
 from .backends import DeviceBackend, MI355XBackend, ROCmBackend, detect_backend
 from .buffer_pool import DeviceBufferPool
 from .pinned_pool import PinnedHostBufferPool
@@ -14,11 +15,12 @@ from .quantize import (CompositeDequantizer, Float16Dequantizer, Int8Dequantizer
                        dequantize_rows_int8, quantize_moe_tensors, quantize_rows_int8)
 from .runtime import LayerExecutor, LayerMetrics, OffloadRuntime, RuntimeMetrics
 from .scheduler import LookaheadScheduler, PrefetchScheduler
-from .storage import InMemoryStorage, LayerStorage
+from .storage import DeviceResidentStorage, InMemoryStorage, LayerStorage
 from .types import DeviceBuffer, HostBuffer, LayerSpec
 
 __all__ = [
-    "CompositeDequantizer", "DeviceBackend", "DeviceBuffer", "DeviceBufferPool",
+    "CompositeDequantizer", "DeviceActivations", "DeviceBackend", "DeviceBuffer",
+    "DeviceBufferPool", "DeviceResidentStorage",
     "Float16Dequantizer", "GLM4MoeExecutor", "HostBuffer", "InMemoryStorage", "Int8Dequantizer",
     "LayerExecutor", "LayerMetrics", "LayerSpec", "LayerStorage", "LookaheadScheduler",
     "MI355XBackend", "MoeConfig", "MoeLayerLayout", "MoeRunner",

@@ -23,7 +23,10 @@ of the MoE path either: pass ``dense=callable`` with the same signature as ``att
 reference's ``_dense_mlp_block``, glm4_moe.py:166-172).
 
 Before ``run_layer`` returns, the compute stream is synchronised: the runtime frees or
-re-pools ``device_weights`` right after the call (runtime.py:180).
+re-pools ``device_weights`` right after the call (runtime.py:180).  Under a runtime that
+fences buffer reuse with events (``stream_ordered``, set by ``moe_mi355x.OffloadRuntime``)
+and with ``device_activations=True``, ``run_layer`` returns without waiting: the output
+stays on the device as ``DeviceActivations`` and the next layer reads it in place.
 """
 from __future__ import annotations
 
@@ -35,6 +38,7 @@ from . import _lib
 from .layout import NORM, MoeLayerLayout
 from .full_attn import FullAttnLayout, FullAttnRunner, has_full_attn
 from .linear_attn import LinearAttnLayout, LinearAttnRunner, has_linear_attn
+from .activations import DeviceActivations
 from .moe import MoeConfig, MoeRunner
 from .types import DeviceBuffer, HostBuffer, LayerSpec
 
@@ -128,12 +132,20 @@ class _MoeExecutorBase:
 
     def __init__(self, config: dict[str, Any], *, router_mode: int | str | None = None,
                  attention: AttentionFn | None = None, dense: AttentionFn | None = None,
-                 max_tokens: int = 32) -> None:
+                 max_tokens: int = 32, device_activations: bool = False) -> None:
         self.hidden_size = int(config["hidden_size"])
         self.router_mode = router_mode if router_mode is not None else self._router_default
         self.attention = attention
         self.dense = dense
         self.max_tokens = max_tokens
+        # run_layer returns DeviceActivations (the next layer reads them in place) instead
+        # of NumPy; inputs may be either in both modes.
+        self.device_activations = bool(device_activations)
+        # Set by a runtime that records an event on the compute stream after run_layer and
+        # fences every reuse or free of the layer buffer on it (moe_mi355x.OffloadRuntime
+        # does).  The reference runtime frees the buffer right after run_layer returns
+        # (runtime.py:180), so by default run_layer waits for its device work.
+        self.stream_ordered = False
         self._runner: MoeRunner | None = None
         self._layouts: dict[int, tuple[list, MoeLayerLayout]] = {}
         self._la_runner: LinearAttnRunner | None = None
@@ -158,10 +170,16 @@ class _MoeExecutorBase:
         self._layouts[layer.layer_id] = (meta, lay)
         return lay
 
-    def moe_config(self, layout: MoeLayerLayout) -> MoeConfig:
+    def moe_config(self, layout: MoeLayerLayout, layer: LayerSpec | None = None) -> MoeConfig:
+        """Block configuration; a layer whose expert matrices were re-laid in the
+        fragment layout on the device says so with ``metadata["weight_layout"] = "frag16"``."""
+        wl = _lib.MX_LAYOUT_ROWS
+        if layer is not None and layer.metadata.get("weight_layout", "rows") == "frag16":
+            wl = _lib.MX_LAYOUT_FRAG16
         return MoeConfig.from_layout(layout, top_k=self.top_k, router_mode=self.router_mode,
                                      norm_topk_prob=self.norm_topk_prob,
-                                     routed_scaling=self.routed_scaling, eps=self.rms_norm_eps)
+                                     routed_scaling=self.routed_scaling, eps=self.rms_norm_eps,
+                                     weight_layout=wl)
 
     def moe_block(self, layer: LayerSpec, x: np.ndarray, device_weights: DeviceBuffer,
                   backend: Any, stream: Any, pre: Callable[[int, int], None] | None = None
@@ -175,14 +193,23 @@ class _MoeExecutorBase:
             raise RuntimeError(f"Layer {layer.layer_id}: device buffer size "
                                f"{device_weights.nbytes} < expected {layer.nbytes}")
         layout = self._layout(layer)
-        cfg = self.moe_config(layout)
+        cfg = self.moe_config(layout, layer)
         desc = cfg.desc()
         if self._runner is None:
             self._runner = MoeRunner(backend)
-        T = int(np.shape(x)[0])
+        T = len(x)
         self._runner.reserve(desc, max(T, self.max_tokens, 1))
         weights = self._runner.bind(layout, int(device_weights.handle), stream)
-        return self._runner.forward_numpy(desc, weights, x, stream, pre=pre)
+        out = self._runner.forward_numpy(desc, weights, x, stream, pre=pre,
+                                         keep_on_device=self.device_activations)
+        return self._fence(out, backend, stream)
+
+    def _fence(self, out: Any, backend: Any, stream: Any) -> Any:
+        """Device output under a caller that does not fence buffer reuse: wait for the
+        device work before the layer buffer can be freed (NumPy output already waited)."""
+        if isinstance(out, DeviceActivations) and not self.stream_ordered:
+            backend.synchronize_stream(stream)
+        return out
 
     def moe_block_granular(self, layer: LayerSpec, x: np.ndarray, device_weights: DeviceBuffer,
                            backend: Any, stream: Any, fetch: Callable[[list[int]], None],
@@ -197,15 +224,17 @@ class _MoeExecutorBase:
             raise RuntimeError(f"Layer {layer.layer_id}: device buffer size "
                                f"{device_weights.nbytes} < expected {layer.nbytes}")
         layout = self._layout(layer)
-        desc = self.moe_config(layout).desc()
+        desc = self.moe_config(layout, layer).desc()
         if self._runner is None:
             self._runner = MoeRunner(backend)
-        T = int(np.shape(x)[0])
+        T = len(x)
         self._runner.reserve(desc, max(T, self.max_tokens, 1))
         weights = self._runner.bind(layout, int(device_weights.handle), stream)
         active = self._runner.route_numpy(desc, weights, x, stream, pre=pre)
         fetch(active)
-        return self._runner.finish_numpy(desc, weights, stream)
+        out = self._runner.finish_numpy(desc, weights, stream,
+                                        keep_on_device=self.device_activations)
+        return self._fence(out, backend, stream)
 
     def expert_ranges(self, layer: LayerSpec) -> tuple[list[tuple[int, int]], list[tuple[int, int]]]:
         """(core byte ranges, per-routed-expert byte ranges) of a packed MoE layer."""
@@ -217,7 +246,8 @@ class _MoeExecutorBase:
         """Run (host hook) or schedule (device block, returned as a ``pre`` hook) the
         layer's attention part."""
         if self.attention is not None:
-            return self.attention(x, layer, device_weights, backend, stream), None
+            return self.attention(np.asarray(x, dtype=np.float32), layer, device_weights,
+                                  backend, stream), None
         pre = self._device_attention(layer, device_weights, backend, stream)
         if pre is None and not self._moe_only(layer):
             raise NotImplementedError(
@@ -231,18 +261,27 @@ class _MoeExecutorBase:
     def run_layer_granular(self, layer: LayerSpec, activations: Any, device_weights: DeviceBuffer,
                            backend: Any, stream: Any, fetch: Callable[[list[int]], None]) -> Any:
         """``run_layer`` for a layer whose routed experts are copied on demand."""
-        x, pre = self._attention(layer, np.asarray(activations, dtype=np.float32),
-                                 device_weights, backend, stream)
+        x, pre = self._attention(layer, self._as_input(activations), device_weights, backend,
+                                 stream)
         return self.moe_block_granular(layer, x, device_weights, backend, stream, fetch, pre=pre)
 
     def is_moe_layer(self, layer: LayerSpec) -> bool:
         """Whether the layer's MLP is the MoE block (else a dense MLP)."""
         return True
 
+    @staticmethod
+    def _as_input(activations: Any) -> Any:
+        if isinstance(activations, DeviceActivations):
+            return activations
+        return np.asarray(activations, dtype=np.float32)
+
     def run_layer(self, layer: LayerSpec, activations: Any, device_weights: DeviceBuffer,
                   backend: Any, stream: Any) -> Any:
-        x, pre = self._attention(layer, np.asarray(activations, dtype=np.float32),
-                                 device_weights, backend, stream)
+        """The reference contract (runtime.py:15-26): the layer's output activations.
+        ``activations`` may be NumPy or ``DeviceActivations``; the result is NumPy, or
+        ``DeviceActivations`` for an executor built with ``device_activations=True``."""
+        x, pre = self._attention(layer, self._as_input(activations), device_weights, backend,
+                                 stream)
         if not self.is_moe_layer(layer):
             if self.dense is None:
                 raise NotImplementedError(
@@ -250,8 +289,8 @@ class _MoeExecutorBase:
                     "pass dense=... (for example host_dense(fn)) to run it")
             if pre is not None:
                 raise NotImplementedError("a dense MLP after a device attention block")
-            return np.asarray(self.dense(x, layer, device_weights, backend, stream),
-                              dtype=np.float32)
+            return np.asarray(self.dense(np.asarray(x, dtype=np.float32), layer,
+                                         device_weights, backend, stream), dtype=np.float32)
         return self.moe_block(layer, x, device_weights, backend, stream, pre=pre)
 
     @staticmethod

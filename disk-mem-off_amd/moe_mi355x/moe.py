@@ -1,10 +1,11 @@
 """Host driver of the device MoE block: configuration, workspace, pointer tables, I/O.
 
 ``MoeConfig`` carries the executor config keys of the reference (glm4_moe.py:70-84,
-qwen3_next.py:126-133) plus the two choices the reference does not expose: the router
-mode and the expert weight format.  ``MoeRunner`` owns the device workspace, the expert
-pointer table and pinned staging for NumPy inputs/outputs, and calls ``mx_moe_forward``.
-All allocation happens in ``reserve``/``bind``; ``forward_device`` allocates nothing.
+qwen3_next.py:126-133) plus the choices the reference does not expose: the router mode,
+the expert weight format and layout.  ``MoeRunner`` owns the device workspace, the expert
+pointer tables, the device activation buffers and pinned staging for NumPy inputs/outputs,
+and calls ``mx_moe_forward``.  Allocation happens in ``reserve`` and at a table's first
+``bind``; ``forward_device`` allocates nothing.
 """
 from __future__ import annotations
 
@@ -15,6 +16,7 @@ from typing import Any, Callable
 import numpy as np
 
 from . import _lib
+from .activations import DeviceActivations
 from .backends import MI355XBackend
 from .layout import MoeLayerLayout
 from .types import DeviceBuffer
@@ -100,76 +102,112 @@ def workspace_bytes(desc: _lib.MxMoeDesc, tokens: int) -> int:
 
 
 class MoeRunner:
-    """Device resources for running MoE blocks of one shape family on one stream."""
+    """Device resources for running MoE blocks of one shape family on one stream.
+
+    * workspace (``reserve``), sized by ``mx_moe_workspace_size``;
+    * one expert pointer table per (layer layout, buffer address), uploaded at its first
+      ``bind`` and kept (a layer streamed through a pool of k buffers has at most k);
+    * activations: an input buffer (NumPy inputs are uploaded into it through pinned
+      staging) and two output buffers used in turn, so a layer's output can be handed to the
+      next layer on the device (``DeviceActivations``) while that layer writes the other.
+    """
+
+    MAX_TABLES = 256
+    _SLOTS = ("x", "out", "out2")  # generation-counted device activation buffers
 
     def __init__(self, backend: MI355XBackend) -> None:
         self.backend = backend
         self.lib = _lib.load()
         self._ws: DeviceBuffer | None = None
-        self._table_dev: DeviceBuffer | None = None
-        # The layout object and buffer address the uploaded pointer table was built from;
-        # the layout is held by reference so a new layout can never be taken for it.
-        self._table_layout: MoeLayerLayout | None = None
-        self._table_base: int | None = None
-        self._table_ev: Any = None
+        # (id(layout), base) -> (layout, device table); the layout is held so its id cannot
+        # be reused by another layout while the entry lives.
+        self._tables: dict[tuple[int, int], tuple[MoeLayerLayout, DeviceBuffer]] = {}
+        self._table_ev: Any = None   # last table upload (reads the pinned staging copy)
+        self._x_ev: Any = None       # last upload of x (reads the pinned staging copy)
         self._io: dict[str, DeviceBuffer] = {}
         self._pinned: dict[str, Any] = {}
-        self._split_tokens = 0
+        self._gen = [0, 0, 0]
+        self._next_out = 1
+        self._closed = False
+        self._last_stream: Any = None
+        # tokens, output slot and input address of the last route_numpy
+        self._split: tuple[int, int, int] = (0, 1, 0)
+
+    def generation(self, slot: int) -> int:
+        return -1 if self._closed else self._gen[slot]
 
     # -- allocation (never called from forward_device) --
+    def _quiesce(self) -> None:
+        """Wait for the work that may still read buffers about to be freed."""
+        if self._last_stream is not None:
+            self.backend.synchronize_stream(self._last_stream)
+
     def reserve(self, desc: _lib.MxMoeDesc, tokens: int) -> None:
         need = workspace_bytes(desc, tokens)
         if self._ws is None or self._ws.nbytes < need:
+            self._quiesce()
             if self._ws is not None:
                 self.backend.free_device(self._ws)
             self._ws = self.backend.alloc_device(need)
         nbytes_act = tokens * desc.hidden * 4
-        for key in ("x", "out"):
+        for i, key in enumerate(self._SLOTS):
             buf = self._io.get(key)
             if buf is None or buf.nbytes < nbytes_act:
+                self._quiesce()
                 if buf is not None:
                     self.backend.free_device(buf)
                 self._io[key] = self.backend.alloc_device(max(nbytes_act, 16))
+                self._gen[i] += 1  # handles to the old buffer are stale
+        for key in ("x", "out"):
             pin = self._pinned.get(key)
             if pin is None or pin.nbytes < nbytes_act:
+                self._quiesce()
+                self._wait(("_x_ev",))
                 if pin is not None:
                     self.backend.free_pinned_host(pin)
                 self._pinned[key] = self.backend.alloc_pinned_host(max(nbytes_act, 16))
 
     def bind(self, layout: MoeLayerLayout, base: int, stream: Any) -> _lib.MxMoeWeights:
-        """Upload the expert pointer table for a layer buffer at ``base`` (cached while the
-        same layout object is bound at the same address)."""
+        """Weights of the layer buffer at ``base``; its expert pointer table is uploaded on
+        ``stream`` the first time this layout is bound at this address."""
+        self._last_stream = stream
+        key = (id(layout), int(base))
+        hit = self._tables.get(key)
+        if hit is not None and hit[0] is layout:
+            return layout.weights(base, hit[1].handle)
+        if len(self._tables) >= self.MAX_TABLES:
+            self._quiesce()
+            self._wait(("_table_ev",))
+            for _, dev in self._tables.values():
+                self.backend.free_device(dev)
+            self._tables.clear()
         nbytes = ctypes.sizeof(_lib.MxExpertPtrs) * (layout.n_experts + 1)
-        if self._table_dev is None or self._table_dev.nbytes < nbytes:
-            self._wait_table_upload()
-            if self._table_dev is not None:
-                self.backend.free_device(self._table_dev)
-            self._table_dev = self.backend.alloc_device(nbytes)
-            self._table_layout = self._table_base = None
-            pin = self._pinned.pop("table", None)
+        pin = self._pinned.get("table")
+        if pin is None or pin.nbytes < nbytes:
+            self._wait(("_table_ev",))
             if pin is not None:
                 self.backend.free_pinned_host(pin)
-            self._pinned["table"] = self.backend.alloc_pinned_host(nbytes)
-        if self._table_layout is not layout or self._table_base != base:
-            table = layout.expert_table(base)
-            pin = self._pinned["table"]
-            # The previous upload may still be reading the pinned staging copy.
-            self._wait_table_upload()
-            ctypes.memmove(ctypes.addressof(ctypes.c_char.from_buffer(pin.view)), table, nbytes)
-            self.backend.copy_h2d_ptr_async(self._table_dev.handle,
-                                            ctypes.addressof(ctypes.c_char.from_buffer(pin.view)),
-                                            nbytes, stream)
-            self._table_ev = self.backend.record_event(stream)
-            self._table_layout, self._table_base = layout, base
-        return layout.weights(base, self._table_dev.handle)
+            pin = self._pinned["table"] = self.backend.alloc_pinned_host(max(nbytes, 4096))
+        dev = self.backend.alloc_device(nbytes)
+        table = layout.expert_table(base)
+        # The previous upload may still be reading the pinned staging copy.
+        self._wait(("_table_ev",))
+        addr = ctypes.addressof(ctypes.c_char.from_buffer(pin.view))
+        ctypes.memmove(addr, table, nbytes)
+        self.backend.copy_h2d_ptr_async(dev.handle, addr, nbytes, stream)
+        self._table_ev = self.backend.record_event(stream)
+        self._tables[key] = (layout, dev)
+        return layout.weights(base, dev.handle)
 
-    def _wait_table_upload(self) -> None:
-        if self._table_ev is not None:
-            sync = getattr(self.backend, "event_synchronize", None)
-            if sync is not None:
-                sync(self._table_ev)
-            self.backend.destroy_event(self._table_ev)
-            self._table_ev = None
+    def _wait(self, names: tuple[str, ...]) -> None:
+        for name in names:
+            ev = getattr(self, name)
+            if ev is not None:
+                sync = getattr(self.backend, "event_synchronize", None)
+                if sync is not None:
+                    sync(ev)
+                self.backend.destroy_event(ev)
+                setattr(self, name, None)
 
     # -- hot path --
     def forward_device(self, desc: _lib.MxMoeDesc, weights: _lib.MxMoeWeights, x: int, out: int,
@@ -188,76 +226,126 @@ class MoeRunner:
                                                   arr, len(events))
         _lib.check(rc, "mx_moe_forward")
 
-    def forward_numpy(self, desc: _lib.MxMoeDesc, weights: _lib.MxMoeWeights, x: np.ndarray,
-                      stream: Any, pre: Callable[[int, int], None] | None = None) -> np.ndarray:
-        """Host fp32 [T, H] in, host fp32 [T, H] out; synchronises ``stream``.  ``pre(x_dev,
-        T)``, when given, runs on ``stream`` after the upload and rewrites the device copy of
-        x in place (for example the layer's attention block) before the MoE block reads it."""
+    def _stage_input(self, desc: _lib.MxMoeDesc, x: Any, stream: Any,
+                     pre: Callable[[int, int], None] | None,
+                     fence: bool = False) -> tuple[int, int, int | None]:
+        """Put the activations on the device; returns (tokens, device address, slot of that
+        buffer or None for a caller-owned one).  NumPy goes up through pinned staging.  A
+        ``DeviceActivations`` is read in place, or, when ``pre`` rewrites it, first copied
+        into the input buffer so the caller's rows stay intact.  ``fence``: the call will not
+        synchronise ``stream``, so the upload's end is recorded before the staging copy is
+        written again."""
+        self._last_stream = stream
+        if isinstance(x, DeviceActivations):
+            x.check()
+            T, H = x.shape
+            if H != desc.hidden:
+                raise ValueError(f"activations must be [T, {desc.hidden}], got {x.shape}")
+            self.reserve(desc, max(T, 1))
+            if T and x.stream is not None and x.stream != stream:
+                # produced on another stream: order this stream after it
+                ev = self.backend.record_event(x.stream)
+                self.backend.wait_event(stream, ev)
+                self.backend.destroy_event(ev)
+            if pre is None:
+                return T, x.ptr, self._slot_of(x)
+            if T:
+                _lib.check(self.lib.mx_memcpy_d2d_async(self._io["x"].handle, x.ptr, x.nbytes,
+                                                        stream), "hipMemcpyAsync")
+                pre(self._io["x"].handle, T)
+            return T, self._io["x"].handle, 0
         x = np.ascontiguousarray(x, dtype=np.float32)
         if x.ndim != 2 or x.shape[1] != desc.hidden:
             raise ValueError(f"activations must be [T, {desc.hidden}], got {x.shape}")
         T = x.shape[0]
         self.reserve(desc, max(T, 1))
+        if T:
+            px = self._pinned["x"]
+            self._wait(("_x_ev",))  # the previous upload may still read the staging copy
+            np.frombuffer(px.view, dtype=np.uint8, count=x.nbytes)[:] = x.view(np.uint8).ravel()
+            self.backend.copy_h2d_ptr_async(self._io["x"].handle,
+                                            ctypes.addressof(ctypes.c_char.from_buffer(px.view)),
+                                            x.nbytes, stream)
+            if fence:
+                self._x_ev = self.backend.record_event(stream)
+            if pre is not None:
+                pre(self._io["x"].handle, T)
+        return T, self._io["x"].handle, 0
+
+    def _slot_of(self, x: DeviceActivations) -> int | None:
+        return x._slot if x._owner is self else None
+
+    def _pick_out(self, in_slot: int | None) -> int:
+        slot = self._next_out
+        if slot == in_slot:
+            slot = 3 - slot
+        self._next_out = 3 - slot
+        return slot
+
+    def _finish(self, desc: _lib.MxMoeDesc, T: int, slot: int, stream: Any,
+                keep_on_device: bool) -> Any:
+        out_buf = self._io[self._SLOTS[slot]]
+        if keep_on_device:
+            return DeviceActivations(self, slot, self._gen[slot], out_buf.handle, T,
+                                     desc.hidden, stream)
         if T == 0:
-            return x.copy()
-        nb = x.nbytes
-        px, po = self._pinned["x"], self._pinned["out"]
-        np.frombuffer(px.view, dtype=np.uint8, count=nb)[:] = x.view(np.uint8).ravel()
-        addr_x = ctypes.addressof(ctypes.c_char.from_buffer(px.view))
+            return np.zeros((0, desc.hidden), np.float32)
+        nb = T * desc.hidden * 4
+        po = self._pinned["out"]
         addr_o = ctypes.addressof(ctypes.c_char.from_buffer(po.view))
-        self.backend.copy_h2d_ptr_async(self._io["x"].handle, addr_x, nb, stream)
-        if pre is not None:
-            pre(self._io["x"].handle, T)
-        self.forward_device(desc, weights, self._io["x"].handle, self._io["out"].handle, T, stream)
-        self.backend.copy_d2h_ptr_async(addr_o, self._io["out"].handle, nb, stream)
+        self.backend.copy_d2h_ptr_async(addr_o, out_buf.handle, nb, stream)
         self.backend.synchronize_stream(stream)
         return np.frombuffer(po.view, dtype=np.float32, count=T * desc.hidden).reshape(T, -1).copy()
 
+    def forward_numpy(self, desc: _lib.MxMoeDesc, weights: _lib.MxMoeWeights, x: Any,
+                      stream: Any, pre: Callable[[int, int], None] | None = None,
+                      keep_on_device: bool = False) -> Any:
+        """MoE block of ``x`` (host fp32 [T, H] or ``DeviceActivations``).  Returns host
+        fp32 [T, H] (synchronises ``stream``) or, with ``keep_on_device``, a
+        ``DeviceActivations`` without waiting for the device.  ``pre(x_dev, T)``, when
+        given, runs on ``stream`` on the device copy of x, rewriting it in place (for
+        example the layer's attention block) before the MoE block reads it."""
+        T, x_ptr, in_slot = self._stage_input(desc, x, stream, pre, fence=keep_on_device)
+        slot = self._pick_out(in_slot)
+        self._gen[slot] += 1  # handles to the previous contents of this buffer are stale
+        if T:
+            self.forward_device(desc, weights, x_ptr, self._io[self._SLOTS[slot]].handle, T,
+                                stream)
+        return self._finish(desc, T, slot, stream, keep_on_device)
+
     # -- split forward (router part, then the expert part after the experts are copied) --
-    def route_numpy(self, desc: _lib.MxMoeDesc, weights: _lib.MxMoeWeights, x: np.ndarray,
+    def route_numpy(self, desc: _lib.MxMoeDesc, weights: _lib.MxMoeWeights, x: Any,
                     stream: Any, pre: Callable[[int, int], None] | None = None) -> list[int]:
-        """Upload x (then ``pre`` as in ``forward_numpy``) and run stages 0..3 (RMSNorm,
+        """Stage x (then ``pre``) as ``forward_numpy`` does and run stages 0..3 (RMSNorm,
         router, top-k, dispatch); returns the routed experts the batch uses, ascending
         (synchronises ``stream``)."""
-        x = np.ascontiguousarray(x, dtype=np.float32)
-        if x.ndim != 2 or x.shape[1] != desc.hidden:
-            raise ValueError(f"activations must be [T, {desc.hidden}], got {x.shape}")
-        T = x.shape[0]
-        self.reserve(desc, max(T, 1))
-        self._split_tokens = T
+        T, x_ptr, in_slot = self._stage_input(desc, x, stream, pre)
+        slot = self._pick_out(in_slot)
+        self._gen[slot] += 1
+        self._split = (T, slot, x_ptr)
         if T == 0:
             return []
-        px = self._pinned["x"]
-        np.frombuffer(px.view, dtype=np.uint8, count=x.nbytes)[:] = x.view(np.uint8).ravel()
-        self.backend.copy_h2d_ptr_async(self._io["x"].handle,
-                                        ctypes.addressof(ctypes.c_char.from_buffer(px.view)),
-                                        x.nbytes, stream)
-        if pre is not None:
-            pre(self._io["x"].handle, T)
-        self._stages(desc, weights, T, 0, _lib.MX_STAGE_ROUTE_END, stream)
+        self._stages(desc, weights, T, x_ptr, slot, 0, _lib.MX_STAGE_ROUTE_END, stream)
         v = self.views(desc, T)
         ng = int(read_device(self.backend, v.n_groups, np.int32, 1, stream)[0])
         ge = read_device(self.backend, v.g_expert, np.int32, ng, stream)
         return sorted(int(e) for e in ge if e < desc.n_experts)
 
-    def finish_numpy(self, desc: _lib.MxMoeDesc, weights: _lib.MxMoeWeights,
-                     stream: Any) -> np.ndarray:
-        """Stages 4..6 for the batch of the last ``route_numpy``; synchronises ``stream``."""
-        T = self._split_tokens
-        nb = T * desc.hidden * 4
-        if T == 0:
-            return np.zeros((0, desc.hidden), np.float32)
-        self._stages(desc, weights, T, _lib.MX_STAGE_ROUTE_END, _lib.MX_N_STAGES, stream)
-        po = self._pinned["out"]
-        addr_o = ctypes.addressof(ctypes.c_char.from_buffer(po.view))
-        self.backend.copy_d2h_ptr_async(addr_o, self._io["out"].handle, nb, stream)
-        self.backend.synchronize_stream(stream)
-        return np.frombuffer(po.view, dtype=np.float32, count=T * desc.hidden).reshape(T, -1).copy()
+    def finish_numpy(self, desc: _lib.MxMoeDesc, weights: _lib.MxMoeWeights, stream: Any,
+                     keep_on_device: bool = False) -> Any:
+        """Stages 4..6 for the batch of the last ``route_numpy``; returns as
+        ``forward_numpy`` does."""
+        T, slot, x_ptr = self._split
+        if T:
+            self._stages(desc, weights, T, x_ptr, slot, _lib.MX_STAGE_ROUTE_END,
+                         _lib.MX_N_STAGES, stream)
+        return self._finish(desc, T, slot, stream, keep_on_device)
 
-    def _stages(self, desc, weights, T: int, begin: int, end: int, stream: Any) -> None:
+    def _stages(self, desc, weights, T: int, x_ptr: int, slot: int, begin: int, end: int,
+                stream: Any) -> None:
         ws = self._ws
         _lib.check(self.lib.mx_moe_forward_stages(ctypes.byref(desc), ctypes.byref(weights),
-                                                  self._io["x"].handle, self._io["out"].handle,
+                                                  x_ptr, self._io[self._SLOTS[slot]].handle,
                                                   T, ws.handle, ws.nbytes, begin, end, stream),
                    "mx_moe_forward_stages")
 
@@ -269,16 +357,19 @@ class MoeRunner:
         return v
 
     def close(self) -> None:
-        self._wait_table_upload()
-        for buf in [self._ws, self._table_dev, *self._io.values()]:
+        self._quiesce()
+        self._wait(("_table_ev", "_x_ev"))
+        bufs = [self._ws, *self._io.values(), *(dev for _, dev in self._tables.values())]
+        for buf in bufs:
             if buf is not None:
                 self.backend.free_device(buf)
         for pin in self._pinned.values():
             self.backend.free_pinned_host(pin)
-        self._ws = self._table_dev = None
-        self._table_layout = self._table_base = None
+        self._ws = None
+        self._tables.clear()
         self._io.clear()
         self._pinned.clear()
+        self._closed = True
 
 
 def read_device(backend: MI355XBackend, ptr: int, dtype: Any, count: int, stream: Any = None) -> np.ndarray:

@@ -22,6 +22,7 @@ from dataclasses import dataclass, field
 from typing import Any, Protocol
 
 from .backends import DeviceBackend
+from .activations import DeviceActivations
 from .buffer_pool import DeviceBufferPool
 from .pinned_pool import PinnedHostBufferPool
 from .scheduler import PrefetchScheduler
@@ -104,6 +105,7 @@ class _Inflight:
     t_end: Any = None
     granular: bool = False  # routed experts are copied on demand
     extra_copies: list = field(default_factory=list)  # timing events of on-demand copies
+    resident: bool = False  # the storage handed over a device buffer it keeps
 
 
 class OffloadRuntime:
@@ -119,6 +121,7 @@ class OffloadRuntime:
         dequantizer: Any | None = None,
         transfer_lookahead: int | None = None,
         expert_granular: bool = False,
+        event_timing: bool = True,
     ) -> None:
         self.layers = {layer.layer_id: layer for layer in layers}
         self.backend = backend
@@ -137,7 +140,12 @@ class OffloadRuntime:
         if transfer_lookahead < 0:
             raise ValueError("transfer_lookahead must be >= 0")
         self.transfer_lookahead = transfer_lookahead
-        self._timing = hasattr(backend, "create_timing_event")
+        self._timing = bool(event_timing) and hasattr(backend, "create_timing_event")
+        # Every buffer this runtime frees or re-pools after run_layer is fenced by an event
+        # recorded on the compute stream after the call, so an executor that can return
+        # before its device work ends may do so.
+        if hasattr(executor, "stream_ordered"):
+            executor.stream_ordered = True
         self._deferred_free: list[tuple[DeviceBuffer, Any]] = []
         # Expert-granular transfer: ahead of compute only the bytes outside the routed
         # experts are copied; after the layer's router has run, the executor asks for the
@@ -213,6 +221,8 @@ class OffloadRuntime:
         """Hand a pinned staging buffer back with the event of the copy that reads it (the
         pool owns the event from then on and waits on it before lending the buffer again);
         otherwise destroy that event."""
+        if rec.resident:
+            return
         if rec.staged is not rec.host and self._pinned_pool is not None:
             self._pinned_pool.release(rec.staged, copy_event=rec.copied)
         else:
@@ -233,6 +243,9 @@ class OffloadRuntime:
             host = self.dequantizer.dequantize(layer, host)
             lm.compressed_nbytes = compressed
             metrics.compressed_bytes += compressed
+        if isinstance(host, DeviceBuffer):
+            # a layer resident on the device (DeviceResidentStorage): nothing to copy
+            return _Inflight(index, layer, lm, host, host, host, None, resident=True)
         nbytes = host.nbytes
         is_moe = getattr(self.executor, "is_moe_layer", None)
         granular = self.expert_granular and (is_moe(layer) if is_moe is not None else
@@ -321,7 +334,8 @@ class OffloadRuntime:
                     inflight.append(self._issue(next_issue, ordered_layer_ids[next_issue], metrics))
                     next_issue += 1
                 rec = inflight.popleft()
-                self.backend.wait_event(self.compute_stream, rec.copied)
+                if rec.copied is not None:
+                    self.backend.wait_event(self.compute_stream, rec.copied)
 
                 c_start = c_end = None
                 if self._timing:
@@ -352,8 +366,10 @@ class OffloadRuntime:
                 rec.lm.compute_ms = compute_elapsed * 1000
                 metrics.compute_seconds += compute_elapsed
 
-                done = self.backend.record_event(self.compute_stream) if self._timing else None
-                self._free_device(rec.device, done)
+                if not rec.resident:
+                    # fences the next copy into (or the free of) this layer's buffer
+                    done = self.backend.record_event(self.compute_stream)
+                    self._free_device(rec.device, done)
                 self.storage.release(layer_id)
                 self._release_staging(rec)
                 timings.append((rec.lm, rec.t_start, rec.t_end, c_start, c_end,
@@ -368,24 +384,30 @@ class OffloadRuntime:
             while inflight:
                 rec = inflight.popleft()
                 self.backend.synchronize_stream(self.transfer_stream)
-                self._free_device(rec.device, None)
+                if not rec.resident:
+                    self._free_device(rec.device, None)
                 self._release_staging(rec)
             self.backend.synchronize_stream(self.transfer_stream)
             self.backend.synchronize_stream(self.compute_stream)
             self._flush_deferred(force=True)
 
+        if isinstance(activations, DeviceActivations) and not isinstance(inputs, DeviceActivations):
+            # NumPy in, NumPy out (the reference contract); the chain kept them on the device
+            activations = activations.numpy()
         metrics.end_to_end_seconds = time.perf_counter() - wall_start
         if self._timing and timings:
             first = None
             for lm, hs, he, cs, ce, extra in timings:
-                lm.h2d_gpu_ms = self.backend.elapsed_ms(hs, he) + \
-                    sum(self.backend.elapsed_ms(a, b) for a, b in extra)
+                if hs is not None:
+                    lm.h2d_gpu_ms = self.backend.elapsed_ms(hs, he) + \
+                        sum(self.backend.elapsed_ms(a, b) for a, b in extra)
                 lm.compute_gpu_ms = self.backend.elapsed_ms(cs, ce)
                 metrics.transfer_gpu_seconds += lm.h2d_gpu_ms / 1000
                 metrics.compute_gpu_seconds += lm.compute_gpu_ms / 1000
-                first = hs if first is None else first
+                first = (hs if hs is not None else cs) if first is None else first
             metrics.device_seconds = self.backend.elapsed_ms(first, timings[-1][4]) / 1000
             for _, hs, he, cs, ce, extra in timings:
                 for ev in (hs, he, cs, ce, *[x for pair in extra for x in pair]):
-                    self.backend.destroy_event(ev)
+                    if ev is not None:
+                        self.backend.destroy_event(ev)
         return activations, metrics

@@ -41,3 +41,29 @@ class InMemoryStorage:
 
     def get_disk_read_ms(self, layer_id: int) -> float:
         return 0.0
+
+
+class DeviceResidentStorage:
+    """Layers kept resident in device memory (a model whose layers fit in HBM, or the hot
+    subset of one): ``get`` returns the layer's ``DeviceBuffer``, which the runtime hands to
+    the executor without a copy and never frees or re-pools (the store keeps it).  Same
+    ``LayerStorage`` protocol; no counterpart in the reference, whose runtime copies every
+    layer from host storage."""
+
+    def __init__(self, buffers: dict[int, Any]) -> None:
+        self._buffers = buffers
+
+    def request(self, layer_id: int) -> None:
+        return None
+
+    def wait(self, layer_id: int) -> None:
+        return None
+
+    def get(self, layer_id: int) -> Any:
+        return self._buffers[layer_id]
+
+    def release(self, layer_id: int) -> None:
+        return None
+
+    def get_disk_read_ms(self, layer_id: int) -> float:
+        return 0.0

@@ -274,3 +274,113 @@ def test_qwen_hybrid_layers_match_oracle(mi355x):
     err = normwise_err(out, ref)
     say(f"    normwise err {err:.2e}")
     assert err <= 5e-3
+
+
+@pytest.mark.parametrize("arch,lookahead,resident", [
+    (syn.GLM, 2, False),
+    (syn.GLM, 1, True),
+    (syn.QWEN, 2, True),
+])
+def test_device_activation_chain_equals_numpy_chain(mi355x, arch, lookahead, resident):
+    """The same chain run twice: activations through NumPy after every layer (the reference
+    contract) and kept on the device between layers (``device_activations=True``, no host
+    wait per layer).  Outputs equal bit for bit; the first chain is checked against the
+    oracle.  With ``resident`` the layers stay on the device (``DeviceResidentStorage``):
+    nothing is copied and the runtime frees nothing."""
+    from moe_mi355x.activations import DeviceActivations
+    from moe_mi355x.storage import DeviceResidentStorage
+
+    say(f"[gpu] device-activation chain {arch} lookahead={lookahead} resident={resident}")
+    if arch == syn.GLM:
+        shape = syn.MoeShape(syn.GLM, 256, 16, 4, 128, 128, 2.5, 1e-5)
+        make = GLM4MoeExecutor
+    else:
+        shape = syn.MoeShape(syn.QWEN, 256, 32, 6, 64, 64, 1.0, 1e-6, has_bias=False,
+                             has_shared_gate=True)
+        make = Qwen3NextExecutor
+    tensors, layers, blobs = build_layers(shape, 4, "float16", 90)
+    x = syn.make_inputs(90, 20, shape.hidden)
+    order = [0, 1, 2, 3, 1, 0]
+    dev_bufs = {}
+    stream = mi355x.create_stream("resident")
+    try:
+        if resident:
+            for i, raw in blobs.items():
+                dev_bufs[i] = mi355x.alloc_device(len(raw))
+                arr = np.frombuffer(raw, np.uint8)
+                mi355x.copy_h2d_ptr_async(dev_bufs[i].handle, arr.ctypes.data, arr.nbytes, stream)
+            mi355x.synchronize_stream(stream)
+        outs, seen = {}, []
+        for keep in (False, True):
+            ex = make(shape.config(), device_activations=keep)
+            storage = DeviceResidentStorage(dev_bufs) if resident else InMemoryStorage(blobs)
+            rt = OffloadRuntime(layers, mi355x, storage, LookaheadScheduler(lookahead), ex,
+                                use_buffer_pool=not resident)
+            assert ex.stream_ordered
+            orig = ex.run_layer
+
+            def spy(layer, activations, device_weights, backend, stream_, orig=orig):
+                out = orig(layer, activations, device_weights, backend, stream_)
+                seen.append((keep, type(activations).__name__, type(out).__name__))
+                return out
+
+            ex.run_layer = spy
+            try:
+                out, metrics = rt.run_inference(order, x)
+                ntab = len(ex._runner._tables)
+            finally:
+                rt.close()
+                ex.close()
+            assert isinstance(out, np.ndarray) and out.shape == x.shape
+            assert metrics.transferred_bytes == (0 if resident else
+                                                 sum(len(blobs[i]) for i in order))
+            # one pointer table per (layer, device buffer): resident layers bind 4 in all
+            assert ntab == 4 if resident else ntab <= 4 * (lookahead + 1)
+            outs[keep] = out
+        names = [s for s in seen if s[0]]
+        assert names[0][1] == "ndarray" and all(s[2] == "DeviceActivations" for s in names)
+        assert all(s[1] == "DeviceActivations" for s in names[1:])
+        assert np.array_equal(outs[False], outs[True])
+        ref = x
+        spec = spec_for(shape)
+        for i in order:
+            ref = orc.moe_block(ref, tensors[i], spec)["out"]
+        err = normwise_err(outs[False], ref)
+        say(f"    normwise err vs oracle {err:.2e}; device and NumPy chains equal")
+        assert err <= 5e-3
+    finally:
+        mi355x.synchronize_stream(stream)
+        for b in dev_bufs.values():
+            mi355x.free_device(b)
+        mi355x.destroy_stream(stream)
+
+
+def test_device_activations_go_stale_two_layers_later(mi355x, stream):
+    """An output handle stays readable while the next layer runs and is refused once the
+    layer after that has written its buffer again."""
+    from moe_mi355x.activations import DeviceActivations
+
+    shape = syn.MoeShape(syn.GLM, 128, 8, 2, 64, 64, 2.5, 1e-5)
+    tensors, layers, blobs = build_layers(shape, 1, "float16", 95)
+    raw = np.frombuffer(blobs[0], np.uint8)
+    buf = mi355x.alloc_device(raw.nbytes)
+    ex = GLM4MoeExecutor(shape.config(), device_activations=True)
+    try:
+        mi355x.copy_h2d_ptr_async(buf.handle, raw.ctypes.data, raw.nbytes, stream)
+        x = syn.make_inputs(95, 5, shape.hidden)
+        a = ex.run_layer(layers[0], x, buf, mi355x, stream)
+        b = ex.run_layer(layers[0], a, buf, mi355x, stream)
+        assert isinstance(a, DeviceActivations) and a.valid and b.valid
+        a_host = np.asarray(a)
+        ref_a = orc.moe_block(x, tensors[0], spec_for(shape))["out"]
+        assert normwise_err(a_host, ref_a) <= 5e-3
+        c = ex.run_layer(layers[0], b, buf, mi355x, stream)
+        assert not a.valid and b.valid and c.valid
+        with pytest.raises(RuntimeError, match="overwritten"):
+            a.numpy()
+        ref_c = orc.moe_block(orc.moe_block(ref_a, tensors[0], spec_for(shape))["out"],
+                              tensors[0], spec_for(shape))["out"]
+        assert normwise_err(c.numpy(), ref_c) <= 5e-3
+    finally:
+        ex.close()
+        mi355x.free_device(buf)

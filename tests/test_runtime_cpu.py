@@ -187,3 +187,79 @@ def test_expert_granular_needs_capable_executor_and_backend():
     with pytest.raises(ValueError, match="pointer copies"):
         OffloadRuntime([], HostArenaBackend(), InMemoryStorage({}), LookaheadScheduler(1), Granular(),
                        expert_granular=True)
+
+
+def test_resident_layers_are_neither_copied_nor_freed():
+    from moe_mi355x.storage import DeviceResidentStorage
+
+    backend = HostArenaBackend()
+    bufs = {i: backend.alloc_device(16) for i in range(3)}
+    seen = []
+
+    class Ex:
+        stream_ordered = False
+
+        def run_layer(self, layer, activations, device_weights, backend, stream):
+            seen.append(device_weights.handle)
+            return activations + 1
+
+    ex = Ex()
+    rt = OffloadRuntime(layers(3), backend, DeviceResidentStorage(bufs), LookaheadScheduler(2),
+                        ex, use_buffer_pool=True)
+    with rt:
+        out, m = rt.run_inference([0, 1, 2, 1], inputs=0)
+    assert out == 4 and m.transferred_bytes == 0 and ex.stream_ordered
+    assert seen == [bufs[i].handle for i in (0, 1, 2, 1)]
+    assert len(backend.allocations) == 3 and backend.live_events == 0
+    assert not any(op[0] == "h2d" for op in rt.transfer_stream.log)
+
+
+def test_device_activations_come_back_as_numpy():
+    """An executor that keeps activations on the device: the runtime returns NumPy when
+    it was given NumPy (the reference contract); a stale handle refuses to read."""
+    import ctypes
+
+    import numpy as np
+
+    from moe_mi355x.activations import DeviceActivations
+
+    class Owner:
+        def __init__(self):
+            self.gen = [0, 0, 0]
+            self.backend = self
+
+        def generation(self, slot):
+            return self.gen[slot]
+
+        def copy_d2h_ptr_async(self, dst, src, nbytes, stream):
+            ctypes.memmove(dst, src, nbytes)
+
+        def synchronize_stream(self, stream):
+            return None
+
+    owner = Owner()
+    store = [np.zeros((2, 4), np.float32) for _ in range(3)]
+
+    class Ex:
+        stream_ordered = False
+
+        def __init__(self):
+            self.k = 0
+
+        def run_layer(self, layer, activations, device_weights, backend, stream):
+            x = np.asarray(activations, np.float32)
+            slot = 1 + self.k % 2
+            self.k += 1
+            store[slot][:] = x + 1
+            owner.gen[slot] += 1
+            return DeviceActivations(owner, slot, owner.gen[slot], store[slot].ctypes.data,
+                                     2, 4, None)
+
+    rt = OffloadRuntime(layers(2), HostArenaBackend(), storage(2), LookaheadScheduler(1), Ex())
+    with rt:
+        out, _ = rt.run_inference([0, 1, 0], np.zeros((2, 4), np.float32))
+    assert isinstance(out, np.ndarray) and np.all(out == 3)
+    h = DeviceActivations(owner, 1, owner.gen[1], store[1].ctypes.data, 2, 4, None)
+    owner.gen[1] += 1
+    with pytest.raises(RuntimeError, match="overwritten"):
+        h.numpy()
