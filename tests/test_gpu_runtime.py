@@ -302,14 +302,14 @@ def test_device_activation_chain_equals_numpy_chain(mi355x, arch, lookahead, res
     x = syn.make_inputs(90, 20, shape.hidden)
     order = [0, 1, 2, 3, 1, 0]
     dev_bufs = {}
-    stream = mi355x.create_stream("resident")
+    st = mi355x.create_stream("resident")
     try:
         if resident:
             for i, raw in blobs.items():
                 dev_bufs[i] = mi355x.alloc_device(len(raw))
                 arr = np.frombuffer(raw, np.uint8)
-                mi355x.copy_h2d_ptr_async(dev_bufs[i].handle, arr.ctypes.data, arr.nbytes, stream)
-            mi355x.synchronize_stream(stream)
+                mi355x.copy_h2d_ptr_async(dev_bufs[i].handle, arr.ctypes.data, arr.nbytes, st)
+            mi355x.synchronize_stream(st)
         outs, seen = {}, []
         for keep in (False, True):
             ex = make(shape.config(), device_activations=keep)
@@ -319,8 +319,8 @@ def test_device_activation_chain_equals_numpy_chain(mi355x, arch, lookahead, res
             assert ex.stream_ordered
             orig = ex.run_layer
 
-            def spy(layer, activations, device_weights, backend, stream_, orig=orig):
-                out = orig(layer, activations, device_weights, backend, stream_)
+            def spy(layer, activations, device_weights, backend, stream, orig=orig):
+                out = orig(layer, activations, device_weights, backend, stream)
                 seen.append((keep, type(activations).__name__, type(out).__name__))
                 return out
 
@@ -349,10 +349,10 @@ def test_device_activation_chain_equals_numpy_chain(mi355x, arch, lookahead, res
         say(f"    normwise err vs oracle {err:.2e}; device and NumPy chains equal")
         assert err <= 5e-3
     finally:
-        mi355x.synchronize_stream(stream)
+        mi355x.synchronize_stream(st)
         for b in dev_bufs.values():
             mi355x.free_device(b)
-        mi355x.destroy_stream(stream)
+        mi355x.destroy_stream(st)
 
 
 def test_device_activations_go_stale_two_layers_later(mi355x, stream):
