@@ -682,17 +682,18 @@ def main() -> int:
     # ---- the drop-in path: OffloadRuntime + executors on resident layers ---------------------
     if not args.no_sweep and (only is None or only.startswith("dropin")):
         k = min(args.steps, 40)
+        sel = None if only in (None, "dropin") else only  # "dropin": every drop-in row
         for lay_name in ("frag16", "rows"):
-            if only is not None and not only.endswith(lay_name):
+            if sel is not None and not sel.endswith(lay_name):
                 continue
-            if only is None or only.startswith("dropin_glm47"):
+            if sel is None or sel.startswith("dropin_glm47"):
                 layers = build_layers(G, "float16", nl, layout=lay_name)
                 sweep.update(dropin_case(backend, stream, layers, G,
                                          _lib.MX_ROUTER_SIGMOID_SELECT_BIAS, (1, 32), lay_name,
                                          k, "dropin_glm47_fp16"))
                 for lay in layers:
                     lay.close()
-            if lay_name == "frag16" and (only is None or only.startswith("dropin_qwen3next")):
+            if lay_name == "frag16" and (sel is None or sel.startswith("dropin_qwen3next")):
                 Q = syn.QWEN3_NEXT
                 layers = build_layers(Q, "float16", nl, layout=lay_name)
                 sweep.update(dropin_case(backend, stream, layers, Q, _lib.MX_ROUTER_SOFTMAX,

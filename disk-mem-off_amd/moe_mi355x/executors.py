@@ -152,12 +152,38 @@ class _MoeExecutorBase:
         self._la_layouts: dict[int, tuple[list, LinearAttnLayout]] = {}
         self._fa_runner: FullAttnRunner | None = None
         self._fa_layouts: dict[int, tuple[list, FullAttnLayout]] = {}
+        self._facts: dict[tuple[int, str], tuple[list, Any]] = {}
 
     # values supplied by subclasses
     top_k: int
     norm_topk_prob: bool
     routed_scaling: float
     rms_norm_eps: float
+
+    def _desc(self, layer: LayerSpec, layout: MoeLayerLayout) -> Any:
+        """The block descriptor of a layer, built once per (layer, tensor list, layout
+        flag, router settings)."""
+        key = (layer.layer_id, "desc")
+        meta = layer.metadata["tensors"]
+        stamp = (layer.metadata.get("weight_layout"), self.router_mode, self.top_k,
+                 self.norm_topk_prob, self.routed_scaling, self.rms_norm_eps)
+        hit = self._facts.get(key)
+        if hit is not None and hit[0] is meta and hit[1][0] == stamp:
+            return hit[1][1]
+        desc = self.moe_config(layout, layer).desc()
+        self._facts[key] = (meta, (stamp, desc))
+        return desc
+
+    def _cached(self, layer: LayerSpec, key: str, fn: Callable[[LayerSpec], bool]) -> bool:
+        """A per-layer fact derived from its tensor list (a scan of every tensor name),
+        computed once per (layer, tensor list)."""
+        meta = layer.metadata["tensors"]
+        hit = self._facts.get((layer.layer_id, key))
+        if hit is not None and hit[0] is meta:
+            return hit[1]
+        v = bool(fn(layer))
+        self._facts[(layer.layer_id, key)] = (meta, v)
+        return v
 
     def _layout(self, layer: LayerSpec) -> MoeLayerLayout:
         meta = layer.metadata["tensors"]
@@ -193,8 +219,7 @@ class _MoeExecutorBase:
             raise RuntimeError(f"Layer {layer.layer_id}: device buffer size "
                                f"{device_weights.nbytes} < expected {layer.nbytes}")
         layout = self._layout(layer)
-        cfg = self.moe_config(layout, layer)
-        desc = cfg.desc()
+        desc = self._desc(layer, layout)
         if self._runner is None:
             self._runner = MoeRunner(backend)
         T = len(x)
@@ -224,7 +249,7 @@ class _MoeExecutorBase:
             raise RuntimeError(f"Layer {layer.layer_id}: device buffer size "
                                f"{device_weights.nbytes} < expected {layer.nbytes}")
         layout = self._layout(layer)
-        desc = self.moe_config(layout, layer).desc()
+        desc = self._desc(layer, layout)
         if self._runner is None:
             self._runner = MoeRunner(backend)
         T = len(x)
@@ -249,7 +274,7 @@ class _MoeExecutorBase:
             return self.attention(np.asarray(x, dtype=np.float32), layer, device_weights,
                                   backend, stream), None
         pre = self._device_attention(layer, device_weights, backend, stream)
-        if pre is None and not self._moe_only(layer):
+        if pre is None and not self._cached(layer, "moe_only", self._moe_only):
             raise NotImplementedError(
                 "layer holds attention tensors; pass attention=... to run them")
         return x, pre
@@ -410,10 +435,11 @@ class Qwen3NextExecutor(_MoeExecutorBase):
     def _device_attention(self, layer: LayerSpec, device_weights: DeviceBuffer, backend: Any,
                           stream: Any) -> Callable[[int, int], None] | None:
         kind = layer.metadata.get("attn_type", "linear")
-        meta = layer.metadata["tensors"]
-        if kind == "full" and has_full_attn(meta):
+        if kind == "full" and self._cached(layer, "full", lambda l: has_full_attn(
+                l.metadata["tensors"])):
             return self._device_full_attention(layer, device_weights, backend, stream)
-        if kind != "linear" or not has_linear_attn(meta):
+        if kind != "linear" or not self._cached(layer, "linear", lambda l: has_linear_attn(
+                l.metadata["tensors"])):
             return None
         if device_weights.backend != "rocm":
             raise RuntimeError("the linear-attention block needs the MI355X backend; got "

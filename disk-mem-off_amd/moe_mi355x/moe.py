@@ -119,9 +119,9 @@ class MoeRunner:
         self.backend = backend
         self.lib = _lib.load()
         self._ws: DeviceBuffer | None = None
-        # (id(layout), base) -> (layout, device table); the layout is held so its id cannot
-        # be reused by another layout while the entry lives.
-        self._tables: dict[tuple[int, int], tuple[MoeLayerLayout, DeviceBuffer]] = {}
+        # (id(layout), base) -> (layout, device table, weights struct); the layout is held so
+        # its id cannot be reused by another layout while the entry lives.
+        self._tables: dict[tuple[int, int], tuple[MoeLayerLayout, DeviceBuffer, Any]] = {}
         self._table_ev: Any = None   # last table upload (reads the pinned staging copy)
         self._x_ev: Any = None       # last upload of x (reads the pinned staging copy)
         self._io: dict[str, DeviceBuffer] = {}
@@ -132,6 +132,7 @@ class MoeRunner:
         self._last_stream: Any = None
         # tokens, output slot and input address of the last route_numpy
         self._split: tuple[int, int, int] = (0, 1, 0)
+        self._reserved: dict[bytes, int] = {}  # desc bytes -> tokens its buffers cover
 
     def generation(self, slot: int) -> int:
         return -1 if self._closed else self._gen[slot]
@@ -143,6 +144,9 @@ class MoeRunner:
             self.backend.synchronize_stream(self._last_stream)
 
     def reserve(self, desc: _lib.MxMoeDesc, tokens: int) -> None:
+        key = bytes(desc)
+        if self._reserved.get(key, -1) >= tokens:
+            return
         need = workspace_bytes(desc, tokens)
         if self._ws is None or self._ws.nbytes < need:
             self._quiesce()
@@ -166,6 +170,7 @@ class MoeRunner:
                 if pin is not None:
                     self.backend.free_pinned_host(pin)
                 self._pinned[key] = self.backend.alloc_pinned_host(max(nbytes_act, 16))
+        self._reserved[bytes(desc)] = tokens
 
     def bind(self, layout: MoeLayerLayout, base: int, stream: Any) -> _lib.MxMoeWeights:
         """Weights of the layer buffer at ``base``; its expert pointer table is uploaded on
@@ -174,11 +179,11 @@ class MoeRunner:
         key = (id(layout), int(base))
         hit = self._tables.get(key)
         if hit is not None and hit[0] is layout:
-            return layout.weights(base, hit[1].handle)
+            return hit[2]
         if len(self._tables) >= self.MAX_TABLES:
             self._quiesce()
             self._wait(("_table_ev",))
-            for _, dev in self._tables.values():
+            for _, dev, _ in self._tables.values():
                 self.backend.free_device(dev)
             self._tables.clear()
         nbytes = ctypes.sizeof(_lib.MxExpertPtrs) * (layout.n_experts + 1)
@@ -196,8 +201,9 @@ class MoeRunner:
         ctypes.memmove(addr, table, nbytes)
         self.backend.copy_h2d_ptr_async(dev.handle, addr, nbytes, stream)
         self._table_ev = self.backend.record_event(stream)
-        self._tables[key] = (layout, dev)
-        return layout.weights(base, dev.handle)
+        w = layout.weights(base, dev.handle)
+        self._tables[key] = (layout, dev, w)
+        return w
 
     def _wait(self, names: tuple[str, ...]) -> None:
         for name in names:
@@ -359,7 +365,7 @@ class MoeRunner:
     def close(self) -> None:
         self._quiesce()
         self._wait(("_table_ev", "_x_ev"))
-        bufs = [self._ws, *self._io.values(), *(dev for _, dev in self._tables.values())]
+        bufs = [self._ws, *self._io.values(), *(dev for _, dev, _ in self._tables.values())]
         for buf in bufs:
             if buf is not None:
                 self.backend.free_device(buf)
@@ -369,6 +375,7 @@ class MoeRunner:
         self._tables.clear()
         self._io.clear()
         self._pinned.clear()
+        self._reserved.clear()
         self._closed = True
 
 
