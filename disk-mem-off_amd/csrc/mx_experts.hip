@@ -917,11 +917,14 @@ __global__ __launch_bounds__((64 * NW), (LdsShape<WF>::OCC * 4 / NW)) void k_exp
 // ------------------------------------------------------------------------------------
 // Host side.
 // ------------------------------------------------------------------------------------
+#ifndef MX_PREFILL_M_BLK
+#define MX_PREFILL_M_BLK 128
+#endif
 int mx_m_blk_for(int tokens, int weight_dtype) {
   if (tokens <= 16) return 16;
   if (tokens <= 32) return 32;
   if (tokens <= 64 || weight_dtype == MX_DT_F32) return 64;
-  return 128;
+  return MX_PREFILL_M_BLK;
 }
 
 static int expert_check(const MxMoeDesc* d) {

@@ -535,8 +535,18 @@ int launch_scan(const float* q, const float* kb, const float* v, const float* de
   return mx_launch_status();
 }
 
+// Inputs of at least MX_LA_CHUNK_MIN_T tokens run the chunked form on MFMA (mx_la_chunk.hip)
+// where it is built for the head sizes; shorter ones (a chain of a few tokens) and other
+// head sizes the token-sequential scan.
+#ifndef MX_LA_CHUNK_MIN_T
+#define MX_LA_CHUNK_MIN_T 64
+#endif
 int scan_launch(const float* q, const float* kb, const float* v, const float* decay, int T,
                 int n, int dk, int dv, float* o, hipStream_t s) {
+  if (T >= MX_LA_CHUNK_MIN_T) {
+    const int rc = mx_la_chunked_scan(q, kb, v, decay, T, n, dk, dv, o, s);
+    if (rc != MX_ERR_UNSUPPORTED) return rc;
+  }
   switch (dk) {
     case 4: return launch_scan<4, 1>(q, kb, v, decay, T, n, dv, o, s);
     case 8: return launch_scan<8, 1>(q, kb, v, decay, T, n, dv, o, s);

@@ -36,17 +36,23 @@ def upload(mi355x, stream, arr):
     return buf
 
 
-@pytest.mark.parametrize("n,dk,dv,T", [
-    (2, 4, 4, 3), (3, 8, 12, 17), (4, 16, 8, 33), (2, 32, 40, 50), (2, 64, 64, 1),
-    (4, 128, 128, 37), (2, 128, 96, 16), (1, 256, 64, 21), (1, 512, 32, 9),
+@pytest.mark.parametrize("n,dk,dv,T,gs", [
+    (2, 4, 4, 3, 0.2), (3, 8, 12, 17, 0.2), (4, 16, 8, 33, 0.2), (2, 32, 40, 50, 0.2),
+    (2, 64, 64, 1, 0.2), (4, 128, 128, 37, 0.2), (2, 128, 96, 16, 0.2), (1, 256, 64, 21, 0.2),
+    (1, 512, 32, 9, 0.2),
+    # from 64 tokens the chunked form on MFMA: whole and partial chunks, the four head
+    # shapes it is built for, a shape it is not (sequential), strong and mixed decays
+    (2, 128, 128, 64, 0.2), (3, 128, 128, 200, 0.2), (2, 64, 64, 130, 0.2),
+    (1, 128, 64, 150, 0.2), (2, 64, 128, 300, 0.2), (2, 128, 96, 100, 0.2),
+    (2, 128, 128, 257, 3.0), (1, 64, 64, 1000, 0.05),
 ])
-def test_scan_matches_oracle(mi355x, stream, n, dk, dv, T):
-    say(f"[gpu] scan n={n} dk={dk} dv={dv} T={T}")
+def test_scan_matches_oracle(mi355x, stream, n, dk, dv, T, gs):
+    say(f"[gpu] scan n={n} dk={dk} dv={dv} T={T} decay scale {gs}")
     rng = np.random.default_rng(n * 1000 + dk + T)
     q = rng.standard_normal((T, n * dk)).astype(np.float32)
     kb = (rng.standard_normal((T, n * dk)) * 0.3).astype(np.float32)
     v = rng.standard_normal((T, n * dv)).astype(np.float32)
-    g = (-np.abs(rng.standard_normal((T, n))) * 0.2).astype(np.float32)
+    g = (-np.abs(rng.standard_normal((T, n))) * gs).astype(np.float32)
     decay = np.exp(g).astype(np.float32)
     bufs = [upload(mi355x, stream, a) for a in (q, kb, v, decay)]
     o = mi355x.alloc_device(T * n * dv * 4)
@@ -62,6 +68,39 @@ def test_scan_matches_oracle(mi355x, stream, n, dk, dv, T):
     err = normwise_err(got, ref)
     say(f"    normwise err {err:.2e}")
     assert err <= 1e-5
+
+
+@pytest.mark.parametrize("T", [70, 300])
+def test_chunked_scan_zero_and_tiny_decays(mi355x, stream, T):
+    """Decays that underflow to zero (the state restarts there, inside a chunk and on a
+    chunk's first token) and tiny nonzero ones between ordinary ones."""
+    n, dk, dv = 2, 128, 128
+    say(f"[gpu] chunked scan with zero decays, T={T}")
+    rng = np.random.default_rng(77 + T)
+    q = rng.standard_normal((T, n * dk)).astype(np.float32)
+    kb = (rng.standard_normal((T, n * dk)) * 0.3).astype(np.float32)
+    v = rng.standard_normal((T, n * dv)).astype(np.float32)
+    g = (-np.abs(rng.standard_normal((T, n))) * 0.3).astype(np.float32)
+    g[5, 0] = g[64 % T, 1] = g[T - 2, 0] = -200.0      # exp -> 0 in fp32
+    g[10, 1] = g[40, 0] = -80.0                         # exp -> ~1.8e-35
+    g[11:20, 1] = -0.01
+    decay = np.exp(g).astype(np.float32)
+    assert decay[5, 0] == 0.0 and decay[10, 1] > 0.0
+    bufs = [upload(mi355x, stream, a) for a in (q, kb, v, decay)]
+    o = mi355x.alloc_device(T * n * dv * 4)
+    try:
+        _lib.check(_lib.load().mx_gated_delta_scan(bufs[0].handle, bufs[1].handle,
+                                                   bufs[2].handle, bufs[3].handle, T, n, dk,
+                                                   dv, o.handle, stream))
+        got = read_device(mi355x, o.handle, np.float32, T * n * dv, stream).reshape(T, -1)
+    finally:
+        for b in bufs + [o]:
+            mi355x.free_device(b)
+    with np.errstate(divide="ignore"):
+        ref = la.gated_recurrence(q, kb, v, np.log(decay), n, dk, dv)
+    err = normwise_err(got, ref)
+    say(f"    normwise err {err:.2e}")
+    assert np.all(np.isfinite(got)) and err <= 1e-5
 
 
 def _block(mi355x, stream, shape, t, x):
