@@ -9,9 +9,10 @@
 //   S_end = a(end, t0 - 1) S_p + sum_s a(end, s) v_s kb_s^T
 // which is the recurrence unrolled over the chunk (exact in real arithmetic).  The first
 // sum (intra-chunk) needs no state: k_la_chunk_intra computes it for every (head, chunk)
-// in parallel as (Q Kb^T masked and scaled by a) V and writes it to o.  The second part
-// walks the chunks of a head in order: k_la_chunk_state holds 16 state rows of one head
-// in MFMA accumulators, adds a(t, t0 - 1) S_p q_t to o and updates S, one chunk at a time.
+// in parallel as (Q Kb^T masked and scaled by a) V, writes it to o, and writes the chunk's
+// decay coefficients to a small buffer.  The second part walks the chunks of a head in
+// order: k_la_chunk_state holds 16 state rows of one head in MFMA accumulators, adds
+// a(t, t0 - 1) S_p q_t to o and updates S, one chunk at a time.
 //
 // The decay factors are formed in double precision from the fp32 decays the reference
 // multiplies by: with G_t = sum over the chunk of log(d_r) up to t, a(t, s) =
@@ -77,6 +78,10 @@ __device__ __forceinline__ void chunk_log_decay(const float* __restrict__ decay,
   sLR[l] = lr;
 }
 
+// Coefficients the state walk reads per (head, chunk): a(t, t0 - 1) for the 64 tokens, then
+// a(end, s) for the 64 tokens, then a(end, t0 - 1) (padded to 132 floats).
+constexpr int kCoef = 132;
+
 // LDS row strides in floats: (stride / 4) odd, so the 16-byte reads of 16 consecutive rows
 // at one column group hit distinct bank groups.
 template <int W>
@@ -85,19 +90,24 @@ struct Pad {
 };
 
 // ---- intra-chunk part: o[t] = sum_{t0 <= s <= t} a(t, s) (kb_s . q_t) v_s ---------------
-// Block (chunk, head), 4 waves; wave w takes tokens 16 w .. 16 w + 15 of the chunk.
+// Block (chunk, head), 4 waves; wave w takes tokens 16 w .. 16 w + 15 of the chunk.  Its q
+// rows go straight into MFMA A registers; kb (B of the scores, all 64 tokens) and v
+// (transposed, B of the products with v) are shared through LDS, and the scores' LDS
+// region is then reused for each wave's masked scores (A of the products with v).  Wave 0
+// also writes the chunk's coefficients for the state walk.
 template <int DK, int DV>
-__global__ __launch_bounds__(256) void k_la_chunk_intra(const float* __restrict__ q,
-                                                        const float* __restrict__ kb,
-                                                        const float* __restrict__ v,
-                                                        const float* __restrict__ decay, int T,
-                                                        int n, int nchunk,
-                                                        float* __restrict__ o) {
+__global__ __launch_bounds__(256, 2) void k_la_chunk_intra(const float* __restrict__ q,
+                                                           const float* __restrict__ kb,
+                                                           const float* __restrict__ v,
+                                                           const float* __restrict__ decay,
+                                                           int T, int n, int nchunk,
+                                                           float* __restrict__ o,
+                                                           float* __restrict__ coef) {
   constexpr int SK = Pad<DK>::S, SC = Pad<kC>::S;
-  __shared__ __align__(16) float sQ[kC * SK];
-  __shared__ __align__(16) float sK[kC * SK];
-  __shared__ __align__(16) float sVt[DV * SC];     // v transposed: [value row][token]
-  __shared__ __align__(16) float sP[4 * 16 * SC];  // each wave's masked scores
+  constexpr int KP = kC * DK / 4 / 256, VP = kC * DV / 4 / 256;  // float4 pieces per thread
+  static_assert(4 * 16 * SC <= kC * SK, "masked scores reuse the kb tile");
+  __shared__ __align__(16) float sK[kC * SK];    // kb tile, then the masked scores
+  __shared__ __align__(16) float sVt[DV * SC];   // v transposed: [value row][token]
   __shared__ double sG[kC];
   __shared__ int sLR[kC];
 
@@ -107,26 +117,40 @@ __global__ __launch_bounds__(256) void k_la_chunk_intra(const float* __restrict_
   const int j = lane & 15, qq = lane >> 4;
   const int qd = n * DK, vd = n * DV;
 
-  for (int i = tid; i < kC * DK / 4; i += 256) {
-    const int r = i / (DK / 4), c = 4 * (i % (DK / 4)), t = t0 + r;
-    float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
-    if (t < T) {
-      a = *(const float4*)(q + (size_t)t * qd + h * DK + c);
-      b = *(const float4*)(kb + (size_t)t * qd + h * DK + c);
-    }
-    *(float4*)(sQ + r * SK + c) = a;
-    *(float4*)(sK + r * SK + c) = b;
+  // every global load of the block first, then the LDS stores
+  float4 qa[DK / 16];
+  const int tq = t0 + 16 * w + j;
+#pragma unroll
+  for (int u = 0; u < DK / 16; ++u)
+    qa[u] = tq < T ? *(const float4*)(q + (size_t)tq * qd + h * DK + 16 * u + 4 * qq)
+                   : make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 kr[KP], vr[VP];
+#pragma unroll
+  for (int p = 0; p < KP; ++p) {
+    const int i = tid + 256 * p, r = i / (DK / 4), c = 4 * (i % (DK / 4)), t = t0 + r;
+    kr[p] = t < T ? *(const float4*)(kb + (size_t)t * qd + h * DK + c)
+                  : make_float4(0.f, 0.f, 0.f, 0.f);
   }
-  for (int i = tid; i < kC * DV / 4; i += 256) {
-    const int r = i / (DV / 4), c = 4 * (i % (DV / 4)), t = t0 + r;
-    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (t < T) a = *(const float4*)(v + (size_t)t * vd + h * DV + c);
-    sVt[(c + 0) * SC + r] = a.x;
-    sVt[(c + 1) * SC + r] = a.y;
-    sVt[(c + 2) * SC + r] = a.z;
-    sVt[(c + 3) * SC + r] = a.w;
+#pragma unroll
+  for (int p = 0; p < VP; ++p) {
+    const int i = tid + 256 * p, r = i / (DV / 4), c = 4 * (i % (DV / 4)), t = t0 + r;
+    vr[p] = t < T ? *(const float4*)(v + (size_t)t * vd + h * DV + c)
+                  : make_float4(0.f, 0.f, 0.f, 0.f);
   }
   if (w == 0) chunk_log_decay(decay, t0, T, n, h, sG, sLR);
+#pragma unroll
+  for (int p = 0; p < KP; ++p) {
+    const int i = tid + 256 * p, r = i / (DK / 4), c = 4 * (i % (DK / 4));
+    *(float4*)(sK + r * SK + c) = kr[p];
+  }
+#pragma unroll
+  for (int p = 0; p < VP; ++p) {
+    const int i = tid + 256 * p, r = i / (DV / 4), c = 4 * (i % (DV / 4));
+    sVt[(c + 0) * SC + r] = vr[p].x;
+    sVt[(c + 1) * SC + r] = vr[p].y;
+    sVt[(c + 2) * SC + r] = vr[p].z;
+    sVt[(c + 3) * SC + r] = vr[p].w;
+  }
   __syncthreads();
 
   // scores of this wave's 16 tokens against the chunk's 64: P = Q Kb^T
@@ -134,16 +158,16 @@ __global__ __launch_bounds__(256) void k_la_chunk_intra(const float* __restrict_
 #pragma unroll
   for (int nt = 0; nt < 4; ++nt) pacc[nt] = (float4_t){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int k0 = 0; k0 < DK; k0 += 16) {
-    const float4 a = *(const float4*)(sQ + (16 * w + j) * SK + k0 + 4 * qq);
+  for (int u = 0; u < DK / 16; ++u) {
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
-      const float4 b = *(const float4*)(sK + (16 * nt + j) * SK + k0 + 4 * qq);
-      pacc[nt] = mfma_k16(a, b, pacc[nt]);
+      const float4 b = *(const float4*)(sK + (16 * nt + j) * SK + 16 * u + 4 * qq);
+      pacc[nt] = mfma_k16(qa[u], b, pacc[nt]);
     }
   }
+  __syncthreads();  // every wave is done with the kb tile: its region takes the scores
   // causal mask and decay factors; lane (j, qq) holds P[16 w + 4 qq + r][16 nt + j]
-  float* myP = sP + w * 16 * SC;
+  float* myP = sK + w * 16 * SC;
 #pragma unroll
   for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
@@ -178,179 +202,184 @@ __global__ __launch_bounds__(256) void k_la_chunk_intra(const float* __restrict_
       for (int nt = 0; nt < NV; ++nt) o[(size_t)t * vd + h * DV + 16 * nt + j] = oacc[nt][r];
     }
   }
+  if (w == 0) {
+    // coefficients of the state walk, lane l = token l of the chunk
+    const int l = lane;
+    const int lastv = min(kC, T - t0) - 1;
+    const double ge = sG[lastv], gl = sG[l];
+    const int lre = sLR[lastv];
+    float* cf = coef + ((size_t)h * nchunk + chunk) * kCoef;
+    cf[l] = sLR[l] < 0 ? expf((float)gl) : 0.f;
+    cf[kC + l] = (l <= lastv && lre <= l) ? expf((float)(ge - gl)) : 0.f;
+    if (l == 0) cf[2 * kC] = lre < 0 ? expf((float)ge) : 0.f;
+  }
 }
 
 // ---- state part: o[t] += a(t, t0 - 1) S_p q_t, then S <- a(end) S_p + sum a(end, s) v kb^T
-// Block (head, 16 value rows), 4 waves, walking the chunks in order.  The state rows live
-// in MFMA accumulators (wave w: key columns 16 DK/64 w ..), with a copy in LDS that the
-// next chunk's output products read.  The next chunk's q, kb and v are loaded into
-// registers while the current chunk computes.
+// Block (head, 16 value rows), 4 waves, walking the chunks in order.  The block keeps the
+// transposed state rows S^T[c][i] (c: key column, i: one of its 16 value rows) in MFMA
+// accumulators, wave w holding key columns 16 NT w .. 16 NT (w + 1) - 1; lane (j, qq) of a
+// tile holds S^T[4 qq + r][j], which is exactly the B operand of the output product when
+// lane group qq sums key columns 4 qq .. 4 qq + 3, so the state never leaves registers.
+// Each wave forms the output over its own key columns for all 64 tokens; the four partial
+// outputs are summed through LDS (double-buffered, one barrier per chunk) and added to the
+// intra-chunk part already in o.  The next chunk's operands are loaded while this one
+// computes.
 template <int DK>
 __global__ __launch_bounds__(256) void k_la_chunk_state(const float* __restrict__ q,
                                                         const float* __restrict__ kb,
                                                         const float* __restrict__ v,
-                                                        const float* __restrict__ decay, int T,
+                                                        const float* __restrict__ coef, int T,
                                                         int n, int dv, int nchunk,
                                                         float* __restrict__ o) {
-  constexpr int SK = Pad<DK>::S, SC = Pad<kC>::S;
-  constexpr int NT = DK / 64;                 // 16-column state tiles per wave
-  constexpr int QP = kC * DK / 4 / 256;        // float4 pieces of q (and of kb) per thread
-  __shared__ __align__(16) float sQ[kC * SK];
-  __shared__ __align__(16) float sKt[DK * SC];  // kb transposed: [key column][token]
-  __shared__ __align__(16) float sVt[16 * SC];  // this block's value rows: [row][token]
-  __shared__ __align__(16) float sS[16 * SK];   // state rows before the chunk
-  __shared__ double sG[kC];
-  __shared__ int sLR[kC];
-  __shared__ __align__(16) float sE[kC];  // a(t, t0 - 1): weight of S_p q_t
-  __shared__ __align__(16) float sW[kC];  // a(end, s): weight of v_s kb_s^T in the new state
-  __shared__ float sGam;     // a(end, t0 - 1): decay of S_p over the chunk
+  constexpr int NT = DK / 64;  // 16-column state tiles per wave
+  constexpr int SO = 16 + 1;   // LDS row stride of a partial output (tokens x 16 rows)
+  __shared__ float sO[2][4][kC * SO];
 
   const int blocks_per_head = dv / 16;
   const int h = blockIdx.x / blocks_per_head, i0 = 16 * (blockIdx.x % blocks_per_head);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int j = lane & 15, qq = lane >> 4;
   const int qd = n * DK, vd = n * dv;
+  const int cw = 16 * NT * w;  // this wave's first key column
 
-  float4_t sacc[NT];
-#pragma unroll
-  for (int u = 0; u < NT; ++u) sacc[u] = (float4_t){0.f, 0.f, 0.f, 0.f};
-  for (int i = tid; i < 16 * SK; i += 256) sS[i] = 0.f;
-
-  float4 rq[QP], rk[QP];
-  // v: 64 tokens x 16 rows = 1024 values, 4 per thread
-  float rvv[4];
-  auto load_all = [&](int t0) {
-#pragma unroll
-    for (int p = 0; p < QP; ++p) {
-      const int i = tid + 256 * p;
-      const int r = i / (DK / 4), c = 4 * (i % (DK / 4)), t = t0 + r;
-      rq[p] = rk[p] = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (t < T) {
-        rq[p] = *(const float4*)(q + (size_t)t * qd + h * DK + c);
-        rk[p] = *(const float4*)(kb + (size_t)t * qd + h * DK + c);
-      }
-    }
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const int i = tid + 256 * p, r = i >> 4, c = i & 15, t = t0 + r;
-      rvv[p] = t < T ? v[(size_t)t * vd + h * dv + i0 + c] : 0.f;
-    }
+  // operands of one chunk, in registers
+  struct Ops {
+    float4 qf[4][NT];  // q[t0 + 16 mt + j][cw + 16 u + 4 qq ..]          (A, output)
+    float kf[4][NT][4];  // kb[t0 + 16 kg + 4 qq + e][cw + 16 u + j]        (A, state)
+    float vf[4][4];      // v[t0 + 16 kg + 4 qq + e][i0 + j]                 (B, state)
+    float et[4];         // a(t, t0 - 1) of token 16 mt + j
+    float4 ws[4];        // a(end, s) of tokens 16 kg + 4 qq ..
+    float gam;
+    float oi[4];         // intra-chunk o of token 16 w + 4 qq + r, row i0 + j
   };
-  auto store_all = [&]() {
-#pragma unroll
-    for (int p = 0; p < QP; ++p) {
-      const int i = tid + 256 * p;
-      const int r = i / (DK / 4), c = 4 * (i % (DK / 4));
-      *(float4*)(sQ + r * SK + c) = rq[p];
-      sKt[(c + 0) * SC + r] = rk[p].x;
-      sKt[(c + 1) * SC + r] = rk[p].y;
-      sKt[(c + 2) * SC + r] = rk[p].z;
-      sKt[(c + 3) * SC + r] = rk[p].w;
-    }
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const int i = tid + 256 * p, r = i >> 4, c = i & 15;
-      sVt[c * SC + r] = rvv[p];
-    }
-  };
-  load_all(0);
-  for (int ch = 0; ch < nchunk; ++ch) {
+  auto load = [&](Ops& x, int ch) {
     const int t0 = ch * kC;
-    store_all();
-    if (w == 0) {
-      chunk_log_decay(decay, t0, T, n, h, sG, sLR);
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-      const int l = lane;
-      const double gl = sG[l];
-      const int lastv = min(kC, T - t0) - 1;  // last token of the chunk inside T
-      const double ge = sG[lastv];
-      const int lre = sLR[lastv];
-      sE[l] = sLR[l] < 0 ? expf((float)gl) : 0.f;
-      sW[l] = (l <= lastv && lre <= l) ? expf((float)(ge - gl)) : 0.f;
-      if (l == 0) sGam = lre < 0 ? expf((float)ge) : 0.f;
+    const float* cf = coef + ((size_t)h * nchunk + ch) * kCoef;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const int t = t0 + 16 * mt + j;
+#pragma unroll
+      for (int u = 0; u < NT; ++u)
+        x.qf[mt][u] = t < T ? *(const float4*)(q + (size_t)t * qd + h * DK + cw + 16 * u + 4 * qq)
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
+      x.et[mt] = cf[16 * mt + j];
     }
-    __syncthreads();
-    if (ch + 1 < nchunk) load_all(t0 + kC);
-
-    // output: o[t, i0 + j] += sum_c a(t, t0 - 1) q_t[c] S_p[j][c] for t = t0 + 16 w + ..
-    float ov[4];
+#pragma unroll
+    for (int kg = 0; kg < 4; ++kg) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int t = t0 + 16 * kg + 4 * qq + e;
+        const bool ok = t < T;
+#pragma unroll
+        for (int u = 0; u < NT; ++u)
+          x.kf[kg][u][e] = ok ? kb[(size_t)t * qd + h * DK + cw + 16 * u + j] : 0.f;
+        x.vf[kg][e] = ok ? v[(size_t)t * vd + h * dv + i0 + j] : 0.f;
+      }
+      x.ws[kg] = *(const float4*)(cf + kC + 16 * kg + 4 * qq);
+    }
+    x.gam = cf[2 * kC];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = t0 + 16 * w + 4 * qq + r;
-      ov[r] = t < T ? o[(size_t)t * vd + h * dv + i0 + j] : 0.f;
+      x.oi[r] = t < T ? o[(size_t)t * vd + h * dv + i0 + j] : 0.f;
     }
-    float4_t oacc = (float4_t){0.f, 0.f, 0.f, 0.f};
-    const float et = sE[16 * w + j];
-#pragma unroll
-    for (int k0 = 0; k0 < DK; k0 += 16) {
-      float4 a = *(const float4*)(sQ + (16 * w + j) * SK + k0 + 4 * qq);
-      a.x *= et;
-      a.y *= et;
-      a.z *= et;
-      a.w *= et;
-      const float4 b = *(const float4*)(sS + j * SK + k0 + 4 * qq);
-      oacc = mfma_k16(a, b, oacc);
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = t0 + 16 * w + 4 * qq + r;
-      if (t < T) o[(size_t)t * vd + h * dv + i0 + j] = ov[r] + oacc[r];
-    }
+  };
 
-    // state: S <- a(end) S_p + sum_s a(end, s) v_s kb_s^T; lane (j, qq) of wave w holds
-    // S[4 qq + r][16 (NT w + u) + j]
-    const float gam = sGam;
+  float4_t st[NT];
 #pragma unroll
-    for (int u = 0; u < NT; ++u) sacc[u] *= gam;
+  for (int u = 0; u < NT; ++u) st[u] = (float4_t){0.f, 0.f, 0.f, 0.f};
+  Ops cur, nxt;
+  load(cur, 0);
+  for (int ch = 0; ch < nchunk; ++ch) {
+    if (ch + 1 < nchunk) load(nxt, ch + 1);
+    // partial output over this wave's key columns, all 64 tokens: A = a(t) q_t, B = S^T
+    float4_t op[4];
 #pragma unroll
-    for (int k0 = 0; k0 < kC; k0 += 16) {
-      float4 a = *(const float4*)(sVt + j * SC + k0 + 4 * qq);
-      const float4 ws = *(const float4*)(sW + k0 + 4 * qq);
-      a.x *= ws.x;
-      a.y *= ws.y;
-      a.z *= ws.z;
-      a.w *= ws.w;
+    for (int mt = 0; mt < 4; ++mt) {
+      op[mt] = (float4_t){0.f, 0.f, 0.f, 0.f};
+      const float et = cur.et[mt];
 #pragma unroll
       for (int u = 0; u < NT; ++u) {
-        const float4 b = *(const float4*)(sKt + (16 * (NT * w + u) + j) * SC + k0 + 4 * qq);
-        sacc[u] = mfma_k16(a, b, sacc[u]);
+        const float4 a = cur.qf[mt][u];
+        op[mt] = mfma4(a.x * et, st[u][0], op[mt]);
+        op[mt] = mfma4(a.y * et, st[u][1], op[mt]);
+        op[mt] = mfma4(a.z * et, st[u][2], op[mt]);
+        op[mt] = mfma4(a.w * et, st[u][3], op[mt]);
       }
     }
-    __syncthreads();  // every wave is done with sQ, sKt, sVt and sS of this chunk
+    // state update: S^T <- a(end) S^T + sum_s kb_s (a(end, s) v_s)^T
 #pragma unroll
-    for (int u = 0; u < NT; ++u)
+    for (int u = 0; u < NT; ++u) st[u] *= cur.gam;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sS[(4 * qq + r) * SK + 16 * (NT * w + u) + j] = sacc[u][r];
+    for (int kg = 0; kg < 4; ++kg) {
+      const float b0 = cur.vf[kg][0] * cur.ws[kg].x, b1 = cur.vf[kg][1] * cur.ws[kg].y;
+      const float b2 = cur.vf[kg][2] * cur.ws[kg].z, b3 = cur.vf[kg][3] * cur.ws[kg].w;
+#pragma unroll
+      for (int u = 0; u < NT; ++u) {
+        st[u] = mfma4(cur.kf[kg][u][0], b0, st[u]);
+        st[u] = mfma4(cur.kf[kg][u][1], b1, st[u]);
+        st[u] = mfma4(cur.kf[kg][u][2], b2, st[u]);
+        st[u] = mfma4(cur.kf[kg][u][3], b3, st[u]);
+      }
+    }
+    // sum of the four waves' partial outputs; lane (j, qq) holds op[mt][r] for token
+    // 16 mt + 4 qq + r, row j
+    float* so = sO[ch & 1][w];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) so[(16 * mt + 4 * qq + r) * SO + j] = op[mt][r];
+    __syncthreads();
+    const int t0 = ch * kC;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int tl = 16 * w + 4 * qq + r, t = t0 + tl;
+      float sum = cur.oi[r];
+#pragma unroll
+      for (int w2 = 0; w2 < 4; ++w2) sum += sO[ch & 1][w2][tl * SO + j];
+      if (t < T) o[(size_t)t * vd + h * dv + i0 + j] = sum;
+    }
+    if (ch + 1 < nchunk) cur = nxt;
   }
 }
 
 template <int DK, int DV>
 int launch_chunked(const float* q, const float* kb, const float* v, const float* decay, int T,
-                   int n, float* o, hipStream_t s) {
+                   int n, float* o, float* coef, hipStream_t s) {
   const int nchunk = (T + kC - 1) / kC;
   mx_clear_error();
   hipLaunchKernelGGL((k_la_chunk_intra<DK, DV>), dim3((unsigned)(nchunk * n)), dim3(256), 0, s,
-                     q, kb, v, decay, T, n, nchunk, o);
+                     q, kb, v, decay, T, n, nchunk, o, coef);
   MX_TRY(mx_launch_status());
   hipLaunchKernelGGL((k_la_chunk_state<DK>), dim3((unsigned)(n * (DV / 16))), dim3(256), 0, s,
-                     q, kb, v, decay, T, n, DV, nchunk, o);
+                     q, kb, v, coef, T, n, DV, nchunk, o);
   return mx_launch_status();
 }
 
+bool chunk_shape(int dk, int dv) { return (dk == 64 || dk == 128) && (dv == 64 || dv == 128); }
+
 }  // namespace
 
-// Chunked scan for the shapes it is built for (key and value heads of 64 or 128); returns
-// MX_ERR_UNSUPPORTED otherwise, and the caller runs the token-sequential scan.
+size_t mx_la_chunk_coef_bytes(int T, int n, int dk, int dv) {
+  if (T <= 0 || !chunk_shape(dk, dv)) return 0;
+  return (size_t)n * ((T + kC - 1) / kC) * kCoef * sizeof(float);
+}
+
+// Chunked scan for the head shapes it is built for (key and value heads of 64 or 128), with
+// `coef` of mx_la_chunk_coef_bytes; MX_ERR_UNSUPPORTED for other shapes (the caller then
+// runs the token-sequential scan).
 int mx_la_chunked_scan(const float* q, const float* kb, const float* v, const float* decay,
-                       int T, int n, int dk, int dv, float* o, hipStream_t s) {
+                       int T, int n, int dk, int dv, float* o, void* coef, hipStream_t s) {
   if (T <= 0 || n <= 0) return MX_ERR_INVALID;
+  if (!chunk_shape(dk, dv) || !coef) return MX_ERR_UNSUPPORTED;
   if ((long)T * n * (dk > dv ? dk : dv) >= (1l << 31)) return MX_ERR_UNSUPPORTED;
-  if (!mx_aligned16(q) || !mx_aligned16(kb) || !mx_aligned16(v)) return MX_ERR_UNSUPPORTED;
-  if (dk == 128 && dv == 128) return launch_chunked<128, 128>(q, kb, v, decay, T, n, o, s);
-  if (dk == 64 && dv == 64) return launch_chunked<64, 64>(q, kb, v, decay, T, n, o, s);
-  if (dk == 128 && dv == 64) return launch_chunked<128, 64>(q, kb, v, decay, T, n, o, s);
-  if (dk == 64 && dv == 128) return launch_chunked<64, 128>(q, kb, v, decay, T, n, o, s);
-  return MX_ERR_UNSUPPORTED;
+  if (!mx_aligned16(q) || !mx_aligned16(kb) || !mx_aligned16(v) || !mx_aligned16(o) ||
+      !mx_aligned16(coef))
+    return MX_ERR_UNSUPPORTED;
+  float* cf = (float*)coef;
+  if (dk == 128 && dv == 128) return launch_chunked<128, 128>(q, kb, v, decay, T, n, o, cf, s);
+  if (dk == 64 && dv == 64) return launch_chunked<64, 64>(q, kb, v, decay, T, n, o, cf, s);
+  if (dk == 128 && dv == 64) return launch_chunked<128, 64>(q, kb, v, decay, T, n, o, cf, s);
+  return launch_chunked<64, 128>(q, kb, v, decay, T, n, o, cf, s);
 }

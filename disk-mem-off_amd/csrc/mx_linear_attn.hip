@@ -66,7 +66,8 @@ struct Carve {
 
 struct LaWork {
   MxLinearAttnViews v;
-  MxDenseWork dw;  // projections: entry 0 qkvz, 1 ba, 2 out
+  MxDenseWork dw;      // projections: entry 0 qkvz, 1 ba, 2 out
+  void* coef = nullptr;  // decay coefficients of the chunked scan (NULL: sequential scan)
 };
 
 int layout(const MxLinearAttnDesc* d, int T, void* ws, LaWork* w, size_t* total) {
@@ -90,6 +91,8 @@ int layout(const MxLinearAttnDesc* d, int T, void* ws, LaWork* w, size_t* total)
   t.v.y = (float*)c.take(Tn * m.H * 4);
   char* dwb = (char*)c.take(mx_dense_work_bytes((int)Tn, d->weight_dtype, 3));
   mx_dense_work_carve(dwb, (int)Tn, d->weight_dtype, 3, &t.dw);
+  const size_t cb = mx_la_chunk_coef_bytes((int)Tn, m.n, m.dk, m.dv);
+  t.coef = cb ? c.take(cb) : nullptr;
   if (w) *w = t;
   if (total) *total = mx_align_up(c.off, 256);
   return MX_OK;
@@ -542,9 +545,9 @@ int launch_scan(const float* q, const float* kb, const float* v, const float* de
 #define MX_LA_CHUNK_MIN_T 64
 #endif
 int scan_launch(const float* q, const float* kb, const float* v, const float* decay, int T,
-                int n, int dk, int dv, float* o, hipStream_t s) {
-  if (T >= MX_LA_CHUNK_MIN_T) {
-    const int rc = mx_la_chunked_scan(q, kb, v, decay, T, n, dk, dv, o, s);
+                int n, int dk, int dv, float* o, void* coef, hipStream_t s) {
+  if (T >= MX_LA_CHUNK_MIN_T && coef) {
+    const int rc = mx_la_chunked_scan(q, kb, v, decay, T, n, dk, dv, o, coef, s);
     if (rc != MX_ERR_UNSUPPORTED) return rc;
   }
   switch (dk) {
@@ -684,7 +687,8 @@ int run_stage(int st, const MxLinearAttnDesc* d, const MxLinearAttnWeights* w, c
       return mx_launch_status();
     }
     case 4:
-      return scan_launch(k.v.q, k.v.kb, k.v.v, k.v.decay, T, m.n, m.dk, m.dv, k.v.o, s);
+      return scan_launch(k.v.q, k.v.kb, k.v.v, k.v.decay, T, m.n, m.dk, m.dv, k.v.o, k.coef,
+                         s);
     case 5:
       mx_clear_error();
       if (m.vd <= 256 * 4)
@@ -786,6 +790,32 @@ extern "C" int mx_gated_delta_scan(const float* q, const float* kb, const float*
       head_dim_v <= 0)
     return MX_ERR_INVALID;
   if (tokens == 0) return MX_OK;
-  return scan_launch(q, kb, v, decay, tokens, n_heads, head_dim_k, head_dim_v, o,
+  return scan_launch(q, kb, v, decay, tokens, n_heads, head_dim_k, head_dim_v, o, nullptr,
                      (hipStream_t)stream);
+}
+
+extern "C" int mx_gated_delta_scan_workspace_size(int32_t tokens, int32_t n_heads,
+                                                  int32_t head_dim_k, int32_t head_dim_v,
+                                                  size_t* nbytes) {
+  if (!nbytes || tokens < 0 || n_heads <= 0 || head_dim_k <= 0 || head_dim_v <= 0)
+    return MX_ERR_INVALID;
+  *nbytes = tokens >= MX_LA_CHUNK_MIN_T
+                ? mx_la_chunk_coef_bytes(tokens, n_heads, head_dim_k, head_dim_v)
+                : 0;
+  return MX_OK;
+}
+
+extern "C" int mx_gated_delta_scan_ws(const float* q, const float* kb, const float* v,
+                                      const float* decay, int32_t tokens, int32_t n_heads,
+                                      int32_t head_dim_k, int32_t head_dim_v, float* o,
+                                      void* workspace, size_t workspace_bytes, void* stream) {
+  if (!q || !kb || !v || !decay || !o || tokens < 0 || n_heads <= 0 || head_dim_k <= 0 ||
+      head_dim_v <= 0)
+    return MX_ERR_INVALID;
+  if (tokens == 0) return MX_OK;
+  size_t need = 0;
+  MX_TRY(mx_gated_delta_scan_workspace_size(tokens, n_heads, head_dim_k, head_dim_v, &need));
+  if (need && (!workspace || workspace_bytes < need)) return MX_ERR_WORKSPACE;
+  return scan_launch(q, kb, v, decay, tokens, n_heads, head_dim_k, head_dim_v, o,
+                     need ? workspace : nullptr, (hipStream_t)stream);
 }

@@ -214,6 +214,11 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                                      c_size_t, c_void_p, P(c_void_p), c_int32]),
     "mx_gated_delta_scan": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32,
                                            c_int32, c_int32, c_int32, c_void_p, c_void_p]),
+    "mx_gated_delta_scan_workspace_size": (ctypes.c_int, [c_int32, c_int32, c_int32, c_int32,
+                                                          P(c_size_t)]),
+    "mx_gated_delta_scan_ws": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32,
+                                              c_int32, c_int32, c_int32, c_void_p, c_void_p,
+                                              c_size_t, c_void_p]),
 }
 
 _lock = threading.Lock()

@@ -454,10 +454,23 @@ int mx_full_attn_forward_profiled(const MxFullAttnDesc* desc, const MxFullAttnWe
                                   int32_t n_events);
 
 /* The recurrence alone (qwen3_next.py:56-95 with beta * k formed): q, kb [T, n dk],
- * v, o [T, n dv], decay [T, n] = exp(g), all fp32 on the device.                      */
+ * v, o [T, n dv], decay [T, n] = exp(g), all fp32 on the device.  Token-sequential.     */
 int mx_gated_delta_scan(const float* q, const float* kb, const float* v, const float* decay,
                         int32_t tokens, int32_t n_heads, int32_t head_dim_k,
                         int32_t head_dim_v, float* o, void* stream);
+/* The same recurrence (qwen3_next.py:56-95) with a caller workspace: from 64 tokens, for
+ * key and value heads of 64 or 128, in chunks of 64 tokens on fp32 MFMA (the products
+ * inside a chunk in parallel, then one pass over the chunks per head carrying the state);
+ * other shapes and shorter inputs run the token-sequential scan.  The workspace holds the
+ * per-chunk decay coefficients (mx_gated_delta_scan_workspace_size bytes, 0 when the
+ * sequential scan runs); a smaller one gives MX_ERR_WORKSPACE.  The linear-attention
+ * block uses this form inside its own workspace.                                       */
+int mx_gated_delta_scan_workspace_size(int32_t tokens, int32_t n_heads, int32_t head_dim_k,
+                                       int32_t head_dim_v, size_t* nbytes);
+int mx_gated_delta_scan_ws(const float* q, const float* kb, const float* v,
+                           const float* decay, int32_t tokens, int32_t n_heads,
+                           int32_t head_dim_k, int32_t head_dim_v, float* o, void* workspace,
+                           size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

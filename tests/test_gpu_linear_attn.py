@@ -54,20 +54,41 @@ def test_scan_matches_oracle(mi355x, stream, n, dk, dv, T, gs):
     v = rng.standard_normal((T, n * dv)).astype(np.float32)
     g = (-np.abs(rng.standard_normal((T, n))) * gs).astype(np.float32)
     decay = np.exp(g).astype(np.float32)
-    bufs = [upload(mi355x, stream, a) for a in (q, kb, v, decay)]
-    o = mi355x.alloc_device(T * n * dv * 4)
-    try:
-        lib = _lib.load()
-        _lib.check(lib.mx_gated_delta_scan(bufs[0].handle, bufs[1].handle, bufs[2].handle,
-                                           bufs[3].handle, T, n, dk, dv, o.handle, stream))
-        got = read_device(mi355x, o.handle, np.float32, T * n * dv, stream).reshape(T, -1)
-    finally:
-        for b in bufs + [o]:
-            mi355x.free_device(b)
     ref = la.gated_recurrence(q, kb, v, g, n, dk, dv)
-    err = normwise_err(got, ref)
-    say(f"    normwise err {err:.2e}")
-    assert err <= 1e-5
+    for form in ("sequential", "workspace"):
+        got = run_scan(mi355x, stream, (q, kb, v, decay), T, n, dk, dv, form)
+        err = normwise_err(got, ref)
+        say(f"    {form}: normwise err {err:.2e}")
+        assert err <= 1e-5
+
+
+def run_scan(mi355x, stream, arrays, T, n, dk, dv, form):
+    """mx_gated_delta_scan (token-sequential) or mx_gated_delta_scan_ws (chunked from 64
+    tokens for heads of 64 / 128) on uploaded copies of ``arrays``."""
+    lib = _lib.load()
+    bufs = [upload(mi355x, stream, a) for a in arrays]
+    o = mi355x.alloc_device(T * n * dv * 4)
+    ws = None
+    try:
+        if form == "sequential":
+            _lib.check(lib.mx_gated_delta_scan(*(b.handle for b in bufs), T, n, dk, dv,
+                                               o.handle, stream))
+        else:
+            nb = ctypes.c_size_t()
+            _lib.check(lib.mx_gated_delta_scan_workspace_size(T, n, dk, dv, ctypes.byref(nb)))
+            chunked = T >= 64 and dk in (64, 128) and dv in (64, 128)
+            assert (nb.value > 0) == chunked
+            ws = mi355x.alloc_device(max(nb.value, 16))
+            if nb.value:
+                rc = lib.mx_gated_delta_scan_ws(*(b.handle for b in bufs), T, n, dk, dv,
+                                                o.handle, ws.handle, nb.value - 4, stream)
+                assert rc == _lib.MX_ERR_WORKSPACE
+            _lib.check(lib.mx_gated_delta_scan_ws(*(b.handle for b in bufs), T, n, dk, dv,
+                                                  o.handle, ws.handle, nb.value, stream))
+        return read_device(mi355x, o.handle, np.float32, T * n * dv, stream).reshape(T, -1)
+    finally:
+        for b in bufs + [o] + ([ws] if ws is not None else []):
+            mi355x.free_device(b)
 
 
 @pytest.mark.parametrize("T", [70, 300])
@@ -86,18 +107,9 @@ def test_chunked_scan_zero_and_tiny_decays(mi355x, stream, T):
     g[11:20, 1] = -0.01
     decay = np.exp(g).astype(np.float32)
     assert decay[5, 0] == 0.0 and decay[10, 1] > 0.0
-    bufs = [upload(mi355x, stream, a) for a in (q, kb, v, decay)]
-    o = mi355x.alloc_device(T * n * dv * 4)
-    try:
-        _lib.check(_lib.load().mx_gated_delta_scan(bufs[0].handle, bufs[1].handle,
-                                                   bufs[2].handle, bufs[3].handle, T, n, dk,
-                                                   dv, o.handle, stream))
-        got = read_device(mi355x, o.handle, np.float32, T * n * dv, stream).reshape(T, -1)
-    finally:
-        for b in bufs + [o]:
-            mi355x.free_device(b)
     with np.errstate(divide="ignore"):
         ref = la.gated_recurrence(q, kb, v, np.log(decay), n, dk, dv)
+    got = run_scan(mi355x, stream, (q, kb, v, decay), T, n, dk, dv, "workspace")
     err = normwise_err(got, ref)
     say(f"    normwise err {err:.2e}")
     assert np.all(np.isfinite(got)) and err <= 1e-5
