@@ -28,6 +28,17 @@ namespace {
 
 constexpr int kC = 64;  // tokens per chunk
 
+typedef __amdgpu_buffer_rsrc_t mx_rsrc_t;
+
+// Buffer descriptor over `bytes` bytes: loads at offsets past the end return zeros.
+__device__ __forceinline__ mx_rsrc_t mx_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ int4_t mx_ld16(mx_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+
 __device__ __forceinline__ float4_t mfma4(float a, float b, float4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
@@ -91,8 +102,8 @@ struct Pad {
 
 // ---- intra-chunk part: o[t] = sum_{t0 <= s <= t} a(t, s) (kb_s . q_t) v_s ---------------
 // Block (chunk, head), 4 waves; wave w takes tokens 16 w .. 16 w + 15 of the chunk.  Its q
-// rows go straight into MFMA A registers; kb (B of the scores, all 64 tokens) and v
-// (transposed, B of the products with v) are shared through LDS, and the scores' LDS
+// rows go straight into MFMA A registers; kb (B of the scores, all 64 tokens) and v (B of
+// the products with v) are shared through LDS (row-major, 16-byte stores), and the kb
 // region is then reused for each wave's masked scores (A of the products with v).  Wave 0
 // also writes the chunk's coefficients for the state walk.
 template <int DK, int DV>
@@ -103,11 +114,11 @@ __global__ __launch_bounds__(256, 2) void k_la_chunk_intra(const float* __restri
                                                            int T, int n, int nchunk,
                                                            float* __restrict__ o,
                                                            float* __restrict__ coef) {
-  constexpr int SK = Pad<DK>::S, SC = Pad<kC>::S;
+  constexpr int SK = Pad<DK>::S, SC = Pad<kC>::S, SV = Pad<DV>::S;
   constexpr int KP = kC * DK / 4 / 256, VP = kC * DV / 4 / 256;  // float4 pieces per thread
   static_assert(4 * 16 * SC <= kC * SK, "masked scores reuse the kb tile");
   __shared__ __align__(16) float sK[kC * SK];    // kb tile, then the masked scores
-  __shared__ __align__(16) float sVt[DV * SC];   // v transposed: [value row][token]
+  __shared__ __align__(16) float sV[kC * SV];    // v tile [token][value row]
   __shared__ double sG[kC];
   __shared__ int sLR[kC];
 
@@ -146,10 +157,7 @@ __global__ __launch_bounds__(256, 2) void k_la_chunk_intra(const float* __restri
 #pragma unroll
   for (int p = 0; p < VP; ++p) {
     const int i = tid + 256 * p, r = i / (DV / 4), c = 4 * (i % (DV / 4));
-    sVt[(c + 0) * SC + r] = vr[p].x;
-    sVt[(c + 1) * SC + r] = vr[p].y;
-    sVt[(c + 2) * SC + r] = vr[p].z;
-    sVt[(c + 3) * SC + r] = vr[p].w;
+    *(float4*)(sV + r * SV + c) = vr[p];
   }
   __syncthreads();
 
@@ -180,7 +188,8 @@ __global__ __launch_bounds__(256, 2) void k_la_chunk_intra(const float* __restri
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 
-  // o = P V over the chunk's 64 tokens
+  // o = P V over the chunk's 64 tokens; token s = k0 + 4 qq + e of v row 16 nt + j (four
+  // rows per lane, one value each: lane groups qq sit 16 banks apart)
   constexpr int NV = DV / 16;
   float4_t oacc[NV];
 #pragma unroll
@@ -190,7 +199,8 @@ __global__ __launch_bounds__(256, 2) void k_la_chunk_intra(const float* __restri
     const float4 a = *(const float4*)(myP + j * SC + k0 + 4 * qq);
 #pragma unroll
     for (int nt = 0; nt < NV; ++nt) {
-      const float4 b = *(const float4*)(sVt + (16 * nt + j) * SC + k0 + 4 * qq);
+      const float* vp = sV + (k0 + 4 * qq) * SV + 16 * nt + j;
+      const float4 b = make_float4(vp[0], vp[SV], vp[2 * SV], vp[3 * SV]);
       oacc[nt] = mfma_k16(a, b, oacc[nt]);
     }
   }
@@ -221,10 +231,12 @@ __global__ __launch_bounds__(256, 2) void k_la_chunk_intra(const float* __restri
 // accumulators, wave w holding key columns 16 NT w .. 16 NT (w + 1) - 1; lane (j, qq) of a
 // tile holds S^T[4 qq + r][j], which is exactly the B operand of the output product when
 // lane group qq sums key columns 4 qq .. 4 qq + 3, so the state never leaves registers.
-// Each wave forms the output over its own key columns for all 64 tokens; the four partial
-// outputs are summed through LDS (double-buffered, one barrier per chunk) and added to the
-// intra-chunk part already in o.  The next chunk's operands are loaded while this one
-// computes.
+// Each wave forms the output over its own key columns for all 64 tokens (its q columns go
+// straight into A registers); the four partial outputs are summed through LDS and added
+// to the intra-chunk part already in o.  kb and v enter the state product with 4 tokens
+// per lane, so their rows are staged through LDS (row-major, 16-byte stores), double-
+// buffered: the next chunk's rows are loaded while this one computes and written to the
+// other buffer after it.  Loads go through buffer descriptors (rows past T read zero).
 template <int DK>
 __global__ __launch_bounds__(256) void k_la_chunk_state(const float* __restrict__ q,
                                                         const float* __restrict__ kb,
@@ -232,56 +244,87 @@ __global__ __launch_bounds__(256) void k_la_chunk_state(const float* __restrict_
                                                         const float* __restrict__ coef, int T,
                                                         int n, int dv, int nchunk,
                                                         float* __restrict__ o) {
-  constexpr int NT = DK / 64;  // 16-column state tiles per wave
-  constexpr int SO = 16 + 1;   // LDS row stride of a partial output (tokens x 16 rows)
-  __shared__ float sO[2][4][kC * SO];
+  constexpr int NT = DK / 64;                  // 16-column state tiles per wave
+  constexpr int SK = Pad<DK>::S;               // LDS row stride of the kb rows
+  constexpr int SV = 16 + 4;                   // LDS row stride of the v rows
+  constexpr int SO = 16 + 1;                   // LDS row stride of a partial output
+  constexpr int KP = kC * DK / 4 / 256;        // kb float4 pieces per thread and chunk
+  __shared__ __align__(16) float sK[2][kC * SK];  // kb rows [token][key column]
+  __shared__ __align__(16) float sV[2][kC * SV];  // this block's v columns [token][row]
+  __shared__ __align__(16) float sCf[2][kCoef];
+  __shared__ float sO[4][kC * SO];
 
-  const int blocks_per_head = dv / 16;
-  const int h = blockIdx.x / blocks_per_head, i0 = 16 * (blockIdx.x % blocks_per_head);
+  // Every block of a head reads the same q and kb rows: the blocks of one head run on one
+  // XCD (hardware block b runs on XCD b % 8), so those rows come from that XCD's L2 after
+  // the first block's read.
+  const int bph = dv / 16;  // blocks per head
+  int h, slice;
+  if ((n & 7) == 0) {
+    const int k = blockIdx.x >> 3;
+    h = (blockIdx.x & 7) * (n >> 3) + k / bph;
+    slice = k % bph;
+  } else {
+    h = blockIdx.x / bph;
+    slice = blockIdx.x % bph;
+  }
+  const int i0 = 16 * slice;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int j = lane & 15, qq = lane >> 4;
   const int qd = n * DK, vd = n * dv;
   const int cw = 16 * NT * w;  // this wave's first key column
+  const uint32_t qrow = (uint32_t)qd * 4, vrow = (uint32_t)vd * 4;
+  const mx_rsrc_t rq = mx_rsrc(q, (uint32_t)T * qrow);
+  const mx_rsrc_t rk = mx_rsrc(kb, (uint32_t)T * qrow);
+  const mx_rsrc_t rv = mx_rsrc(v, (uint32_t)T * vrow);
+  const mx_rsrc_t rc = mx_rsrc(coef, (uint32_t)(n * nchunk * kCoef * 4));
 
-  // operands of one chunk, in registers
-  struct Ops {
-    float4 qf[4][NT];  // q[t0 + 16 mt + j][cw + 16 u + 4 qq ..]          (A, output)
-    float kf[4][NT][4];  // kb[t0 + 16 kg + 4 qq + e][cw + 16 u + j]        (A, state)
-    float vf[4][4];      // v[t0 + 16 kg + 4 qq + e][i0 + j]                 (B, state)
-    float et[4];         // a(t, t0 - 1) of token 16 mt + j
-    float4 ws[4];        // a(end, s) of tokens 16 kg + 4 qq ..
-    float gam;
-    float oi[4];         // intra-chunk o of token 16 w + 4 qq + r, row i0 + j
-  };
-  auto load = [&](Ops& x, int ch) {
-    const int t0 = ch * kC;
-    const float* cf = coef + ((size_t)h * nchunk + ch) * kCoef;
+  // per-lane offsets: q fragment (token j of a 16-row group, columns cw + 4 qq ..), kb and v
+  // rows staged by this thread, coefficients
+  const uint32_t q_lane = (uint32_t)j * qrow + (uint32_t)(h * DK + cw + 4 * qq) * 4;
+  uint32_t k_lane[KP];
+  int k_lds[KP];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      const int t = t0 + 16 * mt + j;
+  for (int p = 0; p < KP; ++p) {
+    const int i = tid + 256 * p, r = i / (DK / 4), c = 4 * (i % (DK / 4));
+    k_lane[p] = (uint32_t)r * qrow + (uint32_t)(h * DK + c) * 4;
+    k_lds[p] = r * SK + c;
+  }
+  const int vr = tid >> 2, vc = 4 * (tid & 3);  // v: token vr, rows i0 + vc .. + 3
+  const uint32_t v_lane = (uint32_t)vr * vrow + (uint32_t)(h * dv + i0 + vc) * 4;
+
+  struct Staged {
+    int4_t k[KP];
+    int4_t v;
+    int4_t cf;
+  };
+  auto load_staged = [&](Staged& x, int ch) {
+    const uint32_t base = (uint32_t)ch * kC * qrow;
+#pragma unroll
+    for (int p = 0; p < KP; ++p) x.k[p] = mx_ld16(rk, k_lane[p] + base);
+    x.v = mx_ld16(rv, v_lane + (uint32_t)ch * kC * vrow);
+    x.cf = tid < kCoef / 4 ? mx_ld16(rc, (uint32_t)(((size_t)h * nchunk + ch) * kCoef * 4 + 16 * tid))
+                           : (int4_t){0, 0, 0, 0};
+  };
+  auto store_staged = [&](const Staged& x, int b) {
+#pragma unroll
+    for (int p = 0; p < KP; ++p) *(int4_t*)(sK[b] + k_lds[p]) = x.k[p];
+    *(int4_t*)(sV[b] + vr * SV + vc) = x.v;
+    if (tid < kCoef / 4) *(int4_t*)(sCf[b] + 4 * tid) = x.cf;
+  };
+  struct Direct {
+    int4_t qf[4][NT];  // q[t0 + 16 mt + j][cw + 16 u + 4 qq ..]  (A of the output product)
+    float oi[4];       // intra-chunk o of token 16 w + 4 qq + r, row i0 + j
+  };
+  auto load_direct = [&](Direct& x, int ch) {
+    const uint32_t base = (uint32_t)ch * kC * qrow;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
       for (int u = 0; u < NT; ++u)
-        x.qf[mt][u] = t < T ? *(const float4*)(q + (size_t)t * qd + h * DK + cw + 16 * u + 4 * qq)
-                            : make_float4(0.f, 0.f, 0.f, 0.f);
-      x.et[mt] = cf[16 * mt + j];
-    }
-#pragma unroll
-    for (int kg = 0; kg < 4; ++kg) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int t = t0 + 16 * kg + 4 * qq + e;
-        const bool ok = t < T;
-#pragma unroll
-        for (int u = 0; u < NT; ++u)
-          x.kf[kg][u][e] = ok ? kb[(size_t)t * qd + h * DK + cw + 16 * u + j] : 0.f;
-        x.vf[kg][e] = ok ? v[(size_t)t * vd + h * dv + i0 + j] : 0.f;
-      }
-      x.ws[kg] = *(const float4*)(cf + kC + 16 * kg + 4 * qq);
-    }
-    x.gam = cf[2 * kC];
+        x.qf[mt][u] = mx_ld16(rq, q_lane + base + (uint32_t)(16 * mt) * qrow + 64u * u);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int t = t0 + 16 * w + 4 * qq + r;
+      const int t = ch * kC + 16 * w + 4 * qq + r;
       x.oi[r] = t < T ? o[(size_t)t * vd + h * dv + i0 + j] : 0.f;
     }
   };
@@ -289,58 +332,116 @@ __global__ __launch_bounds__(256) void k_la_chunk_state(const float* __restrict_
   float4_t st[NT];
 #pragma unroll
   for (int u = 0; u < NT; ++u) st[u] = (float4_t){0.f, 0.f, 0.f, 0.f};
-  Ops cur, nxt;
-  load(cur, 0);
-  for (int ch = 0; ch < nchunk; ++ch) {
-    if (ch + 1 < nchunk) load(nxt, ch + 1);
-    // partial output over this wave's key columns, all 64 tokens: A = a(t) q_t, B = S^T
-    float4_t op[4];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      op[mt] = (float4_t){0.f, 0.f, 0.f, 0.f};
-      const float et = cur.et[mt];
-#pragma unroll
-      for (int u = 0; u < NT; ++u) {
-        const float4 a = cur.qf[mt][u];
-        op[mt] = mfma4(a.x * et, st[u][0], op[mt]);
-        op[mt] = mfma4(a.y * et, st[u][1], op[mt]);
-        op[mt] = mfma4(a.z * et, st[u][2], op[mt]);
-        op[mt] = mfma4(a.w * et, st[u][3], op[mt]);
-      }
-    }
-    // state update: S^T <- a(end) S^T + sum_s kb_s (a(end, s) v_s)^T
-#pragma unroll
-    for (int u = 0; u < NT; ++u) st[u] *= cur.gam;
+
+  // one chunk: operands in LDS buffer b and in x.  The output product reads the old state
+  // and the new contribution goes into fresh accumulators, so the two groups of MFMAs (four
+  // independent chains each, no VALU between them) do not wait on each other; the state is
+  // combined at the end: S^T <- a(end) S^T + U^T.
+  auto step = [&](const Direct& x, int ch, int b) {
+    const float* cf = sCf[b];
+    // contribution U^T = sum_s kb_s (a(end, s) v_s)^T: B operands first (v times a(end, s))
+    // token s = 16 kg + 4 qq + e: kb[s][cw + 16 u + j] (A) and v[s][i0 + j] a(end, s) (B),
+    // four rows per lane read one value each (lane groups qq sit 16 banks apart)
+    float bv[4][4];
 #pragma unroll
     for (int kg = 0; kg < 4; ++kg) {
-      const float b0 = cur.vf[kg][0] * cur.ws[kg].x, b1 = cur.vf[kg][1] * cur.ws[kg].y;
-      const float b2 = cur.vf[kg][2] * cur.ws[kg].z, b3 = cur.vf[kg][3] * cur.ws[kg].w;
+      const float4 ws = *(const float4*)(cf + kC + 16 * kg + 4 * qq);
+      const float* vp = sV[b] + (16 * kg + 4 * qq) * SV + j;
+      bv[kg][0] = vp[0] * ws.x;
+      bv[kg][1] = vp[SV] * ws.y;
+      bv[kg][2] = vp[2 * SV] * ws.z;
+      bv[kg][3] = vp[3 * SV] * ws.w;
+    }
+    float4 ka[4][NT];
+#pragma unroll
+    for (int kg = 0; kg < 4; ++kg)
 #pragma unroll
       for (int u = 0; u < NT; ++u) {
-        st[u] = mfma4(cur.kf[kg][u][0], b0, st[u]);
-        st[u] = mfma4(cur.kf[kg][u][1], b1, st[u]);
-        st[u] = mfma4(cur.kf[kg][u][2], b2, st[u]);
-        st[u] = mfma4(cur.kf[kg][u][3], b3, st[u]);
+        const float* kp = sK[b] + (16 * kg + 4 * qq) * SK + cw + 16 * u + j;
+        ka[kg][u] = make_float4(kp[0], kp[SK], kp[2 * SK], kp[3 * SK]);
       }
-    }
-    // sum of the four waves' partial outputs; lane (j, qq) holds op[mt][r] for token
-    // 16 mt + 4 qq + r, row j
-    float* so = sO[ch & 1][w];
+    // partial output over this wave's key columns, all 64 tokens: (q_t S^T) scaled by a(t)
+    float4_t op[4], ua[NT], ub[NT];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) op[mt] = (float4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < NT; ++u) ua[u] = ub[u] = (float4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < NT; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+          const float4 a = __builtin_bit_cast(float4, x.qf[mt][u]);
+          const float av = e == 0 ? a.x : (e == 1 ? a.y : (e == 2 ? a.z : a.w));
+          op[mt] = mfma4(av, st[u][e], op[mt]);
+        }
+        // two state chains per tile: token groups 0-1 and 2-3
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) {
+          const float4 k0 = ka[2 * kh][u], k1 = ka[2 * kh + 1][u];
+          const float ka0 = e == 0 ? k0.x : (e == 1 ? k0.y : (e == 2 ? k0.z : k0.w));
+          const float ka1 = e == 0 ? k1.x : (e == 1 ? k1.y : (e == 2 ? k1.z : k1.w));
+          float4_t& acc = kh == 0 ? ua[u] : ub[u];
+          acc = mfma4(ka0, bv[2 * kh][e], acc);
+          acc = mfma4(ka1, bv[2 * kh + 1][e], acc);
+        }
+      }
+    const float gam = cf[2 * kC];
+#pragma unroll
+    for (int u = 0; u < NT; ++u) st[u] = st[u] * gam + ua[u] + ub[u];
+    // lane (j, qq) holds op[mt][r] for token 16 mt + 4 qq + r, row j
+    float* so = sO[w];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) so[(16 * mt + 4 * qq + r) * SO + j] = op[mt][r];
-    __syncthreads();
+      for (int r = 0; r < 4; ++r)
+        so[(16 * mt + 4 * qq + r) * SO + j] = op[mt][r] * cf[16 * mt + 4 * qq + r];
+    (void)ch;
+  };
+  auto finish = [&](const Direct& x, int ch) {
     const int t0 = ch * kC;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int tl = 16 * w + 4 * qq + r, t = t0 + tl;
-      float sum = cur.oi[r];
+      float sum = x.oi[r];
 #pragma unroll
-      for (int w2 = 0; w2 < 4; ++w2) sum += sO[ch & 1][w2][tl * SO + j];
+      for (int w2 = 0; w2 < 4; ++w2) sum += sO[w2][tl * SO + j];
       if (t < T) o[(size_t)t * vd + h * dv + i0 + j] = sum;
     }
-    if (ch + 1 < nchunk) cur = nxt;
+  };
+
+  Staged sg;
+  Direct da, db;
+  load_staged(sg, 0);
+  load_direct(da, 0);
+  store_staged(sg, 0);
+  __syncthreads();
+  // Iteration ch: loads of chunk ch + 1 in flight while chunk ch computes from LDS buffer
+  // ch & 1; the staged rows then go to the other buffer.  Two chunks per pass so the
+  // direct operands alternate between two register sets without copies.
+  for (int ch = 0; ch < nchunk; ch += 2) {
+    const bool more1 = ch + 1 < nchunk;
+    if (more1) {
+      load_staged(sg, ch + 1);
+      load_direct(db, ch + 1);
+    }
+    step(da, ch, 0);
+    __syncthreads();  // partial outputs complete; LDS buffer 0 read
+    finish(da, ch);
+    if (more1) store_staged(sg, 1);
+    __syncthreads();  // buffer 1 written, partial outputs read
+    if (!more1) break;
+    const bool more2 = ch + 2 < nchunk;
+    if (more2) {
+      load_staged(sg, ch + 2);
+      load_direct(da, ch + 2);
+    }
+    step(db, ch + 1, 1);
+    __syncthreads();
+    finish(db, ch + 1);
+    if (more2) store_staged(sg, 0);
+    __syncthreads();
   }
 }
 
@@ -373,7 +474,8 @@ int mx_la_chunked_scan(const float* q, const float* kb, const float* v, const fl
                        int T, int n, int dk, int dv, float* o, void* coef, hipStream_t s) {
   if (T <= 0 || n <= 0) return MX_ERR_INVALID;
   if (!chunk_shape(dk, dv) || !coef) return MX_ERR_UNSUPPORTED;
-  if ((long)T * n * (dk > dv ? dk : dv) >= (1l << 31)) return MX_ERR_UNSUPPORTED;
+  // buffer descriptors: byte offsets below 2^31
+  if ((long)T * n * (dk > dv ? dk : dv) * 4 >= (1l << 31)) return MX_ERR_UNSUPPORTED;
   if (!mx_aligned16(q) || !mx_aligned16(kb) || !mx_aligned16(v) || !mx_aligned16(o) ||
       !mx_aligned16(coef))
     return MX_ERR_UNSUPPORTED;
