@@ -33,6 +33,15 @@ static inline bool mx_aligned16(const void* p) { return ((uintptr_t)p & 15u) == 
 __device__ __forceinline__ float mx_load_param(const void* p, int dtype, int i) {
   return dtype == MX_DT_F16 ? (float)((const half_t*)p)[i] : ((const float*)p)[i];
 }
+// Elements i .. i + 3 in one load (16-byte aligned fp32 or 8-byte aligned fp16 at i).
+__device__ __forceinline__ float4 mx_load_param4(const void* p, int dtype, int i) {
+  if (dtype == MX_DT_F16) {
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    const h4 v = *(const h4*)((const half_t*)p + i);
+    return make_float4((float)v[0], (float)v[1], (float)v[2], (float)v[3]);
+  }
+  return *(const float4*)((const float*)p + i);
+}
 
 // Wave reductions: DPP swaps inside each 16-lane row (quad pairs, quads, half-rows), then
 // the four row totals are read with v_readlane, so no step goes through LDS.  The result

@@ -7,6 +7,102 @@
 #include "mx_dispatch_dev.h"
 
 #define TK_MAXK 32
+#ifndef TK_SB
+#define TK_SB 4  // logit slices loaded together by the top-k
+#endif
+
+// ---- selection core shared by the top-k variants ----------------------------------
+// Images: keys mapped to order-preserving 32-bit values (NaN counts as -inf, -0 as +0;
+// 0 marks an absent entry).  A most-significant-bit-first search with wave ballots finds
+// a threshold tau with exactly the k largest images at or above it when they are distinct
+// from the rest: the search stops as soon as the count at the candidate is exactly k
+// (random keys: after about log2(entries) + 3 of the 32 steps); otherwise it ends at the
+// k-th largest image.  Every image above tau is chosen, and the ties at tau in ascending
+// entry order until k are filled, so the chosen set is the one k rounds of arg-max with
+// ties to the lower entry give.
+__device__ __forceinline__ uint32_t mx_key_image(float kv, bool valid) {
+  if (kv != kv) kv = -INFINITY;
+  if (kv == 0.f) kv = 0.f;
+  const uint32_t b = __builtin_bit_cast(uint32_t, kv);
+  return valid ? ((b & 0x80000000u) ? ~b : (b | 0x80000000u)) : 0u;
+}
+
+template <int V>
+__device__ __forceinline__ void mx_choose_k(const uint32_t (&u)[V], int k, bool (&sel)[V]) {
+  const int lane = threadIdx.x & 63;
+  uint32_t tau = 0;
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cand = tau | (1u << bit);
+    unsigned long long m[V];  // all compares first: independent mask registers
+#pragma unroll
+    for (int i = 0; i < V; ++i) m[i] = __builtin_amdgcn_uicmp(u[i], cand, 35 /* uge */);
+    int c = 0;
+#pragma unroll
+    for (int i = 0; i < V; ++i) c += __popcll(m[i]);
+    if (c >= k) {
+      tau = cand;
+      if (c == k) break;
+    }
+  }
+  const unsigned long long below = (1ull << lane) - 1ull;
+  int ngt = 0;
+#pragma unroll
+  for (int i = 0; i < V; ++i) ngt += __popcll(__ballot(u[i] > tau));
+  int ties = 0;
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const unsigned long long eq = __ballot(u[i] == tau);
+    sel[i] = u[i] > tau || (u[i] == tau && ties + __popcll(eq & below) < k - ngt);
+    ties += __popcll(eq);
+  }
+}
+
+// Slots of the k chosen entries (image, id, payload): slot = number of chosen entries
+// ahead (larger image, or equal image and lower id).  The chosen are packed into a
+// per-wave LDS row in entry order, lane r < k takes entry r and counts the entries
+// ahead of it with k wave-uniform reads, and the packed row is rewritten in slot order;
+// lane r < k returns slot r's id and payload.
+template <int V>
+__device__ __forceinline__ void mx_slots_of(const bool (&sel)[V], const uint32_t (&u)[V],
+                                            const int (&id)[V], const float (&w)[V], int k,
+                                            int& my_id, float& my_w) {
+  __shared__ uint32_t s_u[16][TK_MAXK];
+  __shared__ int s_id[16][TK_MAXK];
+  __shared__ float s_w[16][TK_MAXK];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const unsigned long long below = (1ull << lane) - 1ull;
+  int ahead = 0;
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const unsigned long long m = __ballot(sel[i]);
+    if (sel[i]) {
+      const int pos = ahead + __popcll(m & below);
+      s_u[wv][pos] = u[i];
+      s_id[wv][pos] = id[i];
+      s_w[wv][pos] = w[i];
+    }
+    ahead += __popcll(m);
+  }
+  mx_lds_fence();
+  const uint32_t ur = lane < k ? s_u[wv][lane] : 0u;
+  const int ir = lane < k ? s_id[wv][lane] : 0;
+  const float wr = lane < k ? s_w[wv][lane] : 0.f;
+  mx_lds_fence();  // every lane has its entry before the row is rewritten
+  int rank = 0;
+  for (int j = 0; j < k; ++j) {
+    const uint32_t uj = (uint32_t)__builtin_amdgcn_readlane((int)ur, j);
+    const int ij = __builtin_amdgcn_readlane(ir, j);
+    rank += (uj > ur || (uj == ur && ij < ir)) ? 1 : 0;
+  }
+  if (lane < k) {
+    s_id[wv][rank] = ir;
+    s_w[wv][rank] = wr;
+  }
+  mx_lds_fence();
+  my_id = lane < k ? s_id[wv][lane] : 0;
+  my_w = lane < k ? s_w[wv][lane] : 0.f;
+  mx_lds_fence();  // the rows are reused by this wave's next call
+}
 
 // The selection of one token by one wave: lane r < k holds slot r's expert id and its
 // final weight (renormalised and scaled as configured).
@@ -36,10 +132,21 @@ __device__ __forceinline__ MxSel mx_topk_select(const float* __restrict__ logits
 #pragma unroll
     for (int i = 0; i < VPT; ++i) bs[i] = ((const float*)bias)[min(lane + 64 * i, E - 1)];
   }
-  for (int s = 1; s < S; ++s)
+  // Later slices TK_SB at a time: every load of a batch is issued (slice index clamped)
+  // before the adds, which run in slice order and skip the clamped repeats.
+  for (int s0 = 1; s0 < S; s0 += TK_SB) {
+    float ps[TK_SB][VPT];
 #pragma unroll
-    for (int i = 0; i < VPT; ++i)
-      lg[i] += logits[((size_t)s * T + t) * E1 + min(lane + 64 * i, E - 1)];
+    for (int u = 0; u < TK_SB; ++u)
+#pragma unroll
+      for (int i = 0; i < VPT; ++i)
+        ps[u][i] = logits[((size_t)min(s0 + u, S - 1) * T + t) * E1 + min(lane + 64 * i, E - 1)];
+#pragma unroll
+    for (int u = 0; u < TK_SB; ++u)
+#pragma unroll
+      for (int i = 0; i < VPT; ++i)
+        if (s0 + u < S) lg[i] += ps[u][i];
+  }
   float key[VPT], wsrc[VPT];
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
@@ -71,75 +178,18 @@ __device__ __forceinline__ MxSel mx_topk_select(const float* __restrict__ logits
     for (int i = 0; i < VPT; ++i) wsrc[i] = wsrc[i] / sum;
   }
 
-  // Selection without a per-round arg-max.  Keys map to order-preserving 32-bit images
-  // (NaN counts as -inf, -0 as +0; 0 marks an absent expert).  A most-significant-bit-first
-  // search with wave ballots finds tau, the k-th largest image; every image above tau is
-  // taken, and the ties at tau in ascending expert id until k are filled.  A chosen
-  // expert's slot is the number of chosen experts ahead of it (larger key, or equal key
-  // and lower id), i.e. the order k rounds of arg-max with ties to the lower id give.
   uint32_t u[VPT];
+  int eid[VPT];
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
-    float kv = key[i];
-    if (kv != kv) kv = -INFINITY;
-    if (kv == 0.f) kv = 0.f;
-    const uint32_t b = __builtin_bit_cast(uint32_t, kv);
-    u[i] = (lane + 64 * i < E) ? ((b & 0x80000000u) ? ~b : (b | 0x80000000u)) : 0u;
+    eid[i] = lane + 64 * i;
+    u[i] = mx_key_image(key[i], eid[i] < E);
   }
-  uint32_t tau = 0;
-  for (int bit = 31; bit >= 0; --bit) {
-    const uint32_t cand = tau | (1u << bit);
-    unsigned long long m[VPT];  // all compares first: independent mask registers
-#pragma unroll
-    for (int i = 0; i < VPT; ++i) m[i] = __builtin_amdgcn_uicmp(u[i], cand, 35 /* uge */);
-    int c = 0;
-#pragma unroll
-    for (int i = 0; i < VPT; ++i) c += __popcll(m[i]);
-    if (c >= k) tau = cand;
-  }
-  const unsigned long long below = (1ull << lane) - 1ull;
-  int ngt = 0;
-#pragma unroll
-  for (int i = 0; i < VPT; ++i) ngt += __popcll(__ballot(u[i] > tau));
   bool sel[VPT];
-  int ties = 0;
-#pragma unroll
-  for (int i = 0; i < VPT; ++i) {
-    const unsigned long long eq = __ballot(u[i] == tau);
-    sel[i] = u[i] > tau || (u[i] == tau && ties + __popcll(eq & below) < k - ngt);
-    ties += __popcll(eq);
-  }
-  int rank[VPT];
-#pragma unroll
-  for (int i = 0; i < VPT; ++i) rank[i] = 0;
-#pragma unroll
-  for (int iy = 0; iy < VPT; ++iy) {
-    unsigned long long m = __ballot(sel[iy]);
-    while (m) {
-      const int ly = __builtin_ctzll(m);
-      m &= m - 1ull;
-      const uint32_t uy = (uint32_t)__builtin_amdgcn_readlane((int)u[iy], ly);
-      const int ey = ly + 64 * iy;
-#pragma unroll
-      for (int i = 0; i < VPT; ++i)
-        rank[i] += (uy > u[i] || (uy == u[i] && ey < lane + 64 * i)) ? 1 : 0;
-    }
-  }
-  // Chosen experts land in their slots of a per-wave LDS row; lane r then owns slot r.
-  __shared__ int s_id[16][TK_MAXK];
-  __shared__ float s_w[16][TK_MAXK];
-  const int wv = threadIdx.x >> 6;
-#pragma unroll
-  for (int i = 0; i < VPT; ++i) {
-    if (sel[i]) {
-      s_id[wv][rank[i]] = lane + 64 * i;
-      s_w[wv][rank[i]] = wsrc[i];
-    }
-  }
-  mx_lds_fence();
-  const int my_id = lane < k ? s_id[wv][lane] : 0;
-  const float my_w = lane < k ? s_w[wv][lane] : 0.f;
-  mx_lds_fence();  // the row is reused by this wave's next token
+  mx_choose_k(u, k, sel);
+  int my_id;
+  float my_w;
+  mx_slots_of(sel, u, eid, wsrc, k, my_id, my_w);
   float sum = 0.f;  // sequential over the k slots, identical on every lane
   for (int r = 0; r < k; ++r) sum += mx_readlane(my_w, r);
   return MxSel{my_id, (norm ? my_w / (sum + 1e-20f) : my_w) * scaling};
@@ -250,12 +300,6 @@ struct MxTopkPar {
   float m[16], sm[16];
 };
 
-__device__ __forceinline__ uint32_t mx_key_image(float kv, bool valid) {
-  if (kv != kv) kv = -INFINITY;
-  if (kv == 0.f) kv = 0.f;
-  const uint32_t b = __builtin_bit_cast(uint32_t, kv);
-  return valid ? ((b & 0x80000000u) ? ~b : (b | 0x80000000u)) : 0u;
-}
 
 // Phase 1, by wave `wv` < T * NP of the block: candidates of token wv / NP.  A part holds
 // 64 * VPC consecutive experts (VPC per lane, lane-major within each 64).
@@ -300,26 +344,14 @@ __device__ __forceinline__ void mx_topk_par_cand(MxTopkPar& sh, const float* __r
   uint32_t u[VPC];
 #pragma unroll
   for (int i = 0; i < VPC; ++i) u[i] = mx_key_image(key[i], valid[i]);
-  uint32_t tau = 0;
-  for (int bit = 31; bit >= 0; --bit) {
-    const uint32_t cand = tau | (1u << bit);
-    int c = 0;
-#pragma unroll
-    for (int i = 0; i < VPC; ++i) c += __popcll(__builtin_amdgcn_uicmp(u[i], cand, 35 /* uge */));
-    if (c >= k) tau = cand;
-  }
+  bool sel[VPC];
+  mx_choose_k(u, k, sel);
   const unsigned long long below = (1ull << lane) - 1ull;
-  int ngt = 0;
-#pragma unroll
-  for (int i = 0; i < VPC; ++i) ngt += __popcll(__ballot(u[i] > tau));
-  int ties = 0, ahead = 0;
+  int ahead = 0;
 #pragma unroll
   for (int i = 0; i < VPC; ++i) {
-    const unsigned long long eq = __ballot(u[i] == tau);
-    const bool sel = u[i] > tau || (u[i] == tau && ties + __popcll(eq & below) < k - ngt);
-    ties += __popcll(eq);
-    const unsigned long long sm = __ballot(sel);
-    if (sel) {
+    const unsigned long long sm = __ballot(sel[i]);
+    if (sel[i]) {
       const int slot = t * NP * k + part * k + ahead + __popcll(sm & below);
       sh.u[slot] = u[i];
       sh.id[slot] = part * 64 * VPC + 64 * i + lane;
@@ -347,42 +379,8 @@ __device__ __forceinline__ MxSel mx_topk_par_select(const MxTopkPar& sh, int t, 
     cid[i] = v ? sh.id[c0 + s] : 0;
     cw[i] = v ? sh.w[c0 + s] : 0.f;
   }
-  uint32_t tau = 0;
-  for (int bit = 31; bit >= 0; --bit) {
-    const uint32_t cand = tau | (1u << bit);
-    int c = 0;
-#pragma unroll
-    for (int i = 0; i < VC; ++i) c += __popcll(__builtin_amdgcn_uicmp(u[i], cand, 35));
-    if (c >= k) tau = cand;
-  }
-  const unsigned long long below = (1ull << lane) - 1ull;
-  int ngt = 0;
-#pragma unroll
-  for (int i = 0; i < VC; ++i) ngt += __popcll(__ballot(u[i] > tau));
   bool sel[VC];
-  int ties = 0;
-#pragma unroll
-  for (int i = 0; i < VC; ++i) {
-    const unsigned long long eq = __ballot(u[i] == tau);
-    sel[i] = u[i] > tau || (u[i] == tau && ties + __popcll(eq & below) < k - ngt);
-    ties += __popcll(eq);
-  }
-  // Slot = number of chosen candidates ahead (larger image, or equal and lower id).
-  int rank[VC];
-#pragma unroll
-  for (int i = 0; i < VC; ++i) rank[i] = 0;
-#pragma unroll
-  for (int iy = 0; iy < VC; ++iy) {
-    unsigned long long m = __ballot(sel[iy]);
-    while (m) {
-      const int ly = __builtin_ctzll(m);
-      m &= m - 1ull;
-      const uint32_t uy = (uint32_t)__builtin_amdgcn_readlane((int)u[iy], ly);
-      const int ey = __builtin_amdgcn_readlane(cid[iy], ly);
-#pragma unroll
-      for (int i = 0; i < VC; ++i) rank[i] += (uy > u[i] || (uy == u[i] && ey < cid[i])) ? 1 : 0;
-    }
-  }
+  mx_choose_k(u, k, sel);
   float M = 0.f, S = 1.f;
   if (mode != MX_ROUTER_SIGMOID_SELECT_BIAS) {
     M = -INFINITY;
@@ -390,21 +388,10 @@ __device__ __forceinline__ MxSel mx_topk_par_select(const MxTopkPar& sh, int t, 
     S = 0.f;
     for (int p = 0; p < NP; ++p) S += sh.sm[t * NP + p] * expf(sh.m[t * NP + p] - M);
   }
-  __shared__ int s_id[16][TK_MAXK];
-  __shared__ float s_w[16][TK_MAXK];
-  const int wv = threadIdx.x >> 6;
-#pragma unroll
-  for (int i = 0; i < VC; ++i) {
-    if (sel[i]) {
-      s_id[wv][rank[i]] = cid[i];
-      s_w[wv][rank[i]] =
-          mode == MX_ROUTER_SIGMOID_SELECT_BIAS ? cw[i] : expf(cw[i] - M) / S;
-    }
-  }
-  mx_lds_fence();
-  const int my_id = lane < k ? s_id[wv][lane] : 0;
-  const float my_w = lane < k ? s_w[wv][lane] : 0.f;
-  mx_lds_fence();  // the row is reused by this wave's next call
+  int my_id;
+  float my_w;
+  mx_slots_of(sel, u, cid, cw, k, my_id, my_w);
+  if (lane < k && mode != MX_ROUTER_SIGMOID_SELECT_BIAS) my_w = expf(my_w - M) / S;
   float sum = 0.f;  // sequential over the k slots, identical on every lane
   for (int r = 0; r < k; ++r) sum += mx_readlane(my_w, r);
   return MxSel{my_id, (norm ? my_w / (sum + 1e-20f) : my_w) * scaling};

@@ -55,6 +55,20 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x,
     const int base = e * H;
     half_t* hi = rs.whi + (size_t)e * H;
     half_t* lo = rs.wlo + (size_t)e * H;
+    if constexpr (VEC) {  // 4 consecutive elements per thread (H % 4 == 0, aligned rows)
+      const int i = c0 + 4 * threadIdx.x;
+      if (i < H) {
+        const float4 v = mx_load_param4(src, rs.pdt, base + i);
+        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+        const h4 vh = (h4){(half_t)v.x, (half_t)v.y, (half_t)v.z, (half_t)v.w};
+        *(h4*)(hi + i) = vh;
+        *(h4*)(lo + i) = (h4){(half_t)((v.x - (float)vh[0]) * 2048.f),
+                              (half_t)((v.y - (float)vh[1]) * 2048.f),
+                              (half_t)((v.z - (float)vh[2]) * 2048.f),
+                              (half_t)((v.w - (float)vh[3]) * 2048.f)};
+      }
+      return;
+    }
     float v[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -103,17 +117,19 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x,
     for (int i = 0; i < RN_V; ++i) {
       const int c = (threadIdx.x + 256 * i) * 4;
       if (c < H) {
+        const float4 nw = mx_load_param4(w, wdt, c);
         float4 o;
-        o.x = mx_load_param(w, wdt, c + 0) * (v[i].x / rms);
-        o.y = mx_load_param(w, wdt, c + 1) * (v[i].y / rms);
-        o.z = mx_load_param(w, wdt, c + 2) * (v[i].z / rms);
-        o.w = mx_load_param(w, wdt, c + 3) * (v[i].w / rms);
+        o.x = nw.x * (v[i].x / rms);
+        o.y = nw.y * (v[i].y / rms);
+        o.z = nw.z * (v[i].z / rms);
+        o.w = nw.w * (v[i].w / rms);
         if (hr) *(float4*)(hr + c) = o;
         if (rs.gate_out) {
-          gdot = fmaf(o.x, mx_load_param(rs.wsg, rs.pdt, c + 0), gdot);
-          gdot = fmaf(o.y, mx_load_param(rs.wsg, rs.pdt, c + 1), gdot);
-          gdot = fmaf(o.z, mx_load_param(rs.wsg, rs.pdt, c + 2), gdot);
-          gdot = fmaf(o.w, mx_load_param(rs.wsg, rs.pdt, c + 3), gdot);
+          const float4 g = mx_load_param4(rs.wsg, rs.pdt, c);
+          gdot = fmaf(o.x, g.x, gdot);
+          gdot = fmaf(o.y, g.y, gdot);
+          gdot = fmaf(o.z, g.z, gdot);
+          gdot = fmaf(o.w, g.w, gdot);
         }
         if (hr16) {
           typedef _Float16 h4 __attribute__((ext_vector_type(4)));
@@ -167,9 +183,14 @@ int mx_rmsnorm_launch(const float* x, const void* norm_w, int param_dtype, float
   if (!h32 && !h16) return MX_ERR_INVALID;
   const int nsplit = rsw ? rs.E * ((hidden + 1023) >> 10) : 0;
   const unsigned grid = (unsigned)tokens + (unsigned)nsplit;
+  // Vector path: 4 consecutive elements per load, for x, h and the parameters alike.
+  const uintptr_t pal = param_dtype == MX_DT_F16 ? 7u : 15u;
+  const uintptr_t sal = rsw && rs.pdt == MX_DT_F16 ? 7u : 15u;
   const bool vec = hidden % 4 == 0 && hidden <= 256 * 4 * RN_V && mx_aligned16(x) &&
                    (!h32 || mx_aligned16(h32)) && (!h16 || ((uintptr_t)h16 & 7u) == 0) &&
-                   (!h16lo || ((uintptr_t)h16lo & 7u) == 0);
+                   (!h16lo || ((uintptr_t)h16lo & 7u) == 0) && !((uintptr_t)norm_w & pal) &&
+                   (!rsw || (!((uintptr_t)rs.wr & sal) && !((uintptr_t)rs.wsg & sal) &&
+                             !((uintptr_t)rs.whi & 7u) && !((uintptr_t)rs.wlo & 7u)));
   mx_clear_error();
   if (vec)
     hipLaunchKernelGGL(k_rmsnorm<true>, dim3(grid), dim3(256), 0, s, x, norm_w, param_dtype, eps,
@@ -347,6 +368,9 @@ k_router_logits(const float* __restrict__ h32, const WT* __restrict__ wr,
 #ifndef RT_SPLIT_FILL
 #define RT_SPLIT_FILL 256  // blocks of one round of the split-plane GEMM (one per CU)
 #endif
+#ifndef RT_SPLIT_ROUTED
+#define RT_SPLIT_ROUTED 1  // split-plane slice count from the routed rows' tiles
+#endif
 static bool router_on_gemm(int tokens, int hidden, int e1, int param_dtype) {
   return param_dtype == MX_DT_F32 && tokens >= RT_GEMM_MIN_TOKENS && hidden % 16 == 0 &&
          (long)tokens * hidden * 4 < (1l << 31) && (long)e1 * hidden * 4 < (1l << 31);
@@ -367,9 +391,11 @@ int mx_router_splits_for(int tokens, int hidden, int n_experts, int has_shared_g
   long tiles, fill;
   int kch;
   if (weight_dtype >= 0 && mx_router_on_split(t, hidden, e1, weight_dtype)) {
-    // Largest slice count whose blocks fit one round at one block per CU.  Qwen3-Next,
-    // 4096 tokens: 16 x 5 tiles x 3 slices; GLM-4.7, 2048 tokens: 8 x 2 x 16.
-    tiles = (long)mx_ceil_div(t, MX_GEMM_SPLIT_BM) * mx_ceil_div(e1, 128);
+    // Largest slice count whose blocks fit one round at one block per CU.  The GEMM covers
+    // the routed rows only (the RMSNorm launch computes the shared-expert gate logit).
+    // Qwen3-Next, 4096 tokens: 16 x 4 tiles x 4 slices; GLM-4.7, 2048 tokens: 8 x 2 x 16.
+    const int cols = RT_SPLIT_ROUTED ? n_experts : e1;
+    tiles = (long)mx_ceil_div(t, MX_GEMM_SPLIT_BM) * mx_ceil_div(cols, 128);
     fill = RT_SPLIT_FILL;
     kch = hidden / 32;
   } else if (router_on_gemm(t, hidden, e1, param_dtype)) {
