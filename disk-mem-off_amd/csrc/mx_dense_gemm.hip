@@ -159,13 +159,12 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, OCC) void k_gemm_nt(
   };
   // The fragments this wave copies: f = wave + i * NW (A fragments first, then B); the
   // lane's source row and its byte offset at stage 0.
-  // Copy lane l loads row cr = l / 4 of its fragment, 16-byte chunk cq = (l % 4 - cr / 4)
-  // mod 4, so every 4 consecutive lanes read one row's 64 contiguous bytes (the address
-  // unit merges them); the chunk rotation by cr / 4 makes the MFMA operand reads below
-  // (lane (j, q) reads row j, chunk q at position 4 j + (q + j / 4) mod 4) hit 16 distinct
-  // 16-byte bank groups per 16 lanes.
-  const int cr = lane >> 2, cq = ((lane & 3) - (cr >> 2)) & 3;
-  const int rpos = (4 * j + ((q + (j >> 2)) & 3)) * 16;
+  // Copy lane l loads row cr = l / 4 of its fragment, 16-byte chunk mx_frag_copy_chunk(l),
+  // so every 4 consecutive lanes read one row's 64 contiguous bytes (the address unit
+  // merges them); the chunk rotation (mx_lds_copy.h) makes the MFMA operand reads below
+  // (lane (j, q) reads row j, chunk q at mx_frag_read_pos(j, q)) hit distinct bank groups.
+  const int cr = lane >> 2, cq = mx_frag_copy_chunk(lane);
+  const int rpos = mx_frag_read_pos(j, q);
   uint32_t goff[DPW];
 #pragma unroll
   for (int i = 0; i < DPW; ++i) {

@@ -9,6 +9,7 @@
 
 #include "mx_common.h"
 #include "mx_internal.h"
+#include "mx_lds_copy.h"
 
 namespace {
 
@@ -408,12 +409,15 @@ __global__ __launch_bounds__(256) void k_fa_pack_kv(const float* __restrict__ kk
   for (int e = 0; e < 8; ++e) vt[(size_t)(8 * c8 + e) * FA_KT] = vh[e];
 }
 
+#ifndef FA_H_WPE
+#define FA_H_WPE 2  // waves per SIMD the fp16 attention is compiled for
+#endif
 #ifndef FA_H_XCD
 #define FA_H_XCD 1  // XCD-aware head runs in k_fa_attn_h
 #endif
 
 template <int NC, int NW, int S32, int QS>
-__global__ __launch_bounds__(64 * NW) void k_fa_attn_h(const float* __restrict__ qg,
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(FA_H_WPE, FA_H_WPE))) void k_fa_attn_h(const float* __restrict__ qg,
                                                        const half_t* __restrict__ k16,
                                                        const half_t* __restrict__ v16t,
                                                        FaDims m, int T, int Tp, float sqrt_hd,
@@ -421,7 +425,7 @@ __global__ __launch_bounds__(64 * NW) void k_fa_attn_h(const float* __restrict__
   constexpr int DP = NC * 32;          // padded head dim
   constexpr int KT = 32 * S32;         // keys per tile
   constexpr int KR = DP + 8;           // K tile row stride (halfs)
-  constexpr int VR = KT + 8;           // V^T tile row stride (halfs)
+  constexpr int VR = FA_KT + 8;        // V^T row stride (halfs): one row per (32-key block, dim)
   constexpr int NT = 64 * NW;          // threads
   constexpr int KCH = KT * DP / 8;     // 16-byte pieces of a K tile (= of a V^T tile)
   constexpr int PPT = (KCH + NT - 1) / NT;  // pieces of each per thread
@@ -623,6 +627,312 @@ __global__ __launch_bounds__(64 * NW) void k_fa_attn_h(const float* __restrict__
   }
 }
 
+// ------------------------------------------------------------------------------------
+// k_fa_attn_d: the fp16 attention with the key / value tiles copied straight into LDS by
+// the buffer loads' LDS mode and two query sets (32 queries) per wave.
+// A tile is 32 keys: 2 NC key fragments (16 keys x 32 dims) and 2 NC value fragments (16
+// dims x the 32 keys in k-slot order), 1 KiB each, 32 KiB at NC = 8, double-buffered; a
+// wave's copies of tile t + 1 are issued right after the barrier that opens tile t, so
+// one tile is in flight while one computes, and no register holds a staged piece.  Every
+// fragment read from LDS feeds both query sets' MFMAs, half the LDS reads per product of
+// one set per wave.  Copy lane l loads row l / 4 of its fragment, so four consecutive
+// lanes read one row's 64 contiguous bytes, in the chunk rotation of mx_lds_copy.h under
+// which the MFMA operand reads of a fragment are free of bank conflicts.  Keys and values
+// come through buffer descriptors over the key / value head's Tp rows (rows past T are the
+// packed zeros, masked anyway).  The products, the softmax and the epilogue are those of
+// k_fa_attn_h with one 32-key block per tile.
+// ------------------------------------------------------------------------------------
+#ifndef FA_D_WPE
+#define FA_D_WPE 2  // waves per SIMD the LDS-copy attention is compiled for
+#endif
+#ifndef FA_D_NB
+#define FA_D_NB 2  // key / value tile buffers in LDS (2-4)
+#endif
+#ifndef FA_D_PD
+#define FA_D_PD 2  // LDS fragment reads in flight ahead of the MFMAs
+#endif
+#ifndef FA_D_TAU
+#define FA_D_TAU 8.f  // lazy-rescale threshold of the running max (base-2 units)
+#endif
+
+// Max over the lanes l, l ^ 16, l ^ 32 and l ^ 48 (one query's four lane groups) without
+// going through LDS: permlane16_swap exchanges 16-lane rows 2k and 2k + 1 between its two
+// operands and permlane32_swap the wave's halves, so with both operands v the two results
+// hold v of the lane and of its partner row (half).
+__device__ __forceinline__ float fa_rowmax4(float v) {
+  const unsigned b = __builtin_bit_cast(unsigned, v);
+  const auto r = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+  v = fmaxf(__builtin_bit_cast(float, r[0]), __builtin_bit_cast(float, r[1]));
+  const unsigned c = __builtin_bit_cast(unsigned, v);
+  const auto h = __builtin_amdgcn_permlane32_swap(c, c, false, false);
+  return fmaxf(__builtin_bit_cast(float, h[0]), __builtin_bit_cast(float, h[1]));
+}
+
+template <int NC, int NW, int QS>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(FA_D_WPE, FA_D_WPE)))
+void k_fa_attn_d(const float* __restrict__ qg, const half_t* __restrict__ k16,
+                 const half_t* __restrict__ v16t, FaDims m, int T, int Tp, float sqrt_hd,
+                 half_t* __restrict__ act16) {
+  constexpr int DP = NC * 32;
+  constexpr int KT = FA_KT;             // keys per tile
+  constexpr int NFK = 2 * NC;           // key fragments per tile (fragment b NC + c)
+  constexpr int NF = NFK + 2 * NC;      // then the value fragments (16-dim slabs)
+  constexpr int FPW = NF / NW;          // copies per wave and tile
+  constexpr int TILE = NF * 1024;
+  constexpr int WQ = 16 * QS;
+  static_assert(NF % NW == 0 && NFK % NW == 0, "fragments must divide among the waves");
+  constexpr int NB = FA_D_NB;           // tile buffers: NB - 1 tiles in flight
+  __shared__ __align__(1024) char lds[NB * TILE];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int QB = WQ * NW;
+  const int nqb = gridDim.x;
+  int h = blockIdx.y, qx = blockIdx.x;  // qx = 0: the longest query block (the last one)
+  if (FA_H_XCD) {  // whole heads per XCD, longest query blocks first (as k_fa_attn_h)
+    const int nb = nqb * gridDim.y, per = nb >> 3;
+    if ((nb & 7) == 0 && per % nqb == 0) {
+      const int b = blockIdx.x + nqb * blockIdx.y, hpr = per / nqb, i = b >> 3;
+      h = (b & 7) * hpr + i % hpr;
+      qx = i / hpr;
+    }
+  }
+  const int q0 = (nqb - 1 - qx) * QB;
+  const int qw0 = q0 + wave * WQ;
+  const int kvh = h / (m.nh / m.nkv);
+  const int ql = lane & 15, g = lane >> 4;
+  int qi[QS];
+#pragma unroll
+  for (int u = 0; u < QS; ++u) qi[u] = qw0 + 16 * u + ql;
+
+  const uint32_t head_bytes = (uint32_t)Tp * DP * 2;
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(k16 + (size_t)kvh * Tp * DP), (short)0, (int)head_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(v16t + (size_t)kvh * Tp * DP), (short)0, (int)head_bytes, 0x00020000);
+  const int cr = lane >> 2, cq = mx_frag_copy_chunk(lane);
+  const int rpos = mx_frag_read_pos(ql, g);
+  // Byte offsets: a lane part (row cr, chunk cq of a fragment) and a wave-uniform part.
+  const uint32_t lane_k = (uint32_t)((cr * DP + 8 * cq) * 2);
+  const uint32_t lane_v = (uint32_t)((cr * KT + 8 * cq) * 2);
+  auto issue = [&](int kt) {
+    char* buf = lds + (kt % NB) * TILE;
+    const uint32_t t0 = (uint32_t)kt * KT * DP * 2;  // both tiles are KT x DP halfs
+#pragma unroll
+    for (int i = 0; i < FPW; ++i) {
+      const int f = wave + i * NW;
+      if (i * NW < NFK)  // key fragment: keys 16 (f / NC) + row, dims 32 (f % NC) + 8 chunk
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rk, (mx_lds_void*)(buf + f * 1024), 16, lane_k,
+            (int)(t0 + (uint32_t)((16 * (f / NC) * DP + 32 * (f % NC)) * 2)), 0, 0);
+      else  // value fragment: dims 16 (f - NFK) + row of the tile's V^T block
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rv, (mx_lds_void*)(buf + f * 1024), 16, lane_v,
+            (int)(t0 + (uint32_t)(16 * (f - NFK) * KT * 2)), 0, 0);
+    }
+  };
+
+  const int kend = min(T, q0 + QB);
+  const int ntile = (kend + KT - 1) / KT;
+#pragma unroll
+  for (int t = 0; t < NB - 1; ++t)  // in flight while the queries load
+    if (t < ntile) issue(t);
+
+  // Scores in the base-2 domain: the queries are scaled by log2(e) / sqrt(head_dim) before
+  // rounding to fp16, so S = K Q^T needs no scaling.
+  const float rs = 1.4426950408889634f / sqrt_hd;
+  // Queries as fp16 MFMA B fragments, four 32-dim chunks at a time (loads at clamped in-row
+  // offsets, pad dims zeroed), so the staging registers stay few.
+  half8_t qf[QS][NC];
+#pragma unroll
+  for (int u = 0; u < QS; ++u) {
+    const float* qrow = qg + (size_t)min(qi[u], T - 1) * m.qw + (size_t)h * m.hd;
+#pragma unroll
+    for (int c0 = 0; c0 < NC; c0 += 4) {
+      float4 qv[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        qv[i] = *(const float4*)(qrow + min(32 * (c0 + (i >> 1)) + 8 * g + 4 * (i & 1), m.hd - 4));
+#pragma unroll
+      for (int c = c0; c < c0 + 4 && c < NC; ++c)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float4 v = qv[2 * (c - c0) + (e >> 2)];
+          const float x = (e & 3) == 0 ? v.x : (e & 3) == 1 ? v.y : (e & 3) == 2 ? v.z : v.w;
+          qf[u][c][e] = (half_t)(32 * c + 8 * g + e < m.hd ? x * rs : 0.f);
+        }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  float4_t oacc[QS][2 * NC];
+#pragma unroll
+  for (int u = 0; u < QS; ++u)
+#pragma unroll
+    for (int f = 0; f < 2 * NC; ++f) oacc[u][f] = (float4_t){0.f, 0.f, 0.f, 0.f};
+  float mrun[QS], lrun[QS];
+#pragma unroll
+  for (int u = 0; u < QS; ++u) mrun[u] = -INFINITY, lrun[u] = 0.f;
+  const int wq_last = min(qw0 + WQ - 1, T - 1);
+
+  // The wave computes the tiles up to its last query (nt_w of them); past those it only
+  // keeps the block's copy pipeline going (two loops, so the accumulators never merge
+  // across a skipped tile).
+  const int nt_w = min(ntile, wq_last / KT + 1);
+  // Wait for tile kt: the copies of the tiles issued after it (up to NB - 2) may stay out.
+  static_assert(NB >= 2 && NB <= 4, "2 to 4 tile buffers");
+  auto wait_tile = [&](int kt) {
+    const int later = min(NB - 2, ntile - 1 - kt);  // tiles issued after kt
+    if (NB == 4 && later == 2) mx_wait_copies_and_barrier<(NB == 4 ? 2 * FPW : 0)>();
+    else if (NB >= 3 && later == 1) mx_wait_copies_and_barrier<(NB >= 3 ? FPW : 0)>();
+    else mx_wait_copies_and_barrier<0>();
+  };
+  for (int kt = 0; kt < nt_w; ++kt) {
+    // This wave's copies of tile kt have landed (those of the later tiles in flight may
+    // not have), then everyone's have, and every wave is done with tile kt - 1, whose
+    // buffer the copies of tile kt + NB - 1 overwrite.
+    wait_tile(kt);
+    if (kt + NB - 1 < ntile) issue(kt + NB - 1);
+    const int k0 = kt * KT;
+    const bool need_mask = k0 + KT - 1 > qw0 || k0 + KT > T;
+    const char* buf = lds + (kt % NB) * TILE;
+    // Fragments are read FA_D_PD steps ahead of the MFMAs that use them; the scheduling
+    // barriers keep the compiler from hoisting every read of the tile (which would need far
+    // more registers than two waves per SIMD leave).
+    auto frag = [&](int f) { return *(const half8_t*)(buf + f * 1024 + rpos); };
+    // S^T in 4 independent accumulator chains per wave: (query set, key half b) and, with
+    // one query set, the parity of the 32-dim chunk as well; the fragments are taken
+    // chunk-major (c, b), so consecutive MFMAs never wait on each other's results.
+    constexpr int PAR = QS == 1 ? 2 : 1;
+    float4_t sc[QS][2][PAR];
+#pragma unroll
+    for (int u = 0; u < QS; ++u)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int p = 0; p < PAR; ++p) sc[u][b][p] = (float4_t){0.f, 0.f, 0.f, 0.f};
+    auto kidx = [](int i) { return (i & 1) * NC + (i >> 1); };  // step i -> key fragment b NC + c
+    // Fragment ring: step i (key steps, then the value fragments) uses fr[i % PD] and
+    // refills it with step i + PD's fragment.
+    constexpr int PD = FA_D_PD;
+    auto fidx = [&](int i) { return i < NFK ? kidx(i) : i; };
+    half8_t fr[PD];
+#pragma unroll
+    for (int i = 0; i < PD; ++i) fr[i] = frag(fidx(i));
+#pragma unroll
+    for (int i = 0; i < NFK; ++i) {
+      const int b = i & 1, c = i >> 1;
+      const half8_t kf = fr[i % PD];
+      fr[i % PD] = frag(fidx(i + PD));  // past the keys: the first value fragments
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < QS; ++u)
+        sc[u][b][c % PAR] =
+            __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[u][c], sc[u][b][c % PAR], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (PAR == 2) {
+#pragma unroll
+      for (int u = 0; u < QS; ++u)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) sc[u][b][0] += sc[u][b][1];
+    }
+    half8_t pf[QS];
+#pragma unroll
+    for (int u = 0; u < QS; ++u) {
+      if (need_mask) {  // tiles on the diagonal or past T
+        const int lim = min(qi[u], T - 1) - (k0 + 4 * g);  // last key of the query, tile-relative
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (16 * b + r > lim) sc[u][b][0][r] = -INFINITY;
+      }
+      float mt = fmaxf(fmaxf(fmaxf(sc[u][0][0][0], sc[u][0][0][1]),
+                             fmaxf(sc[u][0][0][2], sc[u][0][0][3])),
+                       fmaxf(fmaxf(sc[u][1][0][0], sc[u][1][0][1]),
+                             fmaxf(sc[u][1][0][2], sc[u][1][0][3])));
+      mt = fa_rowmax4(mt);
+      // Lazy rescale: a query's reference max moves only when the tile's max passes it by
+      // more than FA_D_TAU (base-2 units), so the probabilities stay below 2^FA_D_TAU (fp16
+      // holds them) and the accumulators are rescaled on few tiles.  Tile 0 holds key 0,
+      // which every query sees, so the reference is finite from tile 0 on.
+      const bool up = mt > mrun[u] + FA_D_TAU;
+      if (__builtin_amdgcn_ballot_w64(up)) {
+        const float mnew = up ? mt : mrun[u];
+        const float alpha = __builtin_amdgcn_exp2f(mrun[u] - mnew);  // 1 where it stays
+        lrun[u] *= alpha;
+        mrun[u] = mnew;
+#pragma unroll
+        for (int f = 0; f < 2 * NC; ++f) oacc[u][f] *= alpha;
+      }
+      float ps = 0.f;
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float pv2 = __builtin_amdgcn_exp2f(sc[u][b][0][r] - mrun[u]);
+          ps += pv2;
+          pf[u][4 * b + r] = (half_t)pv2;
+        }
+      lrun[u] += ps;
+    }
+#pragma unroll
+    for (int i = NFK; i < NF; ++i) {  // value fragment i: dims 16 (i - NFK) ..
+      const half8_t vf = fr[i % PD];
+      if (i + PD < NF) fr[i % PD] = frag(i + PD);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < QS; ++u)
+        oacc[u][i - NFK] =
+            __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[u], oacc[u][i - NFK], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  for (int kt = nt_w; kt < ntile; ++kt) {
+    wait_tile(kt);
+    if (kt + NB - 1 < ntile) issue(kt + NB - 1);
+  }
+#pragma unroll
+  for (int u = 0; u < QS; ++u) {
+    float l = lrun[u] + __shfl_xor(lrun[u], 16);
+    l = l + __shfl_xor(l, 32);
+    if (qi[u] >= T) continue;
+    const float* gate = qg + (size_t)qi[u] * m.qw + (size_t)m.od + (size_t)h * m.hd;
+    const size_t orow = (size_t)qi[u] * m.od + (size_t)h * m.hd;
+    const float il = 1.f / l;
+#pragma unroll
+    for (int f0 = 0; f0 < 2 * NC; f0 += 4) {  // four 16-dim slabs at a time
+      float4 gv[4];
+#pragma unroll
+      for (int f = 0; f < 4; ++f)
+        gv[f] = *(const float4*)(gate + min(16 * (f0 + f) + 4 * g, m.hd - 4));
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        const int d = 16 * (f0 + f) + 4 * g;
+        if (f0 + f >= 2 * NC || d >= m.hd) continue;
+        typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+        const float4_t a = oacc[u][f0 + f];
+        const half4_t o = {(half_t)(a[0] * il * mx_sigmoid(gv[f].x)),
+                           (half_t)(a[1] * il * mx_sigmoid(gv[f].y)),
+                           (half_t)(a[2] * il * mx_sigmoid(gv[f].z)),
+                           (half_t)(a[3] * il * mx_sigmoid(gv[f].w))};
+        *(half4_t*)(act16 + orow + d) = o;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+}
+
+#ifndef FA_DMA
+#define FA_DMA 1  // LDS-copy attention (k_fa_attn_d) for head dims of 128 and 256
+#endif
+#ifndef FA_D_NW
+#define FA_D_NW 4
+#endif
+#ifndef FA_D_QS
+#define FA_D_QS 2
+#endif
+
 #ifndef FA_H_NW
 #define FA_H_NW 8  // waves per block of the fp16 attention
 #endif
@@ -643,8 +953,14 @@ int launch_attn_h(const float* qg, const float* kk, const float* vv, const FaDim
   hipLaunchKernelGGL(k_fa_pack_kv, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, s, kk,
                      vv, m, T, Tp, DP, k16, v16t);
   MX_TRY(mx_launch_status());
-  const dim3 grid(mx_ceil_div(T, 16 * FA_H_QS * FA_H_NW), m.nh);
   const float sqrt_hd = (float)sqrt((double)m.hd);
+  if constexpr (FA_DMA && NC >= 4) {
+    const dim3 grid(mx_ceil_div(T, 16 * FA_D_QS * FA_D_NW), m.nh);
+    hipLaunchKernelGGL((k_fa_attn_d<NC, FA_D_NW, FA_D_QS>), grid, dim3(64 * FA_D_NW), 0, s, qg,
+                       k16, v16t, m, T, Tp, sqrt_hd, (half_t*)act);
+    return mx_launch_status();
+  }
+  const dim3 grid(mx_ceil_div(T, 16 * FA_H_QS * FA_H_NW), m.nh);
   hipLaunchKernelGGL((k_fa_attn_h<NC, FA_H_NW, FA_H_S32, FA_H_QS>), grid, dim3(64 * FA_H_NW), 0, s, qg,
                      k16, v16t, m, T, Tp, sqrt_hd, (half_t*)act);
   return mx_launch_status();

@@ -24,3 +24,17 @@ __device__ __forceinline__ void mx_wait_copies_and_barrier() {
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
+
+// Chunk rotation of the 1 KiB operand fragments (16 rows x 64 bytes) that the LDS copies
+// fill and the MFMA operand reads consume: row j's 16-byte chunk c sits at slot
+// 4 j + (c + mx_frag_rot(j)) mod 4.  The rotation keeps the four chunks of a row in its own
+// 64 bytes (so four consecutive copy lanes still read one row's 64 contiguous bytes) and
+// makes the reads of lanes (j, c), j = 0..15, fall in distinct 16-byte bank groups both
+// for 8 lanes per 128-byte LDS cycle (slots distinct mod 8 within j = 0..7 and 8..15) and
+// for 16 lanes per 256-byte cycle (slots distinct mod 16).
+__device__ __forceinline__ int mx_frag_rot(int j) { return ((j >> 2) + ((j >> 1) & 1) * 2) & 3; }
+// Copy lane l's chunk (it loads row l / 4) and the byte offset of lane (j, c)'s operand.
+__device__ __forceinline__ int mx_frag_copy_chunk(int l) { return ((l & 3) - mx_frag_rot(l >> 2)) & 3; }
+__device__ __forceinline__ int mx_frag_read_pos(int j, int c) {
+  return (4 * j + ((c + mx_frag_rot(j)) & 3)) * 16;
+}
