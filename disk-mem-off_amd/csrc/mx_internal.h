@@ -176,8 +176,9 @@ static inline bool mx_dense_on_gemm(int wdt, int T, int K) {
 int mx_project(const MxDenseWork& w, int ent, int wdt, const void* wmat, int T, int N, int K,
                const void* a, float* y, hipStream_t s);
 // Chunked gated recurrence on fp32 MFMA (mx_la_chunk.hip) for key / value heads of 64 or
-// 128, with a coefficient buffer of mx_la_chunk_coef_bytes (0: shape not supported);
+// 128, with a 16-byte aligned workspace of mx_la_chunk_ws_bytes (0: shape not supported;
+// per-chunk decay coefficients and the state every chunk after the first starts from);
 // MX_ERR_UNSUPPORTED for other shapes (the caller then runs the token-sequential scan).
-size_t mx_la_chunk_coef_bytes(int T, int n, int dk, int dv);
+size_t mx_la_chunk_ws_bytes(int T, int n, int dk, int dv);
 int mx_la_chunked_scan(const float* q, const float* kb, const float* v, const float* decay,
-                       int T, int n, int dk, int dv, float* o, void* coef, hipStream_t s);
+                       int T, int n, int dk, int dv, float* o, void* ws, hipStream_t s);

@@ -3,16 +3,21 @@
 //   S_t = d_t S_{t-1} + v_t kb_t^T,   o_t = S_t q_t,   S_0 = 0     (per head, d_t = exp(g_t))
 // on fp32 MFMA (v_mfma_f32_16x16x4_f32, full fp32 products and sums).
 //
-// Over a chunk of C = 64 tokens starting at t0, with S_p the state before the chunk and
-// a(t, s) = d_{s+1} ... d_t the decay between tokens s <= t (a(t, t) = 1):
-//   o_t = sum_{t0 <= s <= t} a(t, s) (kb_s . q_t) v_s  +  a(t, t0 - 1) S_p q_t
-//   S_end = a(end, t0 - 1) S_p + sum_s a(end, s) v_s kb_s^T
-// which is the recurrence unrolled over the chunk (exact in real arithmetic).  The first
-// sum (intra-chunk) needs no state: k_la_chunk_intra computes it for every (head, chunk)
-// in parallel as (Q Kb^T masked and scaled by a) V, writes it to o, and writes the chunk's
-// decay coefficients to a small buffer.  The second part walks the chunks of a head in
-// order: k_la_chunk_state holds 16 state rows of one head in MFMA accumulators, adds
-// a(t, t0 - 1) S_p q_t to o and updates S, one chunk at a time.
+// Over a chunk c of C = 64 tokens starting at t0, with S_{c-1} the state before the chunk
+// and a(t, s) = d_{s+1} ... d_t the decay between tokens s <= t (a(t, t) = 1):
+//   o_t = sum_{t0 <= s <= t} a(t, s) (kb_s . q_t) v_s  +  a(t, t0 - 1) S_{c-1} q_t
+//   S_c = a(end, t0 - 1) S_{c-1} + sum_s a(end, s) v_s kb_s^T
+// which is the recurrence unrolled over the chunk (exact in real arithmetic).  Three
+// launches:
+//   k_la_chunk_coef    one wave per (head, chunk): the chunk's coefficients a(end, s) and
+//                      a(end, t0 - 1) for the state walk;
+//   k_la_chunk_states  walks the chunks of a head in order, the state in MFMA accumulators
+//                      (a block per 32 value rows x 64 key columns of a head), adding only
+//                      the increments sum_s a(end, s) v_s kb_s^T, and stores every state a
+//                      later chunk starts from (S_0 .. S_{nc-2}, fp32);
+//   k_la_chunk_out     a block per (chunk, head), all in parallel: the intra-chunk sum as
+//                      (Q Kb^T masked and scaled by a) V plus a(t, t0 - 1) S_{c-1} q_t.
+// The walk carries no q, o or output product, so its chain per chunk is the increment alone.
 //
 // The decay factors are formed in double precision from the fp32 decays the reference
 // multiplies by: with G_t = sum over the chunk of log(d_r) up to t, a(t, s) =
@@ -21,12 +26,19 @@
 // zero is taken and no difference of huge sums is formed.
 #include <math.h>
 
+#include <utility>
+
 #include "mx_common.h"
 #include "mx_internal.h"
+#include "mx_lds_copy.h"
 
 namespace {
 
 constexpr int kC = 64;  // tokens per chunk
+
+#ifndef MX_OOB
+#define MX_OOB 0x80000000u  // an offset outside every buffer descriptor built here
+#endif
 
 typedef __amdgpu_buffer_rsrc_t mx_rsrc_t;
 
@@ -37,6 +49,16 @@ __device__ __forceinline__ mx_rsrc_t mx_rsrc(const void* base, uint32_t bytes) {
 
 __device__ __forceinline__ int4_t mx_ld16(mx_rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+
+// f(integral_constant<int, i>) for i = 0 .. N - 1, unrolled at compile time.
+template <typename F, int... Is>
+__device__ __forceinline__ void mx_static_for_seq(F&& f, std::integer_sequence<int, Is...>) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void mx_static_for(F&& f) {
+  mx_static_for_seq(f, std::make_integer_sequence<int, N>{});
 }
 
 __device__ __forceinline__ float4_t mfma4(float a, float b, float4_t c) {
@@ -67,8 +89,8 @@ __device__ __forceinline__ double shfl_d(double v, int src) {
 // One wave, lane l = token t0 + l of the chunk: G_l (log decay from the segment start up to
 // and including l) and the last zero-decay token at or before l (-1: none in the chunk).
 // Tokens past T take d = 1.
-__device__ __forceinline__ void chunk_log_decay(const float* __restrict__ decay, int t0, int T,
-                                                int n, int h, double* sG, int* sLR) {
+__device__ __forceinline__ void chunk_log_decay_reg(const float* __restrict__ decay, int t0,
+                                                    int T, int n, int h, double& G, int& LR) {
   const int l = threadIdx.x & 63;
   const int t = t0 + l;
   const float d = t < T ? decay[(size_t)t * n + h] : 1.f;
@@ -85,13 +107,22 @@ __device__ __forceinline__ void chunk_log_decay(const float* __restrict__ decay,
     }
   }
   const double pr = shfl_d(p, lr >= 0 ? lr : 0);
-  sG[l] = lr >= 0 ? p - pr : p;
-  sLR[l] = lr;
+  G = lr >= 0 ? p - pr : p;
+  LR = lr;
 }
 
-// Coefficients the state walk reads per (head, chunk): a(t, t0 - 1) for the 64 tokens, then
-// a(end, s) for the 64 tokens, then a(end, t0 - 1) (padded to 132 floats).
-constexpr int kCoef = 132;
+__device__ __forceinline__ void chunk_log_decay(const float* __restrict__ decay, int t0, int T,
+                                                int n, int h, double* sG, int* sLR) {
+  double G;
+  int LR;
+  chunk_log_decay_reg(decay, t0, T, n, h, G, LR);
+  sG[threadIdx.x & 63] = G;
+  sLR[threadIdx.x & 63] = LR;
+}
+
+// Coefficient record of a (head, chunk), 1 KiB so that one 64-lane LDS copy moves it:
+// a(end, s) for the 64 tokens, then a(end, t0 - 1); the rest is padding.
+constexpr int kCoef = 256;
 
 // LDS row strides in floats: (stride / 4) odd, so the 16-byte reads of 16 consecutive rows
 // at one column group hit distinct bank groups.
@@ -100,22 +131,245 @@ struct Pad {
   static constexpr int S = W + 4;
 };
 
-// ---- intra-chunk part: o[t] = sum_{t0 <= s <= t} a(t, s) (kb_s . q_t) v_s ---------------
-// Block (chunk, head), 4 waves; wave w takes tokens 16 w .. 16 w + 15 of the chunk.  Its q
-// rows go straight into MFMA A registers; kb (B of the scores, all 64 tokens) and v (B of
-// the products with v) are shared through LDS (row-major, 16-byte stores), and the kb
-// region is then reused for each wave's masked scores (A of the products with v).  Wave 0
-// also writes the chunk's coefficients for the state walk.
+// ---- coefficients: one wave per (head, chunk) ---------------------------------------
+__global__ __launch_bounds__(256) void k_la_chunk_coef(const float* __restrict__ decay, int T,
+                                                       int n, int nchunk,
+                                                       float* __restrict__ coef) {
+  const int item = blockIdx.x * 4 + (threadIdx.x >> 6);  // h * nchunk + chunk
+  if (item >= n * nchunk) return;                        // whole waves
+  const int h = item / nchunk, chunk = item % nchunk, t0 = chunk * kC;
+  const int l = threadIdx.x & 63;
+  double G;
+  int LR;
+  chunk_log_decay_reg(decay, t0, T, n, h, G, LR);
+  const int lastv = min(kC, T - t0) - 1;
+  const double ge = shfl_d(G, lastv);
+  const int lre = __shfl(LR, lastv, 64);
+  float* cf = coef + (size_t)item * kCoef;
+  cf[l] = (l <= lastv && lre <= l) ? expf((float)(ge - G)) : 0.f;
+  if (l == 0) cf[kC] = lre < 0 ? expf((float)ge) : 0.f;
+}
+
+// ---- state walk: S_c = a(end, t0 - 1) S_{c-1} + sum_s a(end, s) v_s kb_s^T ------------
+// Block = 32 value rows (i0 ..) x 64 key columns (c0 ..) of one head's state, 4 waves; wave w
+// holds the transposed tiles S^T[c0 + 16 w + ..][i0 + 16 rt + ..], rt = 0, 1, in MFMA
+// accumulators: lane (j, qq) of tile rt holds S[i0 + 16 rt + j][c0 + 16 w + 4 qq + r],
+// r = 0..3, which it stores as one 16-byte piece.  The increment of a chunk is
+// U^T = Kb^T (a(end) V): token s = 16 kg + 4 qq + e enters as k-slot qq of MFMA (kg, e), A =
+// kb[s][c0 + 16 w + j], B = v[s][i0 + 16 rt + j] a(end, s).
+//
+// Operands come through an LDS ring of LA_NB chunk slots filled by the buffer loads' LDS
+// mode (no register holds a staged piece): per chunk the kb tile (64 tokens x 64 columns,
+// 16 KiB), the v tile (64 tokens x 32 rows, 8 KiB) and the coefficient record (1 KiB, one
+// copy per wave), 7 copies per wave, issued LA_NB - 1 chunks ahead.  Copy lane l of a kb copy
+// loads a 16-byte piece of token row r = l / 16 (of its 4 rows), placed at piece position
+// (p + 4 ((r / 4) % 4)) % 16 of the 16 in the row; a v copy holds 8 token rows of 8 pieces,
+// row R of the copy holding token R ^ ((R / 8) % 2) at piece position (p + 4 ((s / 4) % 2)) % 8.
+// With these rotations the 64 lanes of every operand read hit 64 distinct 4-byte banks.
+// Copies past the last chunk, and rows past T, use out-of-range offsets (they return zeros
+// and move no data), so every wave issues the same number of vector memory operations per
+// chunk and one constant wait count per iteration finds the chunk's copies complete.
+#ifndef LA_NB
+#define LA_NB 4  // chunk slots of the state walk's LDS ring
+#endif
+
 template <int DK, int DV>
-__global__ __launch_bounds__(256, 2) void k_la_chunk_intra(const float* __restrict__ q,
-                                                           const float* __restrict__ kb,
-                                                           const float* __restrict__ v,
-                                                           const float* __restrict__ decay,
-                                                           int T, int n, int nchunk,
-                                                           float* __restrict__ o,
-                                                           float* __restrict__ coef) {
+__global__ __launch_bounds__(256) void k_la_chunk_states(const float* __restrict__ kb,
+                                                         const float* __restrict__ v,
+                                                         const float* __restrict__ coef,
+                                                         int T, int n, int nchunk,
+                                                         float* __restrict__ S) {
+  constexpr int NB = LA_NB;
+  static_assert(NB >= 2 && NB <= 5, "ring depth");
+  constexpr int RBK = DV / 32;          // 32-row blocks per head
+  constexpr int BPH = RBK * (DK / 64);  // blocks per head
+  constexpr int KB_BYTES = kC * 64 * 4;
+  constexpr int V_BYTES = kC * 32 * 4;
+  constexpr int SLOT = KB_BYTES + V_BYTES + 4 * 1024;
+  constexpr int P = 7;                  // copies per wave and chunk
+  constexpr int ST = 2;                 // state stores per wave and chunk
+  // One LDS variable per slot, every access naming its slot at compile time: the compiler
+  // then tells a slot's reads from the copies in flight into the other slots (with a single
+  // array it waits for every copy before any read).
+  __shared__ __align__(1024) char lds0[SLOT];
+  __shared__ __align__(1024) char lds1[SLOT];
+  __shared__ __align__(1024) char lds2[NB > 2 ? SLOT : 16];
+  __shared__ __align__(1024) char lds3[NB > 3 ? SLOT : 16];
+  __shared__ __align__(1024) char lds4[NB > 4 ? SLOT : 16];
+  auto slot_of = [&](auto I) -> char* {
+    constexpr int i = decltype(I)::value % NB;
+    if constexpr (i == 0) return lds0;
+    else if constexpr (i == 1) return lds1;
+    else if constexpr (i == 2) return lds2;
+    else if constexpr (i == 3) return lds3;
+    else return lds4;
+  };
+
+  // The blocks of a head share kb columns and v rows: they run on one XCD (hardware block b
+  // runs on XCD b % 8), so a chunk's rows come from that XCD's L2 after the first read.
+  int h, sub;
+  if ((n & 7) == 0) {
+    const int k = blockIdx.x >> 3;
+    h = (blockIdx.x & 7) * (n >> 3) + k / BPH;
+    sub = k % BPH;
+  } else {
+    h = blockIdx.x / BPH;
+    sub = blockIdx.x % BPH;
+  }
+  const int i0 = 32 * (sub % RBK), c0 = 64 * (sub / RBK);
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, qq = lane >> 4;
+  const uint32_t qrow = (uint32_t)n * DK * 4, vrow = (uint32_t)n * DV * 4;
+  const mx_rsrc_t rk = mx_rsrc(kb, (uint32_t)T * qrow);
+  const mx_rsrc_t rv = mx_rsrc(v, (uint32_t)T * vrow);
+  const mx_rsrc_t rc = mx_rsrc(coef, (uint32_t)n * nchunk * kCoef * 4);
+  constexpr uint32_t SB = (uint32_t)DV * DK * 4;  // bytes per stored state
+  const mx_rsrc_t rs = mx_rsrc(S + (size_t)h * (nchunk - 1) * DV * DK, (uint32_t)(nchunk - 1) * SB);
+
+  // copy offsets of this lane (chunk 0)
+  uint32_t k_off[4], v_off[2];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int r = 4 * (4 * w + m) + (lane >> 4);
+    const int p = ((lane & 15) - 4 * ((r >> 2) & 3)) & 15;
+    k_off[m] = (uint32_t)r * qrow + (uint32_t)(h * DK + c0 + 4 * p) * 4;
+  }
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    const int R = 8 * (2 * w + m) + (lane >> 3);
+    const int s = R ^ ((R >> 3) & 1);
+    const int p = ((lane & 7) - 4 * ((s >> 2) & 1)) & 7;
+    v_off[m] = (uint32_t)s * vrow + (uint32_t)(h * DV + i0 + 4 * p) * 4;
+  }
+  const uint32_t c_off = (uint32_t)h * nchunk * kCoef * 4 + 16 * lane;
+  auto copies = [&](char* slot, int ch) {
+    const uint32_t oob = ch < nchunk ? 0u : MX_OOB;
+    const uint32_t kbase = (uint32_t)ch * kC * qrow, vbase = (uint32_t)ch * kC * vrow;
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+      mx_copy_to_lds16(rk, slot + 1024 * (4 * w + m), (kbase + k_off[m]) | oob);
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+      mx_copy_to_lds16(rv, slot + KB_BYTES + 1024 * (2 * w + m), (vbase + v_off[m]) | oob);
+    mx_copy_to_lds16(rc, slot + KB_BYTES + V_BYTES + 1024 * w,
+                     (c_off + (uint32_t)ch * kCoef * 4) | oob);
+  };
+
+  // operand read offsets (floats) of this lane: kb[s][c0 + 16 w + j] at kq + (16 kg + e) 64;
+  // v[s][i0 + 16 rt + j] at (e odd ? vo : ve)[rt] + (16 kg + e) 32
+  const int kq = 4 * qq * 64 + 4 * ((4 * w + (j >> 2) + 4 * qq) & 15) + (j & 3);
+  const int x = qq >> 1;
+  int ve[2], vo[2];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    const int b = 4 * qq * 32 + 4 * ((4 * rt + (j >> 2) + 4 * (qq & 1)) & 7) + (j & 3);
+    ve[rt] = b + 32 * x;
+    vo[rt] = b - 32 * x;
+  }
+  // this lane's stored piece of tile rt (bytes, state 0)
+  uint32_t s_off[2];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+    s_off[rt] = (uint32_t)((i0 + 16 * rt + j) * DK + c0 + 16 * w + 4 * qq) * 4;
+
+  float4_t st[2];
+  st[0] = st[1] = (float4_t){0.f, 0.f, 0.f, 0.f};
+
+  auto step = [&](const char* slot, int ch) {
+    const float* K = (const float*)slot;
+    const float* V = (const float*)(slot + KB_BYTES);
+    const float* CF = (const float*)(slot + KB_BYTES + V_BYTES + 1024 * w);
+    float a[4][4], b[2][4][4];
+#pragma unroll
+    for (int kg = 0; kg < 4; ++kg) {
+      const float4 ws = *(const float4*)(CF + 16 * kg + 4 * qq);
+      const float wv[4] = {ws.x, ws.y, ws.z, ws.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        a[kg][e] = K[kq + (16 * kg + e) * 64];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+          b[rt][kg][e] = V[((e & 1) ? vo[rt] : ve[rt]) + (16 * kg + e) * 32] * wv[e];
+      }
+    }
+    // four independent chains: tiles rt x token halves kh
+    float4_t acc[2][2];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) acc[rt][0] = acc[rt][1] = (float4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+          for (int rt = 0; rt < 2; ++rt)
+            acc[rt][kh] = mfma4(a[2 * kh + kk][e], b[rt][2 * kh + kk][e], acc[rt][kh]);
+    const float gam = CF[kC];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) st[rt] = st[rt] * gam + acc[rt][0] + acc[rt][1];
+    // S_ch, the state chunk ch + 1 starts from (the last chunk's store is out of range)
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(int4_t, st[rt]), rs,
+                                             (uint32_t)ch * SB + s_off[rt], 0, 0);
+  };
+
+  // LDS starts zeroed: a row a copy does not fill holds finite values (a(end, s) = 0 there)
+  for (int i = threadIdx.x; i < SLOT / 16; i += 256) {
+    const int4_t z = {0, 0, 0, 0};
+    *(int4_t*)(lds0 + 16 * i) = z;
+    *(int4_t*)(lds1 + 16 * i) = z;
+    if constexpr (NB > 2) *(int4_t*)(lds2 + 16 * i) = z;
+    if constexpr (NB > 3) *(int4_t*)(lds3 + 16 * i) = z;
+    if constexpr (NB > 4) *(int4_t*)(lds4 + 16 * i) = z;
+  }
+  __syncthreads();
+  mx_static_for<NB - 1>([&](auto I) { copies(slot_of(I), decltype(I)::value); });
+  // Iteration c (slot c % NB): wait for chunk c's copies (after them this wave issued the
+  // later prologue copies and, per earlier iteration, P copies and ST stores), meet the
+  // other waves, issue the copies of chunk c + NB - 1 into the slot chunk c - 1 used,
+  // compute chunk c.  The walk runs whole groups of NB chunks, unrolled and branch-free so
+  // that every slot is named statically; chunks past the last one compute on out-of-range
+  // copies and store out of range.  The first group is peeled for its wait counts.
+  mx_static_for<NB>([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    mx_wait_copies_and_barrier<(NB - 2) * P + (i < NB - 1 ? i : NB - 1) * ST>();
+    copies(slot_of(std::integral_constant<int, i + NB - 1>{}), i + NB - 1);
+    step(slot_of(I), i);
+  });
+  for (int c0 = NB; c0 < nchunk; c0 += NB) {
+    mx_static_for<NB>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      mx_wait_copies_and_barrier<(NB - 2) * P + (NB - 1) * ST>();
+      copies(slot_of(std::integral_constant<int, i + NB - 1>{}), c0 + i + NB - 1);
+      step(slot_of(I), c0 + i);
+    });
+  }
+  // no copy into LDS may still be in flight when the block ends
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+}
+
+// ---- output: o[t] = sum_{t0 <= s <= t} a(t, s) (kb_s . q_t) v_s + a(t, t0 - 1) S_{c-1} q_t
+// Block (chunk, head), 4 waves; wave w takes tokens 16 w .. 16 w + 15 of the chunk.  Its q
+// rows go straight into MFMA A registers and serve both products with q.  The inter-chunk
+// part comes first: B = S_{c-1}[16 nt + j][16 u + 4 qq ..] read straight from the stored
+// states (one value tile ahead), scaled by a(t, t0 - 1) once summed.  kb (B of the scores,
+// all 64 tokens) and v (B of the products with v) are shared through LDS (row-major, 16-byte
+// stores; their loads are issued first and land during the inter-chunk products), and the
+// kb region is then reused for each wave's masked scores (A of the products with v).
+template <int DK, int DV>
+__global__ __launch_bounds__(256, 2) void k_la_chunk_out(const float* __restrict__ q,
+                                                         const float* __restrict__ kb,
+                                                         const float* __restrict__ v,
+                                                         const float* __restrict__ decay,
+                                                         const float* __restrict__ S, int T,
+                                                         int n, int nchunk,
+                                                         float* __restrict__ o) {
   constexpr int SK = Pad<DK>::S, SC = Pad<kC>::S, SV = Pad<DV>::S;
   constexpr int KP = kC * DK / 4 / 256, VP = kC * DV / 4 / 256;  // float4 pieces per thread
+  constexpr int NU = DK / 16, NV = DV / 16;
   static_assert(4 * 16 * SC <= kC * SK, "masked scores reuse the kb tile");
   __shared__ __align__(16) float sK[kC * SK];    // kb tile, then the masked scores
   __shared__ __align__(16) float sV[kC * SV];    // v tile [token][value row]
@@ -129,10 +383,10 @@ __global__ __launch_bounds__(256, 2) void k_la_chunk_intra(const float* __restri
   const int qd = n * DK, vd = n * DV;
 
   // every global load of the block first, then the LDS stores
-  float4 qa[DK / 16];
+  float4 qa[NU];
   const int tq = t0 + 16 * w + j;
 #pragma unroll
-  for (int u = 0; u < DK / 16; ++u)
+  for (int u = 0; u < NU; ++u)
     qa[u] = tq < T ? *(const float4*)(q + (size_t)tq * qd + h * DK + 16 * u + 4 * qq)
                    : make_float4(0.f, 0.f, 0.f, 0.f);
   float4 kr[KP], vr[VP];
@@ -149,6 +403,31 @@ __global__ __launch_bounds__(256, 2) void k_la_chunk_intra(const float* __restri
                   : make_float4(0.f, 0.f, 0.f, 0.f);
   }
   if (w == 0) chunk_log_decay(decay, t0, T, n, h, sG, sLR);
+
+  float4_t oacc[NV];
+#pragma unroll
+  for (int nt = 0; nt < NV; ++nt) oacc[nt] = (float4_t){0.f, 0.f, 0.f, 0.f};
+  if (chunk > 0) {
+    // (Q S^T)[16 w + 4 qq + r][16 nt + j]; the state the chunk starts from is S_{chunk-1}
+    const mx_rsrc_t rs = mx_rsrc(S + ((size_t)h * (nchunk - 1) + chunk - 1) * DV * DK,
+                                 (uint32_t)DV * DK * 4);
+    const uint32_t s_lane = (uint32_t)(j * DK + 4 * qq) * 4;
+    int4_t sb[2][NU];
+#pragma unroll
+    for (int u = 0; u < NU; ++u) sb[0][u] = mx_ld16(rs, s_lane + 64u * u);
+#pragma unroll
+    for (int nt = 0; nt < NV; ++nt) {
+      if (nt + 1 < NV) {
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
+          sb[(nt + 1) & 1][u] = mx_ld16(rs, s_lane + (uint32_t)(16 * (nt + 1) * DK) * 4 + 64u * u);
+      }
+#pragma unroll
+      for (int u = 0; u < NU; ++u)
+        oacc[nt] = mfma_k16(qa[u], __builtin_bit_cast(float4, sb[nt & 1][u]), oacc[nt]);
+    }
+  }
+
 #pragma unroll
   for (int p = 0; p < KP; ++p) {
     const int i = tid + 256 * p, r = i / (DK / 4), c = 4 * (i % (DK / 4));
@@ -161,12 +440,22 @@ __global__ __launch_bounds__(256, 2) void k_la_chunk_intra(const float* __restri
   }
   __syncthreads();
 
+  if (chunk > 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int tl = 16 * w + 4 * qq + r;
+      const float at = sLR[tl] < 0 ? expf((float)sG[tl]) : 0.f;
+#pragma unroll
+      for (int nt = 0; nt < NV; ++nt) oacc[nt][r] *= at;
+    }
+  }
+
   // scores of this wave's 16 tokens against the chunk's 64: P = Q Kb^T
   float4_t pacc[4];
 #pragma unroll
   for (int nt = 0; nt < 4; ++nt) pacc[nt] = (float4_t){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int u = 0; u < DK / 16; ++u) {
+  for (int u = 0; u < NU; ++u) {
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
       const float4 b = *(const float4*)(sK + (16 * nt + j) * SK + 16 * u + 4 * qq);
@@ -188,12 +477,8 @@ __global__ __launch_bounds__(256, 2) void k_la_chunk_intra(const float* __restri
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 
-  // o = P V over the chunk's 64 tokens; token s = k0 + 4 qq + e of v row 16 nt + j (four
+  // o += P V over the chunk's 64 tokens; token s = k0 + 4 qq + e of v row 16 nt + j (four
   // rows per lane, one value each: lane groups qq sit 16 banks apart)
-  constexpr int NV = DV / 16;
-  float4_t oacc[NV];
-#pragma unroll
-  for (int nt = 0; nt < NV; ++nt) oacc[nt] = (float4_t){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int k0 = 0; k0 < kC; k0 += 16) {
     const float4 a = *(const float4*)(myP + j * SC + k0 + 4 * qq);
@@ -212,249 +497,33 @@ __global__ __launch_bounds__(256, 2) void k_la_chunk_intra(const float* __restri
       for (int nt = 0; nt < NV; ++nt) o[(size_t)t * vd + h * DV + 16 * nt + j] = oacc[nt][r];
     }
   }
-  if (w == 0) {
-    // coefficients of the state walk, lane l = token l of the chunk
-    const int l = lane;
-    const int lastv = min(kC, T - t0) - 1;
-    const double ge = sG[lastv], gl = sG[l];
-    const int lre = sLR[lastv];
-    float* cf = coef + ((size_t)h * nchunk + chunk) * kCoef;
-    cf[l] = sLR[l] < 0 ? expf((float)gl) : 0.f;
-    cf[kC + l] = (l <= lastv && lre <= l) ? expf((float)(ge - gl)) : 0.f;
-    if (l == 0) cf[2 * kC] = lre < 0 ? expf((float)ge) : 0.f;
-  }
 }
 
-// ---- state part: o[t] += a(t, t0 - 1) S_p q_t, then S <- a(end) S_p + sum a(end, s) v kb^T
-// Block (head, 16 value rows), 4 waves, walking the chunks in order.  The block keeps the
-// transposed state rows S^T[c][i] (c: key column, i: one of its 16 value rows) in MFMA
-// accumulators, wave w holding key columns 16 NT w .. 16 NT (w + 1) - 1; lane (j, qq) of a
-// tile holds S^T[4 qq + r][j], which is exactly the B operand of the output product when
-// lane group qq sums key columns 4 qq .. 4 qq + 3, so the state never leaves registers.
-// Each wave forms the output over its own key columns for all 64 tokens (its q columns go
-// straight into A registers); the four partial outputs are summed through LDS and added
-// to the intra-chunk part already in o.  kb and v enter the state product with 4 tokens
-// per lane, so their rows are staged through LDS (row-major, 16-byte stores), double-
-// buffered: the next chunk's rows are loaded while this one computes and written to the
-// other buffer after it.  Loads go through buffer descriptors (rows past T read zero).
-template <int DK>
-__global__ __launch_bounds__(256) void k_la_chunk_state(const float* __restrict__ q,
-                                                        const float* __restrict__ kb,
-                                                        const float* __restrict__ v,
-                                                        const float* __restrict__ coef, int T,
-                                                        int n, int dv, int nchunk,
-                                                        float* __restrict__ o) {
-  constexpr int NT = DK / 64;                  // 16-column state tiles per wave
-  constexpr int SK = Pad<DK>::S;               // LDS row stride of the kb rows
-  constexpr int SV = 16 + 4;                   // LDS row stride of the v rows
-  constexpr int SO = 16 + 1;                   // LDS row stride of a partial output
-  constexpr int KP = kC * DK / 4 / 256;        // kb float4 pieces per thread and chunk
-  __shared__ __align__(16) float sK[2][kC * SK];  // kb rows [token][key column]
-  __shared__ __align__(16) float sV[2][kC * SV];  // this block's v columns [token][row]
-  __shared__ __align__(16) float sCf[2][kCoef];
-  __shared__ float sO[4][kC * SO];
-
-  // Every block of a head reads the same q and kb rows: the blocks of one head run on one
-  // XCD (hardware block b runs on XCD b % 8), so those rows come from that XCD's L2 after
-  // the first block's read.
-  const int bph = dv / 16;  // blocks per head
-  int h, slice;
-  if ((n & 7) == 0) {
-    const int k = blockIdx.x >> 3;
-    h = (blockIdx.x & 7) * (n >> 3) + k / bph;
-    slice = k % bph;
-  } else {
-    h = blockIdx.x / bph;
-    slice = blockIdx.x % bph;
-  }
-  const int i0 = 16 * slice;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int j = lane & 15, qq = lane >> 4;
-  const int qd = n * DK, vd = n * dv;
-  const int cw = 16 * NT * w;  // this wave's first key column
-  const uint32_t qrow = (uint32_t)qd * 4, vrow = (uint32_t)vd * 4;
-  const mx_rsrc_t rq = mx_rsrc(q, (uint32_t)T * qrow);
-  const mx_rsrc_t rk = mx_rsrc(kb, (uint32_t)T * qrow);
-  const mx_rsrc_t rv = mx_rsrc(v, (uint32_t)T * vrow);
-  const mx_rsrc_t rc = mx_rsrc(coef, (uint32_t)(n * nchunk * kCoef * 4));
-
-  // per-lane offsets: q fragment (token j of a 16-row group, columns cw + 4 qq ..), kb and v
-  // rows staged by this thread, coefficients
-  const uint32_t q_lane = (uint32_t)j * qrow + (uint32_t)(h * DK + cw + 4 * qq) * 4;
-  uint32_t k_lane[KP];
-  int k_lds[KP];
-#pragma unroll
-  for (int p = 0; p < KP; ++p) {
-    const int i = tid + 256 * p, r = i / (DK / 4), c = 4 * (i % (DK / 4));
-    k_lane[p] = (uint32_t)r * qrow + (uint32_t)(h * DK + c) * 4;
-    k_lds[p] = r * SK + c;
-  }
-  const int vr = tid >> 2, vc = 4 * (tid & 3);  // v: token vr, rows i0 + vc .. + 3
-  const uint32_t v_lane = (uint32_t)vr * vrow + (uint32_t)(h * dv + i0 + vc) * 4;
-
-  struct Staged {
-    int4_t k[KP];
-    int4_t v;
-    int4_t cf;
-  };
-  auto load_staged = [&](Staged& x, int ch) {
-    const uint32_t base = (uint32_t)ch * kC * qrow;
-#pragma unroll
-    for (int p = 0; p < KP; ++p) x.k[p] = mx_ld16(rk, k_lane[p] + base);
-    x.v = mx_ld16(rv, v_lane + (uint32_t)ch * kC * vrow);
-    x.cf = tid < kCoef / 4 ? mx_ld16(rc, (uint32_t)(((size_t)h * nchunk + ch) * kCoef * 4 + 16 * tid))
-                           : (int4_t){0, 0, 0, 0};
-  };
-  auto store_staged = [&](const Staged& x, int b) {
-#pragma unroll
-    for (int p = 0; p < KP; ++p) *(int4_t*)(sK[b] + k_lds[p]) = x.k[p];
-    *(int4_t*)(sV[b] + vr * SV + vc) = x.v;
-    if (tid < kCoef / 4) *(int4_t*)(sCf[b] + 4 * tid) = x.cf;
-  };
-  struct Direct {
-    int4_t qf[4][NT];  // q[t0 + 16 mt + j][cw + 16 u + 4 qq ..]  (A of the output product)
-    float oi[4];       // intra-chunk o of token 16 w + 4 qq + r, row i0 + j
-  };
-  auto load_direct = [&](Direct& x, int ch) {
-    const uint32_t base = (uint32_t)ch * kC * qrow;
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-      for (int u = 0; u < NT; ++u)
-        x.qf[mt][u] = mx_ld16(rq, q_lane + base + (uint32_t)(16 * mt) * qrow + 64u * u);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = ch * kC + 16 * w + 4 * qq + r;
-      x.oi[r] = t < T ? o[(size_t)t * vd + h * dv + i0 + j] : 0.f;
-    }
-  };
-
-  float4_t st[NT];
-#pragma unroll
-  for (int u = 0; u < NT; ++u) st[u] = (float4_t){0.f, 0.f, 0.f, 0.f};
-
-  // one chunk: operands in LDS buffer b and in x.  The output product reads the old state
-  // and the new contribution goes into fresh accumulators, so the two groups of MFMAs (four
-  // independent chains each, no VALU between them) do not wait on each other; the state is
-  // combined at the end: S^T <- a(end) S^T + U^T.
-  auto step = [&](const Direct& x, int ch, int b) {
-    const float* cf = sCf[b];
-    // contribution U^T = sum_s kb_s (a(end, s) v_s)^T: B operands first (v times a(end, s))
-    // token s = 16 kg + 4 qq + e: kb[s][cw + 16 u + j] (A) and v[s][i0 + j] a(end, s) (B),
-    // four rows per lane read one value each (lane groups qq sit 16 banks apart)
-    float bv[4][4];
-#pragma unroll
-    for (int kg = 0; kg < 4; ++kg) {
-      const float4 ws = *(const float4*)(cf + kC + 16 * kg + 4 * qq);
-      const float* vp = sV[b] + (16 * kg + 4 * qq) * SV + j;
-      bv[kg][0] = vp[0] * ws.x;
-      bv[kg][1] = vp[SV] * ws.y;
-      bv[kg][2] = vp[2 * SV] * ws.z;
-      bv[kg][3] = vp[3 * SV] * ws.w;
-    }
-    float4 ka[4][NT];
-#pragma unroll
-    for (int kg = 0; kg < 4; ++kg)
-#pragma unroll
-      for (int u = 0; u < NT; ++u) {
-        const float* kp = sK[b] + (16 * kg + 4 * qq) * SK + cw + 16 * u + j;
-        ka[kg][u] = make_float4(kp[0], kp[SK], kp[2 * SK], kp[3 * SK]);
-      }
-    // partial output over this wave's key columns, all 64 tokens: (q_t S^T) scaled by a(t)
-    float4_t op[4], ua[NT], ub[NT];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) op[mt] = (float4_t){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int u = 0; u < NT; ++u) ua[u] = ub[u] = (float4_t){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int u = 0; u < NT; ++u)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          const float4 a = __builtin_bit_cast(float4, x.qf[mt][u]);
-          const float av = e == 0 ? a.x : (e == 1 ? a.y : (e == 2 ? a.z : a.w));
-          op[mt] = mfma4(av, st[u][e], op[mt]);
-        }
-        // two state chains per tile: token groups 0-1 and 2-3
-#pragma unroll
-        for (int kh = 0; kh < 2; ++kh) {
-          const float4 k0 = ka[2 * kh][u], k1 = ka[2 * kh + 1][u];
-          const float ka0 = e == 0 ? k0.x : (e == 1 ? k0.y : (e == 2 ? k0.z : k0.w));
-          const float ka1 = e == 0 ? k1.x : (e == 1 ? k1.y : (e == 2 ? k1.z : k1.w));
-          float4_t& acc = kh == 0 ? ua[u] : ub[u];
-          acc = mfma4(ka0, bv[2 * kh][e], acc);
-          acc = mfma4(ka1, bv[2 * kh + 1][e], acc);
-        }
-      }
-    const float gam = cf[2 * kC];
-#pragma unroll
-    for (int u = 0; u < NT; ++u) st[u] = st[u] * gam + ua[u] + ub[u];
-    // lane (j, qq) holds op[mt][r] for token 16 mt + 4 qq + r, row j
-    float* so = sO[w];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        so[(16 * mt + 4 * qq + r) * SO + j] = op[mt][r] * cf[16 * mt + 4 * qq + r];
-    (void)ch;
-  };
-  auto finish = [&](const Direct& x, int ch) {
-    const int t0 = ch * kC;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int tl = 16 * w + 4 * qq + r, t = t0 + tl;
-      float sum = x.oi[r];
-#pragma unroll
-      for (int w2 = 0; w2 < 4; ++w2) sum += sO[w2][tl * SO + j];
-      if (t < T) o[(size_t)t * vd + h * dv + i0 + j] = sum;
-    }
-  };
-
-  Staged sg;
-  Direct da, db;
-  load_staged(sg, 0);
-  load_direct(da, 0);
-  store_staged(sg, 0);
-  __syncthreads();
-  // Iteration ch: loads of chunk ch + 1 in flight while chunk ch computes from LDS buffer
-  // ch & 1; the staged rows then go to the other buffer.  Two chunks per pass so the
-  // direct operands alternate between two register sets without copies.
-  for (int ch = 0; ch < nchunk; ch += 2) {
-    const bool more1 = ch + 1 < nchunk;
-    if (more1) {
-      load_staged(sg, ch + 1);
-      load_direct(db, ch + 1);
-    }
-    step(da, ch, 0);
-    __syncthreads();  // partial outputs complete; LDS buffer 0 read
-    finish(da, ch);
-    if (more1) store_staged(sg, 1);
-    __syncthreads();  // buffer 1 written, partial outputs read
-    if (!more1) break;
-    const bool more2 = ch + 2 < nchunk;
-    if (more2) {
-      load_staged(sg, ch + 2);
-      load_direct(da, ch + 2);
-    }
-    step(db, ch + 1, 1);
-    __syncthreads();
-    finish(db, ch + 1);
-    if (more2) store_staged(sg, 0);
-    __syncthreads();
-  }
+// Workspace: the coefficient records [n][nchunk] (1 KiB each), then the stored states
+// [n][nchunk - 1][DV][DK] (fp32).
+size_t chunk_coef_bytes(int T, int n) { return (size_t)n * ((T + kC - 1) / kC) * kCoef * 4; }
+size_t chunk_state_bytes(int T, int n, int dk, int dv) {
+  return (size_t)n * ((T + kC - 1) / kC - 1) * dk * dv * 4;
 }
 
 template <int DK, int DV>
 int launch_chunked(const float* q, const float* kb, const float* v, const float* decay, int T,
-                   int n, float* o, float* coef, hipStream_t s) {
+                   int n, float* o, char* ws, hipStream_t s) {
   const int nchunk = (T + kC - 1) / kC;
+  float* coef = (float*)ws;
+  float* S = (float*)(ws + mx_align_up(chunk_coef_bytes(T, n), 256));
   mx_clear_error();
-  hipLaunchKernelGGL((k_la_chunk_intra<DK, DV>), dim3((unsigned)(nchunk * n)), dim3(256), 0, s,
-                     q, kb, v, decay, T, n, nchunk, o, coef);
-  MX_TRY(mx_launch_status());
-  hipLaunchKernelGGL((k_la_chunk_state<DK>), dim3((unsigned)(n * (DV / 16))), dim3(256), 0, s,
-                     q, kb, v, coef, T, n, DV, nchunk, o);
+  if (nchunk > 1) {
+    hipLaunchKernelGGL(k_la_chunk_coef, dim3((unsigned)mx_ceil_div(n * nchunk, 4)), dim3(256),
+                       0, s, decay, T, n, nchunk, coef);
+    MX_TRY(mx_launch_status());
+    constexpr int BPH = (DV / 32) * (DK / 64);
+    hipLaunchKernelGGL((k_la_chunk_states<DK, DV>), dim3((unsigned)(n * BPH)), dim3(256), 0, s,
+                       kb, v, coef, T, n, nchunk, S);
+    MX_TRY(mx_launch_status());
+  }
+  hipLaunchKernelGGL((k_la_chunk_out<DK, DV>), dim3((unsigned)(nchunk * n)), dim3(256), 0, s,
+                     q, kb, v, decay, S, T, n, nchunk, o);
   return mx_launch_status();
 }
 
@@ -462,26 +531,29 @@ bool chunk_shape(int dk, int dv) { return (dk == 64 || dk == 128) && (dv == 64 |
 
 }  // namespace
 
-size_t mx_la_chunk_coef_bytes(int T, int n, int dk, int dv) {
+size_t mx_la_chunk_ws_bytes(int T, int n, int dk, int dv) {
   if (T <= 0 || !chunk_shape(dk, dv)) return 0;
-  return (size_t)n * ((T + kC - 1) / kC) * kCoef * sizeof(float);
+  return mx_align_up(chunk_coef_bytes(T, n), 256) + chunk_state_bytes(T, n, dk, dv);
 }
 
 // Chunked scan for the head shapes it is built for (key and value heads of 64 or 128), with
-// `coef` of mx_la_chunk_coef_bytes; MX_ERR_UNSUPPORTED for other shapes (the caller then
-// runs the token-sequential scan).
+// `ws` of mx_la_chunk_ws_bytes; MX_ERR_UNSUPPORTED for other shapes (the caller then runs
+// the token-sequential scan).
 int mx_la_chunked_scan(const float* q, const float* kb, const float* v, const float* decay,
-                       int T, int n, int dk, int dv, float* o, void* coef, hipStream_t s) {
+                       int T, int n, int dk, int dv, float* o, void* ws, hipStream_t s) {
   if (T <= 0 || n <= 0) return MX_ERR_INVALID;
-  if (!chunk_shape(dk, dv) || !coef) return MX_ERR_UNSUPPORTED;
+  if (!chunk_shape(dk, dv) || !ws) return MX_ERR_UNSUPPORTED;
   // buffer descriptors: byte offsets below 2^31
-  if ((long)T * n * (dk > dv ? dk : dv) * 4 >= (1l << 31)) return MX_ERR_UNSUPPORTED;
-  if (!mx_aligned16(q) || !mx_aligned16(kb) || !mx_aligned16(v) || !mx_aligned16(o) ||
-      !mx_aligned16(coef))
+  if ((long)T * n * (dk > dv ? dk : dv) * 4 >= (1l << 31) ||
+      chunk_coef_bytes(T, n) >= (1ul << 31) ||
+      (size_t)((T + kC - 1) / kC) * dk * dv * 4 >= (1ul << 31))
     return MX_ERR_UNSUPPORTED;
-  float* cf = (float*)coef;
-  if (dk == 128 && dv == 128) return launch_chunked<128, 128>(q, kb, v, decay, T, n, o, cf, s);
-  if (dk == 64 && dv == 64) return launch_chunked<64, 64>(q, kb, v, decay, T, n, o, cf, s);
-  if (dk == 128 && dv == 64) return launch_chunked<128, 64>(q, kb, v, decay, T, n, o, cf, s);
-  return launch_chunked<64, 128>(q, kb, v, decay, T, n, o, cf, s);
+  if (!mx_aligned16(q) || !mx_aligned16(kb) || !mx_aligned16(v) || !mx_aligned16(o) ||
+      !mx_aligned16(ws))
+    return MX_ERR_UNSUPPORTED;
+  char* w = (char*)ws;
+  if (dk == 128 && dv == 128) return launch_chunked<128, 128>(q, kb, v, decay, T, n, o, w, s);
+  if (dk == 64 && dv == 64) return launch_chunked<64, 64>(q, kb, v, decay, T, n, o, w, s);
+  if (dk == 128 && dv == 64) return launch_chunked<128, 64>(q, kb, v, decay, T, n, o, w, s);
+  return launch_chunked<64, 128>(q, kb, v, decay, T, n, o, w, s);
 }

@@ -67,7 +67,7 @@ struct Carve {
 struct LaWork {
   MxLinearAttnViews v;
   MxDenseWork dw;      // projections: entry 0 qkvz, 1 ba, 2 out
-  void* coef = nullptr;  // decay coefficients of the chunked scan (NULL: sequential scan)
+  void* chunk_ws = nullptr;  // chunked scan: coefficients and chunk states (NULL: sequential)
 };
 
 int layout(const MxLinearAttnDesc* d, int T, void* ws, LaWork* w, size_t* total) {
@@ -91,8 +91,8 @@ int layout(const MxLinearAttnDesc* d, int T, void* ws, LaWork* w, size_t* total)
   t.v.y = (float*)c.take(Tn * m.H * 4);
   char* dwb = (char*)c.take(mx_dense_work_bytes((int)Tn, d->weight_dtype, 3));
   mx_dense_work_carve(dwb, (int)Tn, d->weight_dtype, 3, &t.dw);
-  const size_t cb = mx_la_chunk_coef_bytes((int)Tn, m.n, m.dk, m.dv);
-  t.coef = cb ? c.take(cb) : nullptr;
+  const size_t cb = mx_la_chunk_ws_bytes((int)Tn, m.n, m.dk, m.dv);
+  t.chunk_ws = cb ? c.take(cb) : nullptr;
   if (w) *w = t;
   if (total) *total = mx_align_up(c.off, 256);
   return MX_OK;
@@ -545,9 +545,9 @@ int launch_scan(const float* q, const float* kb, const float* v, const float* de
 #define MX_LA_CHUNK_MIN_T 64
 #endif
 int scan_launch(const float* q, const float* kb, const float* v, const float* decay, int T,
-                int n, int dk, int dv, float* o, void* coef, hipStream_t s) {
-  if (T >= MX_LA_CHUNK_MIN_T && coef) {
-    const int rc = mx_la_chunked_scan(q, kb, v, decay, T, n, dk, dv, o, coef, s);
+                int n, int dk, int dv, float* o, void* chunk_ws, hipStream_t s) {
+  if (T >= MX_LA_CHUNK_MIN_T && chunk_ws) {
+    const int rc = mx_la_chunked_scan(q, kb, v, decay, T, n, dk, dv, o, chunk_ws, s);
     if (rc != MX_ERR_UNSUPPORTED) return rc;
   }
   switch (dk) {
@@ -687,7 +687,7 @@ int run_stage(int st, const MxLinearAttnDesc* d, const MxLinearAttnWeights* w, c
       return mx_launch_status();
     }
     case 4:
-      return scan_launch(k.v.q, k.v.kb, k.v.v, k.v.decay, T, m.n, m.dk, m.dv, k.v.o, k.coef,
+      return scan_launch(k.v.q, k.v.kb, k.v.v, k.v.decay, T, m.n, m.dk, m.dv, k.v.o, k.chunk_ws,
                          s);
     case 5:
       mx_clear_error();
@@ -800,7 +800,7 @@ extern "C" int mx_gated_delta_scan_workspace_size(int32_t tokens, int32_t n_head
   if (!nbytes || tokens < 0 || n_heads <= 0 || head_dim_k <= 0 || head_dim_v <= 0)
     return MX_ERR_INVALID;
   *nbytes = tokens >= MX_LA_CHUNK_MIN_T
-                ? mx_la_chunk_coef_bytes(tokens, n_heads, head_dim_k, head_dim_v)
+                ? mx_la_chunk_ws_bytes(tokens, n_heads, head_dim_k, head_dim_v)
                 : 0;
   return MX_OK;
 }

@@ -459,10 +459,12 @@ int mx_gated_delta_scan(const float* q, const float* kb, const float* v, const f
                         int32_t tokens, int32_t n_heads, int32_t head_dim_k,
                         int32_t head_dim_v, float* o, void* stream);
 /* The same recurrence (qwen3_next.py:56-95) with a caller workspace: from 64 tokens, for
- * key and value heads of 64 or 128, in chunks of 64 tokens on fp32 MFMA (the products
- * inside a chunk in parallel, then one pass over the chunks per head carrying the state);
- * other shapes and shorter inputs run the token-sequential scan.  The workspace holds the
- * per-chunk decay coefficients (mx_gated_delta_scan_workspace_size bytes, 0 when the
+ * key and value heads of 64 or 128, in chunks of 64 tokens on fp32 MFMA (one pass over the
+ * chunks per head carrying the state through the chunks' increments, then every chunk's
+ * output in parallel from the state it starts from); other shapes and shorter inputs run
+ * the token-sequential scan.  The workspace (16-byte aligned) holds per-chunk decay
+ * coefficients and the fp32 state each chunk after the first starts from
+ * (mx_gated_delta_scan_workspace_size bytes, about T / 64 * n * dk * dv * 4; 0 when the
  * sequential scan runs); a smaller one gives MX_ERR_WORKSPACE.  The linear-attention
  * block uses this form inside its own workspace.                                       */
 int mx_gated_delta_scan_workspace_size(int32_t tokens, int32_t n_heads, int32_t head_dim_k,
