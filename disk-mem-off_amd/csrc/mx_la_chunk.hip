@@ -89,12 +89,16 @@ __device__ __forceinline__ double shfl_d(double v, int src) {
 // One wave, lane l = token t0 + l of the chunk: G_l (log decay from the segment start up to
 // and including l) and the last zero-decay token at or before l (-1: none in the chunk).
 // Tokens past T take d = 1.
-__device__ __forceinline__ void chunk_log_decay_reg(const float* __restrict__ decay, int t0,
-                                                    int T, int n, int h, double& G, int& LR) {
+__device__ __forceinline__ float chunk_decay_load(const float* __restrict__ decay, int t0,
+                                                  int T, int n, int h) {
+  const int t = t0 + (threadIdx.x & 63);
+  return t < T ? decay[(size_t)t * n + h] : 1.f;
+}
+
+// The prefix from the lane's decay d (chunk_decay_load).
+__device__ __forceinline__ void chunk_log_decay_of(float d, int t0, int T, double& G, int& LR) {
   const int l = threadIdx.x & 63;
-  const int t = t0 + l;
-  const float d = t < T ? decay[(size_t)t * n + h] : 1.f;
-  const bool reset = t < T && !(d > 0.f);
+  const bool reset = t0 + l < T && !(d > 0.f);
   double p = (d > 0.f) ? log((double)d) : 0.0;
   int lr = reset ? l : -1;
 #pragma unroll
@@ -111,11 +115,17 @@ __device__ __forceinline__ void chunk_log_decay_reg(const float* __restrict__ de
   LR = lr;
 }
 
-__device__ __forceinline__ void chunk_log_decay(const float* __restrict__ decay, int t0, int T,
-                                                int n, int h, double* sG, int* sLR) {
+__device__ __forceinline__ void chunk_log_decay_reg(const float* __restrict__ decay, int t0,
+                                                    int T, int n, int h, double& G, int& LR) {
+  chunk_log_decay_of(chunk_decay_load(decay, t0, T, n, h), t0, T, G, LR);
+}
+
+// The same prefix written to LDS (sG, sLR: 64 entries).
+__device__ __forceinline__ void chunk_log_decay_lds(float d, int t0, int T, double* sG,
+                                                    int* sLR) {
   double G;
   int LR;
-  chunk_log_decay_reg(decay, t0, T, n, h, G, LR);
+  chunk_log_decay_of(d, t0, T, G, LR);
   sG[threadIdx.x & 63] = G;
   sLR[threadIdx.x & 63] = LR;
 }
@@ -352,13 +362,20 @@ __global__ __launch_bounds__(256) void k_la_chunk_states(const float* __restrict
 }
 
 // ---- output: o[t] = sum_{t0 <= s <= t} a(t, s) (kb_s . q_t) v_s + a(t, t0 - 1) S_{c-1} q_t
-// Block (chunk, head), 4 waves; wave w takes tokens 16 w .. 16 w + 15 of the chunk.  Its q
-// rows go straight into MFMA A registers and serve both products with q.  The inter-chunk
-// part comes first: B = S_{c-1}[16 nt + j][16 u + 4 qq ..] read straight from the stored
-// states (one value tile ahead), scaled by a(t, t0 - 1) once summed.  kb (B of the scores,
-// all 64 tokens) and v (B of the products with v) are shared through LDS (row-major, 16-byte
-// stores; their loads are issued first and land during the inter-chunk products), and the
-// kb region is then reused for each wave's masked scores (A of the products with v).
+// Block (chunk, head), 4 waves.  Wave w owns key tokens 16 w .. 16 w + 15 of the scores and
+// value columns CW w .. CW w + CW - 1 (CW = DV / 4) of the output, for all 64 tokens:
+//   scores  P[t][16 w + j]     = Q[t] . kb[16 w + j]        A = q rows (LDS), B = kb (registers)
+//   inter   O[t][CW w + ..]    = a(t) Q[t] . S[CW w + ..]   A = the same q fragments, B = its
+//                                                           state rows (registers)
+//   intra   O[t][CW w + ..]   += sum_s P[t][s] v[s][CW w + ..]  A = P (LDS), B = v (LDS)
+// so each q fragment read from LDS feeds the score and the inter-chunk MFMAs, and no wave
+// loads what another loads: the block reads q, kb, v and the state once.  q and v enter LDS
+// by the buffer loads' LDS mode, issued first with the kb and state loads; a q row's 16-byte
+// piece p sits at position (p + t % 16) mod (dk / 4) and a v row's at (p + 4 ((t / 4) % 4))
+// mod (dv / 4), so the operand reads hit distinct banks.  The masked scores then replace q in
+// LDS (64-float rows, piece p of row t at (p + t % 16) mod 16).  Rows past T read as zeros
+// through the descriptors, and chunk 0 (which starts from S = 0) reads its state rows out of
+// range, also zeros.
 template <int DK, int DV>
 __global__ __launch_bounds__(256, 2) void k_la_chunk_out(const float* __restrict__ q,
                                                          const float* __restrict__ kb,
@@ -367,136 +384,139 @@ __global__ __launch_bounds__(256, 2) void k_la_chunk_out(const float* __restrict
                                                          const float* __restrict__ S, int T,
                                                          int n, int nchunk,
                                                          float* __restrict__ o) {
-  constexpr int SK = Pad<DK>::S, SC = Pad<kC>::S, SV = Pad<DV>::S;
-  constexpr int KP = kC * DK / 4 / 256, VP = kC * DV / 4 / 256;  // float4 pieces per thread
-  constexpr int NU = DK / 16, NV = DV / 16;
-  static_assert(4 * 16 * SC <= kC * SK, "masked scores reuse the kb tile");
-  __shared__ __align__(16) float sK[kC * SK];    // kb tile, then the masked scores
-  __shared__ __align__(16) float sV[kC * SV];    // v tile [token][value row]
+  constexpr int NU = DK / 16;    // 16-column groups of a q / kb / state row
+  constexpr int CW = DV / 4;     // value columns per wave
+  constexpr int NCT = CW / 16;   // value tiles per wave
+  constexpr int QPR = DK / 4;    // 16-byte pieces per q row
+  constexpr int VPR = DV / 4;    // 16-byte pieces per v row
+  constexpr int NQC = DK / 16;   // q copies per wave (kC * DK * 4 bytes / 1 KiB / 4 waves)
+  constexpr int NVC = DV / 16;   // v copies per wave
+  static_assert(kC * 64 <= kC * DK, "the scores fit in the q region");
+  __shared__ __align__(1024) float sQ[kC * DK];  // q rows, then the masked scores
+  __shared__ __align__(1024) float sV[kC * DV];  // v rows
   __shared__ double sG[kC];
   __shared__ int sLR[kC];
 
   const int chunk = blockIdx.x % nchunk, h = blockIdx.x / nchunk;
   const int t0 = chunk * kC;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, qq = lane >> 4;
-  const int qd = n * DK, vd = n * DV;
+  const uint32_t qrow = (uint32_t)n * DK * 4, vrow = (uint32_t)n * DV * 4;
+  const uint32_t tq = (uint32_t)t0 * qrow, tv = (uint32_t)t0 * vrow;
+  const mx_rsrc_t rq = mx_rsrc(q, (uint32_t)T * qrow);
+  const mx_rsrc_t rk = mx_rsrc(kb, (uint32_t)T * qrow);
+  const mx_rsrc_t rv = mx_rsrc(v, (uint32_t)T * vrow);
+  // wave 0's decays first: its prefix then waits on them alone
+  const float dl = w == 0 ? chunk_decay_load(decay, t0, T, n, h) : 1.f;
 
-  // every global load of the block first, then the LDS stores
-  float4 qa[NU];
-  const int tq = t0 + 16 * w + j;
+  // q and v tiles into LDS: copy i fills floats 256 i .. 256 i + 255 of the tile
+#pragma unroll
+  for (int m = 0; m < NQC; ++m) {
+    const int i = NQC * w + m, f = 256 * i + 4 * lane, t = f / DK;
+    const int p = ((f % DK) / 4 - (t & 15)) & (QPR - 1);
+    mx_copy_to_lds16(rq, (char*)sQ + 1024 * i, tq + (uint32_t)t * qrow + (uint32_t)(h * DK + 4 * p) * 4);
+  }
+#pragma unroll
+  for (int m = 0; m < NVC; ++m) {
+    const int i = NVC * w + m, f = 256 * i + 4 * lane, t = f / DV;
+    const int p = ((f % DV) / 4 - 4 * ((t >> 2) & 3)) & (VPR - 1);
+    mx_copy_to_lds16(rv, (char*)sV + 1024 * i, tv + (uint32_t)t * vrow + (uint32_t)(h * DV + 4 * p) * 4);
+  }
+  // kb rows 16 w + j (B of the scores): k-slot qq of MFMA (u, e) is column 16 u + 4 qq + e
+  int4_t kbr[NU];
 #pragma unroll
   for (int u = 0; u < NU; ++u)
-    qa[u] = tq < T ? *(const float4*)(q + (size_t)tq * qd + h * DK + 16 * u + 4 * qq)
-                   : make_float4(0.f, 0.f, 0.f, 0.f);
-  float4 kr[KP], vr[VP];
+    kbr[u] = mx_ld16(rk, tq + (uint32_t)(16 * w + j) * qrow + (uint32_t)(h * DK + 16 * u + 4 * qq) * 4);
+  // state rows CW w + 16 ct + j of S_{chunk-1} (B of the inter-chunk products)
+  const mx_rsrc_t rs = mx_rsrc(S + (size_t)h * (nchunk - 1) * DV * DK,
+                               (uint32_t)(nchunk - 1) * DV * DK * 4);
+  const uint32_t s_base = chunk > 0 ? (uint32_t)(chunk - 1) * DV * DK * 4 : MX_OOB;
+  int4_t sr[NCT][NU];
 #pragma unroll
-  for (int p = 0; p < KP; ++p) {
-    const int i = tid + 256 * p, r = i / (DK / 4), c = 4 * (i % (DK / 4)), t = t0 + r;
-    kr[p] = t < T ? *(const float4*)(kb + (size_t)t * qd + h * DK + c)
-                  : make_float4(0.f, 0.f, 0.f, 0.f);
-  }
+  for (int ct = 0; ct < NCT; ++ct)
 #pragma unroll
-  for (int p = 0; p < VP; ++p) {
-    const int i = tid + 256 * p, r = i / (DV / 4), c = 4 * (i % (DV / 4)), t = t0 + r;
-    vr[p] = t < T ? *(const float4*)(v + (size_t)t * vd + h * DV + c)
-                  : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int u = 0; u < NU; ++u)
+      sr[ct][u] = mx_ld16(rs, s_base | (uint32_t)(((CW * w + 16 * ct + j) * DK + 16 * u + 4 * qq) * 4));
+  if (w == 0) {
+    chunk_log_decay_lds(dl, t0, T, sG, sLR);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the prefix is in LDS
   }
-  if (w == 0) chunk_log_decay(decay, t0, T, n, h, sG, sLR);
+  // this wave's q copies, then everyone's (and the decay prefix) are in LDS
+  mx_wait_copies_and_barrier<NVC + NU + NCT * NU>();
 
-  float4_t oacc[NV];
+  // scores and inter-chunk products, one q fragment read per (mt, u)
+  float4_t pacc[4], oacc[4][NCT];
 #pragma unroll
-  for (int nt = 0; nt < NV; ++nt) oacc[nt] = (float4_t){0.f, 0.f, 0.f, 0.f};
-  if (chunk > 0) {
-    // (Q S^T)[16 w + 4 qq + r][16 nt + j]; the state the chunk starts from is S_{chunk-1}
-    const mx_rsrc_t rs = mx_rsrc(S + ((size_t)h * (nchunk - 1) + chunk - 1) * DV * DK,
-                                 (uint32_t)DV * DK * 4);
-    const uint32_t s_lane = (uint32_t)(j * DK + 4 * qq) * 4;
-    int4_t sb[2][NU];
+  for (int mt = 0; mt < 4; ++mt) {
+    pacc[mt] = (float4_t){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int u = 0; u < NU; ++u) sb[0][u] = mx_ld16(rs, s_lane + 64u * u);
+    for (int ct = 0; ct < NCT; ++ct) oacc[mt][ct] = (float4_t){0.f, 0.f, 0.f, 0.f};
+  }
 #pragma unroll
-    for (int nt = 0; nt < NV; ++nt) {
-      if (nt + 1 < NV) {
+  for (int mt = 0; mt < 4; ++mt) {
+    const int t = 16 * mt + j;
 #pragma unroll
-        for (int u = 0; u < NU; ++u)
-          sb[(nt + 1) & 1][u] = mx_ld16(rs, s_lane + (uint32_t)(16 * (nt + 1) * DK) * 4 + 64u * u);
-      }
+    for (int u = 0; u < NU; ++u) {
+      const float4 a = *(const float4*)(sQ + t * DK + 4 * ((4 * u + qq + j) & (QPR - 1)));
+      pacc[mt] = mfma_k16(a, __builtin_bit_cast(float4, kbr[u]), pacc[mt]);
 #pragma unroll
-      for (int u = 0; u < NU; ++u)
-        oacc[nt] = mfma_k16(qa[u], __builtin_bit_cast(float4, sb[nt & 1][u]), oacc[nt]);
+      for (int ct = 0; ct < NCT; ++ct)
+        oacc[mt][ct] = mfma_k16(a, __builtin_bit_cast(float4, sr[ct][u]), oacc[mt][ct]);
     }
   }
-
+  // lane (j, qq) holds P[16 mt + 4 qq + r][16 w + j] and O[16 mt + 4 qq + r][CW w + 16 ct + j]
+  float pm[4][4];
 #pragma unroll
-  for (int p = 0; p < KP; ++p) {
-    const int i = tid + 256 * p, r = i / (DK / 4), c = 4 * (i % (DK / 4));
-    *(float4*)(sK + r * SK + c) = kr[p];
-  }
-#pragma unroll
-  for (int p = 0; p < VP; ++p) {
-    const int i = tid + 256 * p, r = i / (DV / 4), c = 4 * (i % (DV / 4));
-    *(float4*)(sV + r * SV + c) = vr[p];
-  }
-  __syncthreads();
-
-  if (chunk > 0) {
+  for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int tl = 16 * w + 4 * qq + r;
+      const int tl = 16 * mt + 4 * qq + r, sl = 16 * w + j;
       const float at = sLR[tl] < 0 ? expf((float)sG[tl]) : 0.f;
 #pragma unroll
-      for (int nt = 0; nt < NV; ++nt) oacc[nt][r] *= at;
+      for (int ct = 0; ct < NCT; ++ct) oacc[mt][ct][r] *= at;
+      const float f = (sl <= tl && sLR[tl] <= sl) ? expf((float)(sG[tl] - sG[sl])) : 0.f;
+      pm[mt][r] = pacc[mt][r] * f;
     }
-  }
-
-  // scores of this wave's 16 tokens against the chunk's 64: P = Q Kb^T
-  float4_t pacc[4];
+  __syncthreads();  // every wave is done with the q rows: their region takes the scores
+  // P[t][s] at row t, piece (s / 4 + t % 16) mod 16
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt) pacc[nt] = (float4_t){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int u = 0; u < NU; ++u) {
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-      const float4 b = *(const float4*)(sK + (16 * nt + j) * SK + 16 * u + 4 * qq);
-      pacc[nt] = mfma_k16(qa[u], b, pacc[nt]);
-    }
-  }
-  __syncthreads();  // every wave is done with the kb tile: its region takes the scores
-  // causal mask and decay factors; lane (j, qq) holds P[16 w + 4 qq + r][16 nt + j]
-  float* myP = sK + w * 16 * SC;
-#pragma unroll
-  for (int nt = 0; nt < 4; ++nt)
+  for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int tl = 16 * w + 4 * qq + r, sl = 16 * nt + j;
-      const float f = (sl <= tl && sLR[tl] <= sl) ? expf((float)(sG[tl] - sG[sl])) : 0.f;
-      myP[(4 * qq + r) * SC + sl] = pacc[nt][r] * f;
+      const int tl = 16 * mt + 4 * qq + r;
+      sQ[tl * 64 + 4 * ((4 * w + (j >> 2) + tl) & 15) + (j & 3)] = pm[mt][r];
     }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  __syncthreads();  // the scores and every wave's v copies are in LDS
 
-  // o += P V over the chunk's 64 tokens; token s = k0 + 4 qq + e of v row 16 nt + j (four
-  // rows per lane, one value each: lane groups qq sit 16 banks apart)
+  // O[16 mt + ..] += P[16 mt + ..][s] v[s][CW w + 16 ct + ..] over the keys s <= the tile's
+  // last token: token s = 16 kg + 4 qq + e is k-slot qq of MFMA (kg, e)
 #pragma unroll
-  for (int k0 = 0; k0 < kC; k0 += 16) {
-    const float4 a = *(const float4*)(myP + j * SC + k0 + 4 * qq);
+  for (int mt = 0; mt < 4; ++mt) {
+    const int t = 16 * mt + j;
 #pragma unroll
-    for (int nt = 0; nt < NV; ++nt) {
-      const float* vp = sV + (k0 + 4 * qq) * SV + 16 * nt + j;
-      const float4 b = make_float4(vp[0], vp[SV], vp[2 * SV], vp[3 * SV]);
-      oacc[nt] = mfma_k16(a, b, oacc[nt]);
+    for (int kg = 0; kg <= mt; ++kg) {
+      const float4 a = *(const float4*)(sQ + t * 64 + 4 * ((4 * kg + qq + j) & 15));
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) {
+        const int pc = (CW * w + 16 * ct + j) >> 2;
+        const float* vp = sV + (16 * kg + 4 * qq) * DV + 4 * ((pc + 4 * qq) & (VPR - 1)) + (j & 3);
+        const float4 b = make_float4(vp[0], vp[DV], vp[2 * DV], vp[3 * DV]);
+        oacc[mt][ct] = mfma_k16(a, b, oacc[mt][ct]);
+      }
     }
   }
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int t = t0 + 16 * w + 4 * qq + r;
-    if (t < T) {
+  for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-      for (int nt = 0; nt < NV; ++nt) o[(size_t)t * vd + h * DV + 16 * nt + j] = oacc[nt][r];
+    for (int r = 0; r < 4; ++r) {
+      const int t = t0 + 16 * mt + 4 * qq + r;
+      if (t < T) {
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct)
+          o[(size_t)t * n * DV + h * DV + CW * w + 16 * ct + j] = oacc[mt][ct][r];
+      }
     }
-  }
 }
 
 // Workspace: the coefficient records [n][nchunk] (1 KiB each), then the stored states
