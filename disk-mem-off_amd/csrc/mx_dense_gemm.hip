@@ -162,7 +162,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, OCC) void k_gemm_nt(
   // Copy lane l loads row cr = l / 4 of its fragment, 16-byte chunk mx_frag_copy_chunk(l),
   // so every 4 consecutive lanes read one row's 64 contiguous bytes (the address unit
   // merges them); the chunk rotation (mx_lds_copy.h) makes the MFMA operand reads below
-  // (lane (j, q) reads row j, chunk q at mx_frag_read_pos(j, q)) hit distinct bank groups.
+  // (lane (j, q) reads row j, chunk q at mx_frag_read_pos(j, q)) free of bank conflicts.
   const int cr = lane >> 2, cq = mx_frag_copy_chunk(lane);
   const int rpos = mx_frag_read_pos(j, q);
   uint32_t goff[DPW];

@@ -28,11 +28,12 @@ __device__ __forceinline__ void mx_wait_copies_and_barrier() {
 // Chunk rotation of the 1 KiB operand fragments (16 rows x 64 bytes) that the LDS copies
 // fill and the MFMA operand reads consume: row j's 16-byte chunk c sits at slot
 // 4 j + (c + mx_frag_rot(j)) mod 4.  The rotation keeps the four chunks of a row in its own
-// 64 bytes (so four consecutive copy lanes still read one row's 64 contiguous bytes) and
-// makes the reads of lanes (j, c), j = 0..15, fall in distinct 16-byte bank groups both
-// for 8 lanes per 128-byte LDS cycle (slots distinct mod 8 within j = 0..7 and 8..15) and
-// for 16 lanes per 256-byte cycle (slots distinct mod 16).
-__device__ __forceinline__ int mx_frag_rot(int j) { return ((j >> 2) + ((j >> 1) & 1) * 2) & 3; }
+// 64 bytes (so four consecutive copy lanes still read one row's 64 contiguous bytes).  With
+// rotation (j / 2) mod 4 the 16-byte reads of lanes (j, c) = (lane % 16, lane / 16) run
+// without bank-conflict cycles on gfx950 (SQ_LDS_BANK_CONFLICT 0, as for 64 lanes reading 1
+// KiB in order); the rotations (j / 4 + 2 ((j / 2) mod 2)) mod 4, (j / 4) mod 4, j mod 4 and
+// none each double the LDS cycles of the read (measured with a read-only probe).
+__device__ __forceinline__ int mx_frag_rot(int j) { return (j >> 1) & 3; }
 // Copy lane l's chunk (it loads row l / 4) and the byte offset of lane (j, c)'s operand.
 __device__ __forceinline__ int mx_frag_copy_chunk(int l) { return ((l & 3) - mx_frag_rot(l >> 2)) & 3; }
 __device__ __forceinline__ int mx_frag_read_pos(int j, int c) {
