@@ -489,6 +489,12 @@ __global__ __launch_bounds__(256) void k_expert(const ExpertParams p, const Sele
 #ifndef MX_LDS_OCC_F16
 #define MX_LDS_OCC_F16 2  // 4-wave fp16 blocks per CU
 #endif
+#ifndef MX_LDS_APAD
+// Padding of a staged activation row (bytes).  With 32 the MFMA operand reads (lane (j, q):
+// row j, 16-byte chunk q) and the staging stores run without bank-conflict cycles on gfx950;
+// with 16 the reads take twice the LDS cycles.
+#define MX_LDS_APAD 32
+#endif
 #ifndef MX_LDS_8W
 #define MX_LDS_8W 1  // 8-wave fp16 blocks where lds_eight_waves picks them
 #endif
@@ -520,7 +526,7 @@ __device__ __forceinline__ void expert_lds_tile(const ExpertParams& p, char* lds
   constexpr int KS = 4 * EPL * KM;           // reduction columns per stage
   constexpr int MB = 16 * MTX;
   constexpr int NF = GU ? 2 * NBIX : NBIX;
-  constexpr int AROW = KS * 2 + 16;          // LDS bytes per staged activation row
+  constexpr int AROW = KS * 2 + MX_LDS_APAD;  // LDS bytes per staged activation row
   constexpr int ATILE = MB * AROW;
   constexpr int CPR = KS * 2 / 16;           // 16-byte chunks per row and stage
   constexpr int ACH = MB * CPR / (64 * NW);  // chunks each thread stages
@@ -852,7 +858,7 @@ __global__ __launch_bounds__((64 * NW), (LdsShape<WF>::OCC * 4 / NW)) void k_exp
   constexpr int KS = 4 * WTr<WF>::EPL * LdsShape<WF>::KM;
   constexpr int NBI = GU ? 2 : 4;
   constexpr int MB = 128;
-  __shared__ __align__(16) char lds[2 * MB * (KS * 2 + 16)];
+  __shared__ __align__(16) char lds[2 * MB * (KS * 2 + MX_LDS_APAD)];
   __shared__ float wrow[CH > 1 ? MB : 1];
   const int nblk = (nslab + CH - 1) / CH;
 
