@@ -74,6 +74,52 @@ __device__ __forceinline__ float4_t mfma_k16(const float4& a, const float4& b, f
   return mfma4(a.w, b.w, c);
 }
 
+// fp32 products through bf16 MFMAs: x splits exactly into three bf16 planes, x = p0 + p1 + p2,
+// each plane the high half of the residual left by the planes before it (8 + 8 + 8
+// significant bits cover fp32's 24).  A dot product over 32 columns is then the six plane
+// products with p_a + p_b <= 2 (the three dropped ones are below 2^-21 of the sum of |a b|),
+// each exact in the fp32 accumulator, on v_mfma_f32_16x16x32_bf16: 6 x 16 cycles against
+// 8 x 32 for v_mfma_f32_16x16x4_f32.  Lane (j, q) passes 8 values (lo: 4 columns, hi: the 4
+// columns 16 further), element e of a plane in bits 16 e ..; any assignment of the 32
+// columns to (q, e) serves, as long as both operands use the same one.
+#ifndef LA_OUT_BF16X3
+#define LA_OUT_BF16X3 1  // the output launch's score and inter-chunk products on bf16 planes
+#endif
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ void bf16x3_split(const int4_t& lo, const int4_t& hi, int4_t (&p)[3]) {
+  uint32_t b[3][8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    uint32_t u = (uint32_t)(e < 4 ? lo[e] : hi[e - 4]);
+#pragma unroll
+    for (int l = 0; l < 3; ++l) {
+      b[l][e] = u;
+      if (l < 2) {
+        const float r = __builtin_bit_cast(float, u) - __builtin_bit_cast(float, u & 0xFFFF0000u);
+        u = __builtin_bit_cast(uint32_t, r);
+      }
+    }
+  }
+#pragma unroll
+  for (int l = 0; l < 3; ++l)
+#pragma unroll
+    for (int d = 0; d < 4; ++d) p[l][d] = (int)__builtin_amdgcn_perm(b[l][2 * d + 1], b[l][2 * d], 0x07060302u);
+}
+
+__device__ __forceinline__ float4_t mfma_bf16(const int4_t& a, const int4_t& b, float4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ float4_t mfma_bf16x3(const int4_t (&a)[3], const int4_t (&b)[3], float4_t c) {
+  c = mfma_bf16(a[2], b[0], c);
+  c = mfma_bf16(a[0], b[2], c);
+  c = mfma_bf16(a[1], b[1], c);
+  c = mfma_bf16(a[1], b[0], c);
+  c = mfma_bf16(a[0], b[1], c);
+  return mfma_bf16(a[0], b[0], c);
+}
+
 __device__ __forceinline__ double shfl_up_d(double v, int d) {
   const int lo = __shfl_up(__double2loint(v), d, 64);
   const int hi = __shfl_up(__double2hiint(v), d, 64);
@@ -161,43 +207,55 @@ __global__ __launch_bounds__(256) void k_la_chunk_coef(const float* __restrict__
 }
 
 // ---- state walk: S_c = a(end, t0 - 1) S_{c-1} + sum_s a(end, s) v_s kb_s^T ------------
-// Block = 32 value rows (i0 ..) x 64 key columns (c0 ..) of one head's state, 4 waves; wave w
-// holds the transposed tiles S^T[c0 + 16 w + ..][i0 + 16 rt + ..], rt = 0, 1, in MFMA
-// accumulators: lane (j, qq) of tile rt holds S[i0 + 16 rt + j][c0 + 16 w + 4 qq + r],
-// r = 0..3, which it stores as one 16-byte piece.  The increment of a chunk is
-// U^T = Kb^T (a(end) V): token s = 16 kg + 4 qq + e enters as k-slot qq of MFMA (kg, e), A =
-// kb[s][c0 + 16 w + j], B = v[s][i0 + 16 rt + j] a(end, s).
+// Block = 32 value rows (i0 ..) x 64 key columns (c0 ..) of one head's state: eight 16 x 16
+// tiles, LA_ST_NW waves (4: two tiles per wave, 8: one).  Wave w holds the transposed tiles
+// S^T[c0 + 16 ct + ..][i0 + 16 rt + ..] (ct = w % 4) in MFMA accumulators: lane (j, qq) of
+// tile rt holds S[i0 + 16 rt + j][c0 + 16 ct + 4 qq + r], r = 0..3, which it stores as one
+// 16-byte piece.  The increment of a chunk is U^T = Kb^T (a(end) V): token
+// s = 16 kg + 4 qq + e enters as k-slot qq of MFMA (kg, e), A = kb[s][c0 + 16 ct + j],
+// B = v[s][i0 + 16 rt + j] a(end, s).
 //
 // Operands come through an LDS ring of LA_NB chunk slots filled by the buffer loads' LDS
 // mode (no register holds a staged piece): per chunk the kb tile (64 tokens x 64 columns,
-// 16 KiB), the v tile (64 tokens x 32 rows, 8 KiB) and the coefficient record (1 KiB, one
-// copy per wave), 7 copies per wave, issued LA_NB - 1 chunks ahead.  Copy lane l of a kb copy
-// loads a 16-byte piece of token row r = l / 16 (of its 4 rows), placed at piece position
-// (p + 4 ((r / 4) % 4)) % 16 of the 16 in the row; a v copy holds 8 token rows of 8 pieces,
-// row R of the copy holding token R ^ ((R / 8) % 2) at piece position (p + 4 ((s / 4) % 2)) % 8.
-// With these rotations the 64 lanes of every operand read hit 64 distinct 4-byte banks.
-// Copies past the last chunk, and rows past T, use out-of-range offsets (they return zeros
-// and move no data), so every wave issues the same number of vector memory operations per
-// chunk and one constant wait count per iteration finds the chunk's copies complete.
+// 16 KiB), the v tile (64 tokens x 32 rows, 8 KiB) and the coefficient record (1 KiB),
+// issued LA_NB - 1 chunks ahead.  Copy lane l of a kb copy loads a 16-byte piece of token
+// row r = l / 16 (of its 4 rows), placed at piece position (p + 4 ((r / 4) % 4)) % 16 of the
+// 16 in the row; a v copy holds 8 token rows of 8 pieces, row R of the copy holding token
+// R ^ ((R / 8) % 2) at piece position (p + 4 ((s / 4) % 2)) % 8.  With these rotations the 64
+// lanes of every operand read hit 64 distinct 4-byte banks.  Wave 0 copies the coefficient
+// record; the other waves issue an out-of-range copy into a scratch kilobyte instead, and
+// copies past the last chunk, and rows past T, use out-of-range offsets too (they return
+// zeros and move no data): every wave issues the same number of vector memory operations per
+// chunk, so one constant wait count per iteration finds the chunk's copies complete.
 #ifndef LA_NB
 #define LA_NB 4  // chunk slots of the state walk's LDS ring
 #endif
+#ifndef LA_ST_NW
+#define LA_ST_NW 8  // waves per state-walk block (4 or 8)
+#endif
 
 template <int DK, int DV>
-__global__ __launch_bounds__(256) void k_la_chunk_states(const float* __restrict__ kb,
-                                                         const float* __restrict__ v,
-                                                         const float* __restrict__ coef,
-                                                         int T, int n, int nchunk,
-                                                         float* __restrict__ S) {
+__global__ __launch_bounds__(64 * LA_ST_NW) void k_la_chunk_states(const float* __restrict__ kb,
+                                                                   const float* __restrict__ v,
+                                                                   const float* __restrict__ coef,
+                                                                   int T, int n, int nchunk,
+                                                                   float* __restrict__ S) {
   constexpr int NB = LA_NB;
+  constexpr int NW = LA_ST_NW;
   static_assert(NB >= 2 && NB <= 5, "ring depth");
+  static_assert(NW == 4 || NW == 8, "waves per block");
+  constexpr int TPW = 8 / NW;           // state tiles per wave
+  constexpr int NCH = 4 / TPW;          // accumulator chains per tile
+  constexpr int KPW = 16 / NW;          // kb copies per wave and chunk
+  constexpr int VPW = 8 / NW;           // v copies per wave and chunk
   constexpr int RBK = DV / 32;          // 32-row blocks per head
   constexpr int BPH = RBK * (DK / 64);  // blocks per head
   constexpr int KB_BYTES = kC * 64 * 4;
   constexpr int V_BYTES = kC * 32 * 4;
-  constexpr int SLOT = KB_BYTES + V_BYTES + 4 * 1024;
-  constexpr int P = 7;                  // copies per wave and chunk
-  constexpr int ST = 2;                 // state stores per wave and chunk
+  constexpr int CF_OFF = KB_BYTES + V_BYTES;
+  constexpr int SLOT = CF_OFF + 2 * 1024;  // + the coefficient record and a scratch kilobyte
+  constexpr int P = KPW + VPW + 1;      // copies per wave and chunk
+  constexpr int ST = TPW;               // state stores per wave and chunk
   // One LDS variable per slot, every access naming its slot at compile time: the compiler
   // then tells a slot's reads from the copies in flight into the other slots (with a single
   // array it waits for every copy before any read).
@@ -229,6 +287,7 @@ __global__ __launch_bounds__(256) void k_la_chunk_states(const float* __restrict
   const int i0 = 32 * (sub % RBK), c0 = 64 * (sub / RBK);
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ct = w & 3, rt0 = (w >> 2) * TPW;  // the wave's key-column tile, first row tile
   const int j = lane & 15, qq = lane >> 4;
   const uint32_t qrow = (uint32_t)n * DK * 4, vrow = (uint32_t)n * DV * 4;
   const mx_rsrc_t rk = mx_rsrc(kb, (uint32_t)T * qrow);
@@ -238,59 +297,63 @@ __global__ __launch_bounds__(256) void k_la_chunk_states(const float* __restrict
   const mx_rsrc_t rs = mx_rsrc(S + (size_t)h * (nchunk - 1) * DV * DK, (uint32_t)(nchunk - 1) * SB);
 
   // copy offsets of this lane (chunk 0)
-  uint32_t k_off[4], v_off[2];
+  uint32_t k_off[KPW], v_off[VPW];
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const int r = 4 * (4 * w + m) + (lane >> 4);
+  for (int m = 0; m < KPW; ++m) {
+    const int r = 4 * (KPW * w + m) + (lane >> 4);
     const int p = ((lane & 15) - 4 * ((r >> 2) & 3)) & 15;
     k_off[m] = (uint32_t)r * qrow + (uint32_t)(h * DK + c0 + 4 * p) * 4;
   }
 #pragma unroll
-  for (int m = 0; m < 2; ++m) {
-    const int R = 8 * (2 * w + m) + (lane >> 3);
+  for (int m = 0; m < VPW; ++m) {
+    const int R = 8 * (VPW * w + m) + (lane >> 3);
     const int s = R ^ ((R >> 3) & 1);
     const int p = ((lane & 7) - 4 * ((s >> 2) & 1)) & 7;
     v_off[m] = (uint32_t)s * vrow + (uint32_t)(h * DV + i0 + 4 * p) * 4;
   }
+  // wave 0: the coefficient record; the others: out of range into the scratch kilobyte
+  const uint32_t c_oob = w == 0 ? 0u : MX_OOB;
+  const int c_dst = w == 0 ? CF_OFF : CF_OFF + 1024;
   const uint32_t c_off = (uint32_t)h * nchunk * kCoef * 4 + 16 * lane;
   auto copies = [&](char* slot, int ch) {
     const uint32_t oob = ch < nchunk ? 0u : MX_OOB;
     const uint32_t kbase = (uint32_t)ch * kC * qrow, vbase = (uint32_t)ch * kC * vrow;
 #pragma unroll
-    for (int m = 0; m < 4; ++m)
-      mx_copy_to_lds16(rk, slot + 1024 * (4 * w + m), (kbase + k_off[m]) | oob);
+    for (int m = 0; m < KPW; ++m)
+      mx_copy_to_lds16(rk, slot + 1024 * (KPW * w + m), (kbase + k_off[m]) | oob);
 #pragma unroll
-    for (int m = 0; m < 2; ++m)
-      mx_copy_to_lds16(rv, slot + KB_BYTES + 1024 * (2 * w + m), (vbase + v_off[m]) | oob);
-    mx_copy_to_lds16(rc, slot + KB_BYTES + V_BYTES + 1024 * w,
-                     (c_off + (uint32_t)ch * kCoef * 4) | oob);
+    for (int m = 0; m < VPW; ++m)
+      mx_copy_to_lds16(rv, slot + KB_BYTES + 1024 * (VPW * w + m), (vbase + v_off[m]) | oob);
+    mx_copy_to_lds16(rc, slot + c_dst, (c_off + (uint32_t)ch * kCoef * 4) | oob | c_oob);
   };
 
-  // operand read offsets (floats) of this lane: kb[s][c0 + 16 w + j] at kq + (16 kg + e) 64;
-  // v[s][i0 + 16 rt + j] at (e odd ? vo : ve)[rt] + (16 kg + e) 32
-  const int kq = 4 * qq * 64 + 4 * ((4 * w + (j >> 2) + 4 * qq) & 15) + (j & 3);
+  // operand read offsets (floats) of this lane: kb[s][c0 + 16 ct + j] at kq + (16 kg + e) 64;
+  // v[s][i0 + 16 rt + j] at (e odd ? vo : ve)[t] + (16 kg + e) 32
+  const int kq = 4 * qq * 64 + 4 * ((4 * ct + (j >> 2) + 4 * qq) & 15) + (j & 3);
   const int x = qq >> 1;
-  int ve[2], vo[2];
+  int ve[TPW], vo[TPW];
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
+  for (int t = 0; t < TPW; ++t) {
+    const int rt = rt0 + t;
     const int b = 4 * qq * 32 + 4 * ((4 * rt + (j >> 2) + 4 * (qq & 1)) & 7) + (j & 3);
-    ve[rt] = b + 32 * x;
-    vo[rt] = b - 32 * x;
+    ve[t] = b + 32 * x;
+    vo[t] = b - 32 * x;
   }
-  // this lane's stored piece of tile rt (bytes, state 0)
-  uint32_t s_off[2];
+  // this lane's stored piece of tile t (bytes, state 0)
+  uint32_t s_off[TPW];
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
-    s_off[rt] = (uint32_t)((i0 + 16 * rt + j) * DK + c0 + 16 * w + 4 * qq) * 4;
+  for (int t = 0; t < TPW; ++t)
+    s_off[t] = (uint32_t)((i0 + 16 * (rt0 + t) + j) * DK + c0 + 16 * ct + 4 * qq) * 4;
 
-  float4_t st[2];
-  st[0] = st[1] = (float4_t){0.f, 0.f, 0.f, 0.f};
+  float4_t st[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) st[t] = (float4_t){0.f, 0.f, 0.f, 0.f};
 
   auto step = [&](const char* slot, int ch) {
     const float* K = (const float*)slot;
     const float* V = (const float*)(slot + KB_BYTES);
-    const float* CF = (const float*)(slot + KB_BYTES + V_BYTES + 1024 * w);
-    float a[4][4], b[2][4][4];
+    const float* CF = (const float*)(slot + CF_OFF);
+    float a[4][4], b[TPW][4][4];
 #pragma unroll
     for (int kg = 0; kg < 4; ++kg) {
       const float4 ws = *(const float4*)(CF + 16 * kg + 4 * qq);
@@ -299,35 +362,44 @@ __global__ __launch_bounds__(256) void k_la_chunk_states(const float* __restrict
       for (int e = 0; e < 4; ++e) {
         a[kg][e] = K[kq + (16 * kg + e) * 64];
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
-          b[rt][kg][e] = V[((e & 1) ? vo[rt] : ve[rt]) + (16 * kg + e) * 32] * wv[e];
+        for (int t = 0; t < TPW; ++t)
+          b[t][kg][e] = V[((e & 1) ? vo[t] : ve[t]) + (16 * kg + e) * 32] * wv[e];
       }
     }
-    // four independent chains: tiles rt x token halves kh
-    float4_t acc[2][2];
+    // four independent chains: tiles x token groups
+    float4_t acc[TPW][NCH];
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) acc[rt][0] = acc[rt][1] = (float4_t){0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < TPW; ++t)
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
+      for (int c = 0; c < NCH; ++c) acc[t][c] = (float4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 4 / NCH; ++kk)
 #pragma unroll
       for (int e = 0; e < 4; ++e)
 #pragma unroll
-        for (int kh = 0; kh < 2; ++kh)
+        for (int c = 0; c < NCH; ++c)
 #pragma unroll
-          for (int rt = 0; rt < 2; ++rt)
-            acc[rt][kh] = mfma4(a[2 * kh + kk][e], b[rt][2 * kh + kk][e], acc[rt][kh]);
+          for (int t = 0; t < TPW; ++t) {
+            const int kg = c * (4 / NCH) + kk;
+            acc[t][c] = mfma4(a[kg][e], b[t][kg][e], acc[t][c]);
+          }
     const float gam = CF[kC];
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) st[rt] = st[rt] * gam + acc[rt][0] + acc[rt][1];
+    for (int t = 0; t < TPW; ++t) {
+      float4_t u = acc[t][0];
+#pragma unroll
+      for (int c = 1; c < NCH; ++c) u += acc[t][c];
+      st[t] = st[t] * gam + u;
+    }
     // S_ch, the state chunk ch + 1 starts from (the last chunk's store is out of range)
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(int4_t, st[rt]), rs,
-                                             (uint32_t)ch * SB + s_off[rt], 0, 0);
+    for (int t = 0; t < TPW; ++t)
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(int4_t, st[t]), rs,
+                                             (uint32_t)ch * SB + s_off[t], 0, 0);
   };
 
   // LDS starts zeroed: a row a copy does not fill holds finite values (a(end, s) = 0 there)
-  for (int i = threadIdx.x; i < SLOT / 16; i += 256) {
+  for (int i = threadIdx.x; i < SLOT / 16; i += 64 * NW) {
     const int4_t z = {0, 0, 0, 0};
     *(int4_t*)(lds0 + 16 * i) = z;
     *(int4_t*)(lds1 + 16 * i) = z;
@@ -453,16 +525,41 @@ __global__ __launch_bounds__(256, 2) void k_la_chunk_out(const float* __restrict
 #pragma unroll
     for (int ct = 0; ct < NCT; ++ct) oacc[mt][ct] = (float4_t){0.f, 0.f, 0.f, 0.f};
   }
+  if constexpr (LA_OUT_BF16X3) {
+    // bf16 planes of kb and of the state rows, per 32-column block m (u = 2m, 2m + 1)
+    int4_t kb3[NU / 2][3], s3[NCT][NU / 2][3];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-    const int t = 16 * mt + j;
+    for (int m = 0; m < NU / 2; ++m) {
+      bf16x3_split(kbr[2 * m], kbr[2 * m + 1], kb3[m]);
 #pragma unroll
-    for (int u = 0; u < NU; ++u) {
-      const float4 a = *(const float4*)(sQ + t * DK + 4 * ((4 * u + qq + j) & (QPR - 1)));
-      pacc[mt] = mfma_k16(a, __builtin_bit_cast(float4, kbr[u]), pacc[mt]);
+      for (int ct = 0; ct < NCT; ++ct) bf16x3_split(sr[ct][2 * m], sr[ct][2 * m + 1], s3[ct][m]);
+    }
 #pragma unroll
-      for (int ct = 0; ct < NCT; ++ct)
-        oacc[mt][ct] = mfma_k16(a, __builtin_bit_cast(float4, sr[ct][u]), oacc[mt][ct]);
+    for (int mt = 0; mt < 4; ++mt) {
+      const int t = 16 * mt + j;
+#pragma unroll
+      for (int m = 0; m < NU / 2; ++m) {
+        const int4_t a0 = *(const int4_t*)(sQ + t * DK + 4 * ((8 * m + qq + j) & (QPR - 1)));
+        const int4_t a1 = *(const int4_t*)(sQ + t * DK + 4 * ((8 * m + 4 + qq + j) & (QPR - 1)));
+        int4_t q3[3];
+        bf16x3_split(a0, a1, q3);
+        pacc[mt] = mfma_bf16x3(q3, kb3[m], pacc[mt]);
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) oacc[mt][ct] = mfma_bf16x3(q3, s3[ct][m], oacc[mt][ct]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const int t = 16 * mt + j;
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        const float4 a = *(const float4*)(sQ + t * DK + 4 * ((4 * u + qq + j) & (QPR - 1)));
+        pacc[mt] = mfma_k16(a, __builtin_bit_cast(float4, kbr[u]), pacc[mt]);
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct)
+          oacc[mt][ct] = mfma_k16(a, __builtin_bit_cast(float4, sr[ct][u]), oacc[mt][ct]);
+      }
     }
   }
   // lane (j, qq) holds P[16 mt + 4 qq + r][16 w + j] and O[16 mt + 4 qq + r][CW w + 16 ct + j]
@@ -538,7 +635,7 @@ int launch_chunked(const float* q, const float* kb, const float* v, const float*
                        0, s, decay, T, n, nchunk, coef);
     MX_TRY(mx_launch_status());
     constexpr int BPH = (DV / 32) * (DK / 64);
-    hipLaunchKernelGGL((k_la_chunk_states<DK, DV>), dim3((unsigned)(n * BPH)), dim3(256), 0, s,
+    hipLaunchKernelGGL((k_la_chunk_states<DK, DV>), dim3((unsigned)(n * BPH)), dim3(64 * LA_ST_NW), 0, s,
                        kb, v, coef, T, n, nchunk, S);
     MX_TRY(mx_launch_status());
   }
