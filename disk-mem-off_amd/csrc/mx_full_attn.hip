@@ -654,6 +654,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(FA_H_WP
 #ifndef FA_D_TAU
 #define FA_D_TAU 8.f  // lazy-rescale threshold of the running max (base-2 units)
 #endif
+#ifndef FA_D_PAIR
+#define FA_D_PAIR 1  // long and short query blocks paired on each CU
+#endif
 
 // Max over the lanes l, l ^ 16, l ^ 32 and l ^ 48 (one query's four lane groups) without
 // going through LDS: permlane16_swap exchanges 16-lane rows 2k and 2k + 1 between its two
@@ -689,12 +692,17 @@ void k_fa_attn_d(const float* __restrict__ qg, const half_t* __restrict__ k16,
   const int QB = WQ * NW;
   const int nqb = gridDim.x;
   int h = blockIdx.y, qx = blockIdx.x;  // qx = 0: the longest query block (the last one)
-  if (FA_H_XCD) {  // whole heads per XCD, longest query blocks first (as k_fa_attn_h)
+  if (FA_H_XCD) {  // whole heads per XCD (as k_fa_attn_h)
     const int nb = nqb * gridDim.y, per = nb >> 3;
     if ((nb & 7) == 0 && per % nqb == 0) {
       const int b = blockIdx.x + nqb * blockIdx.y, hpr = per / nqb, i = b >> 3;
       h = (b & 7) * hpr + i % hpr;
       qx = i / hpr;
+      // The XCD's first half of the blocks (the longest query blocks, longest first) takes
+      // one slot of each CU and the second half the other: with the second half shortest
+      // first, a CU's two query blocks have about the same sum of key tiles (the causal work
+      // of query block qx is proportional to nqb - qx).
+      if (FA_D_PAIR && (nqb & 1) == 0 && i >= per / 2) qx = nqb - 1 - (i - per / 2) / hpr;
     }
   }
   const int q0 = (nqb - 1 - qx) * QB;
