@@ -16,13 +16,16 @@
 //  split into slices over gridDim.y whose partial sums the top-k adds in slice order.
 //
 // Block tile BM x BN over one weight segment and one reduction slice; the reduction runs in
-// stages of 64 bytes per row (32 fp16 or 16 fp32 columns).  Both operands of a stage are
-// copied from global memory straight into LDS by the buffer loads' LDS mode (no register
-// staging), into a ring of NS stage slots: while the waves compute stage s, the copies of
-// stages s + 1 .. s + NS - 1 are in flight.  Each copy instruction moves one fragment of 16
-// rows x 64 bytes (1 KiB); the LDS mode stores lane l's 16 bytes at 16 l, so the
-// lane-to-(row, chunk) map of the copy fixes the layout of the fragment in LDS (see below:
-// coalesced rows, rotated chunks, no padding).
+// stages of 128 bytes per row (64 fp16 or 32 fp32 columns, two MFMA k-steps of 64 bytes).
+// Both operands of a stage are copied from global memory straight into LDS by the buffer
+// loads' LDS mode (no register staging), into a ring of NS stage slots: while the waves
+// compute stage s, the copies of stages s + 1 .. s + NS - 1 are in flight.  Each copy
+// instruction moves one fragment of 8 rows x 128 bytes (1 KiB), so every row piece a copy
+// reads is a whole 128-byte line: copies of 64-byte half lines (16 rows x 64 bytes) moved
+// half as many bytes per clock from L2 into LDS (26.5 against 51.6 bytes per clock and CU,
+// measured on MI355X with a copy-only probe; 4.5 against 5.8 TB/s from HBM).  The LDS mode
+// stores lane l's 16 bytes at 16 l, so the lane-to-(row, chunk) map of the copy fixes the
+// layout of the fragment in LDS (see below: whole rows, XOR-swizzled chunks, no padding).
 // A stage is waited for with an explicit vmcnt (the copies are this loop's only vector
 // memory operations) and a barrier without a memory fence: a fence on LDS would also wait
 // for every copy still in flight, which would empty the ring at every stage.
@@ -31,11 +34,11 @@
 // reads go through buffer descriptors: rows past M or past N_s read zero.  K must be a
 // multiple of the stage width (MX_ERR_UNSUPPORTED otherwise).
 //
-// Fragment layout (lane = 16 q + j): an activation fragment lane holds the 16 bytes of
-// a[m0 + j] at byte 16 q of the stage, a weight fragment lane those of W[n0 + j]; fp16
-// feeds them to one 16x16x32 MFMA (k = 8 q .. 8 q + 7), fp32 to four 16x16x4 MFMAs (the
-// e-th takes element e of both, so the four cover the stage's 16 columns once each).  With
-// the weights as the MFMA's A operand the accumulator lane holds y[m0 + j][n0 + 4 q + r],
+// Operand layout (lane = 16 q + j): at k-step ks an activation lane holds the 16 bytes of
+// a[m0 + j] at byte 64 ks + 16 q of the stage, a weight lane those of W[n0 + j]; fp16 feeds
+// them to one 16x16x32 MFMA (k = 32 ks + 8 q .. + 7), fp32 to four 16x16x4 MFMAs (the e-th
+// takes element e of both, so the four cover the k-step's 16 columns once each).  With the
+// weights as the MFMA's A operand the accumulator lane holds y[m0 + j][n0 + 4 q + r],
 // r = 0..3.
 #include "mx_common.h"
 #include "mx_internal.h"
@@ -72,35 +75,41 @@ struct GemmArgs {
   GemmSeg seg[MX_GEMM_MAX_SEG];
 };
 
-constexpr int STAGE_BYTES = 64;  // bytes of each row per stage (16 B per lane quarter)
-#ifndef MX_GEMM_NS
-#define MX_GEMM_NS 4  // stage slots in the LDS ring
-#endif
-// Operand fragments read one stage ahead (fp16 256 x 256 tiles; the 128 x 128 tiles at two
-// blocks per CU lose with it: out projection 89 -> 92 us, against qkvz + ba 410 -> 401 us).
-#ifndef MX_GEMM_PF
-#define MX_GEMM_PF 1
-#endif
+constexpr int STAGE_BYTES = MX_GEMM_STAGE_BYTES;  // bytes of each row per stage
+constexpr int KSTEPS = STAGE_BYTES / 64;           // MFMA k-steps of 64 bytes per stage
+constexpr int FRAG_ROWS = 1024 / STAGE_BYTES;      // rows per 1 KiB copy fragment
+constexpr int BLK16 = 16 * STAGE_BYTES;            // bytes of a 16-row operand block per stage
+static_assert(STAGE_BYTES == 128, "the copy and read maps below are for 128-byte rows");
 #ifndef MX_GEMM_GM
 #define MX_GEMM_GM 4  // row blocks per group of the block order (0: one column block at a time)
 #endif
 
-
+// Copy lane l of a fragment loads row l / 8 of it, 16-byte chunk (l % 8) ^ (l / 8), so
+// every 8 consecutive lanes read one row's 128 contiguous bytes and the chunk c of row r
+// lands in slot c ^ r of the row's 128 bytes in LDS.  The operand read of lane (j, q) at
+// k-step ks (row j of a 16-row block, chunk 4 ks + q) is then free of bank conflicts on
+// gfx950 (SQ_LDS_BANK_CONFLICT 0 with a read-only probe; without the XOR the 16-byte reads
+// of a wave take four times the LDS cycles).
+__device__ __forceinline__ int gemm_copy_chunk(int l) { return (l & 7) ^ (l >> 3); }
+__device__ __forceinline__ int gemm_read_pos(int j, int q, int ks) {
+  return (j >> 3) * 1024 + (j & 7) * 128 + ((((ks << 2) + q) ^ (j & 7)) << 4);
+}
 
 template <typename ET, bool SPLIT, int BM, int BN, int WM, int WN, int NS, int OCC>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, OCC) void k_gemm_nt(
     const GemmArgs p) {
   constexpr int ES = sizeof(ET);
-  constexpr int BKE = STAGE_BYTES / ES;           // reduction columns per stage
   constexpr int NWN = BN / WN, NW = (BM / WM) * NWN;
   constexpr int MF = WM / 16, NF = WN / 16;
   constexpr int PL = SPLIT ? 2 : 1;               // planes per operand
-  constexpr int FA1 = BM / 16, FB1 = BN / 16;     // fragments per plane and stage
+  constexpr int FA1 = BM / FRAG_ROWS, FB1 = BN / FRAG_ROWS;  // fragments per plane and stage
   constexpr int FA = PL * FA1, FT = FA + PL * FB1;  // fragments per stage slot: A planes, B planes
   constexpr int SLOT = FT * 1024;
+  constexpr int PA = BM * STAGE_BYTES, PB = BN * STAGE_BYTES;  // bytes of one plane per slot
   constexpr int DPW = FT / NW;                    // copies per wave and stage
   static_assert(!SPLIT || ES == 2, "split planes are fp16");
   static_assert(FA1 % NW == 0 && FB1 % NW == 0, "fragments must divide among the waves");
+  static_assert(NS >= 2, "a stage ring of at least two slots");
   __shared__ __align__(1024) char lds[NS * SLOT];
 
   // Blocks are numbered so that consecutive logical ids run on one XCD (hardware block b
@@ -159,27 +168,22 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, OCC) void k_gemm_nt(
   };
   // The fragments this wave copies: f = wave + i * NW (A fragments first, then B); the
   // lane's source row and its byte offset at stage 0.
-  // Copy lane l loads row cr = l / 4 of its fragment, 16-byte chunk mx_frag_copy_chunk(l),
-  // so every 4 consecutive lanes read one row's 64 contiguous bytes (the address unit
-  // merges them); the chunk rotation (mx_lds_copy.h) makes the MFMA operand reads below
-  // (lane (j, q) reads row j, chunk q at mx_frag_read_pos(j, q)) free of bank conflicts.
-  const int cr = lane >> 2, cq = mx_frag_copy_chunk(lane);
-  const int rpos = mx_frag_read_pos(j, q);
+  const int cr = lane >> 3, cq = gemm_copy_chunk(lane);
   uint32_t goff[DPW];
 #pragma unroll
   for (int i = 0; i < DPW; ++i) {
     const int f = wave + i * NW;
     if (i * NW < FA) {
-      const int row = m0 + 16 * (f % FA1) + cr;
+      const int row = m0 + FRAG_ROWS * (f % FA1) + cr;
       goff[i] = row < M ? ((uint32_t)row * (uint32_t)K + k0) * ES + cq * 16 : kOob;
     } else {
-      const int row = n0 + 16 * ((f - FA) % FB1) + cr;
+      const int row = n0 + FRAG_ROWS * ((f - FA) % FB1) + cr;
       goff[i] = row < N ? ((uint32_t)row * (uint32_t)K + k0) * ES + cq * 16 : kOob;
     }
   }
-  // K and the slice length are multiples of BKE, so every piece of a stage lies inside its
-  // row; rows past M / N have offsets at or above kOob, which stay past the end of the
-  // descriptor.
+  // K and the slice length are multiples of the stage width, so every piece of a stage lies
+  // inside its row; rows past M / N have offsets at or above kOob, which stay past the end
+  // of the descriptor.
   auto issue = [&](int st) {
     char* slot = lds + (st % NS) * SLOT;
 #pragma unroll
@@ -204,62 +208,14 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, OCC) void k_gemm_nt(
 #pragma unroll
       for (int ni = 0; ni < NF; ++ni) acc2[mi][ni] = (float4_t){0.f, 0.f, 0.f, 0.f};
   }
+  int rpos[KSTEPS];
+#pragma unroll
+  for (int ks = 0; ks < KSTEPS; ++ks) rpos[ks] = gemm_read_pos(j, q, ks);
 
-  const int nst = kn / BKE;
+  const int nst = kn / (STAGE_BYTES / ES);
 #pragma unroll
   for (int s0 = 0; s0 < NS - 1; ++s0)
     if (s0 < nst) issue(s0);
-  if constexpr (!SPLIT && ES == 2 && MX_GEMM_PF && BM == 256) {
-    // Fragments one stage ahead: stage st + 1's operand fragments are read from LDS while
-    // stage st's MFMAs run (two register sets, alternating), so no stage starts with the
-    // MFMA pipe waiting on LDS reads after its barrier.  Stage st + 1's copies must have
-    // landed before that read: the barrier of iteration st waits for them, leaving the
-    // copies of the stages after st + 1 in flight.  The slot the copies of iteration st
-    // overwrite held stage st - 1, whose fragments every wave consumed in iteration st - 1.
-    auto wait_landed = [&](int ahead) {  // ahead: stages issued after the awaited one
-      if (ahead >= 2) mx_wait_copies_and_barrier<2 * DPW>();
-      else if (ahead == 1) mx_wait_copies_and_barrier<DPW>();
-      else mx_wait_copies_and_barrier<0>();
-    };
-    auto read_frags = [&](int st, int4_t (&af)[MF], int4_t (&bf)[NF]) {
-      const char* slot = lds + (st % NS) * SLOT;
-#pragma unroll
-      for (int ni = 0; ni < NF; ++ni)
-        bf[ni] = *(const int4_t*)(slot + (FA + wn * NF + ni) * 1024 + rpos);
-#pragma unroll
-      for (int mi = 0; mi < MF; ++mi)
-        af[mi] = *(const int4_t*)(slot + (wm * MF + mi) * 1024 + rpos);
-    };
-    auto mfmas = [&](const int4_t (&af)[MF], const int4_t (&bf)[NF]) {
-#pragma unroll
-      for (int mi = 0; mi < MF; ++mi)
-#pragma unroll
-        for (int ni = 0; ni < NF; ++ni)
-          acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-              __builtin_bit_cast(half8_t, bf[ni]), __builtin_bit_cast(half8_t, af[mi]),
-              acc[mi][ni], 0, 0, 0);
-    };
-    // Every step waits, meets the barrier and reads (the last one reads a slot whose copies
-    // have all landed and whose fragments nobody uses), so the LDS-read counter is in the
-    // same state on every path and the MFMAs wait only for the older fragment set.
-    auto step = [&](int st, const int4_t (&ca)[MF], const int4_t (&cb)[NF], int4_t (&na)[MF],
-                    int4_t (&nb)[NF]) {
-      wait_landed(min(NS - 3, nst - st - 2));
-      if (st + NS - 1 < nst) issue(st + NS - 1);
-      read_frags(st + 1, na, nb);
-      __builtin_amdgcn_sched_barrier(0);  // the reads go out before the MFMAs
-      mfmas(ca, cb);
-    };
-    int4_t fa0[MF], fb0[NF], fa1[MF], fb1[NF];
-    if (nst > 0) {
-      wait_landed(min(NS - 2, nst - 1));
-      read_frags(0, fa0, fb0);
-    }
-    for (int st = 0; st < nst; st += 2) {
-      step(st, fa0, fb0, fa1, fb1);
-      if (st + 1 < nst) step(st + 1, fa1, fb1, fa0, fb0);
-    }
-  } else
   for (int st = 0; st < nst; ++st) {
     // This wave's copies of stage st are done (the NS - 2 later stages may still be in
     // flight), then every wave's are, and every wave has finished computing stage st - 1,
@@ -270,50 +226,55 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, OCC) void k_gemm_nt(
       mx_wait_copies_and_barrier<0>();
     if (st + NS - 1 < nst) issue(st + NS - 1);
     const char* slot = lds + (st % NS) * SLOT;
-    int4_t af[MF], bf[NF];
 #pragma unroll
-    for (int mi = 0; mi < MF; ++mi) af[mi] = *(const int4_t*)(slot + (wm * MF + mi) * 1024 + rpos);
-#pragma unroll
-    for (int ni = 0; ni < NF; ++ni)
-      bf[ni] = *(const int4_t*)(slot + (FA + wn * NF + ni) * 1024 + rpos);
-    if constexpr (SPLIT) {
-      int4_t afl[MF], bfl[NF];
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      int4_t af[MF], bf[NF];
 #pragma unroll
       for (int mi = 0; mi < MF; ++mi)
-        afl[mi] = *(const int4_t*)(slot + (FA1 + wm * MF + mi) * 1024 + rpos);
+        af[mi] = *(const int4_t*)(slot + (wm * MF + mi) * BLK16 + rpos[ks]);
 #pragma unroll
       for (int ni = 0; ni < NF; ++ni)
-        bfl[ni] = *(const int4_t*)(slot + (FA + FB1 + wn * NF + ni) * 1024 + rpos);
+        bf[ni] = *(const int4_t*)(slot + PL * PA + (wn * NF + ni) * BLK16 + rpos[ks]);
+      if constexpr (SPLIT) {
+        int4_t afl[MF], bfl[NF];
 #pragma unroll
-      for (int mi = 0; mi < MF; ++mi)
+        for (int mi = 0; mi < MF; ++mi)
+          afl[mi] = *(const int4_t*)(slot + PA + (wm * MF + mi) * BLK16 + rpos[ks]);
 #pragma unroll
-        for (int ni = 0; ni < NF; ++ni) {
-          const half8_t ah = __builtin_bit_cast(half8_t, af[mi]);
-          const half8_t bh = __builtin_bit_cast(half8_t, bf[ni]);
-          acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bh, ah, acc[mi][ni], 0, 0, 0);
-          acc2[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-              __builtin_bit_cast(half8_t, bfl[ni]), ah, acc2[mi][ni], 0, 0, 0);
-          acc2[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-              bh, __builtin_bit_cast(half8_t, afl[mi]), acc2[mi][ni], 0, 0, 0);
-        }
-      continue;
-    }
+        for (int ni = 0; ni < NF; ++ni)
+          bfl[ni] = *(const int4_t*)(slot + 2 * PA + PB + (wn * NF + ni) * BLK16 + rpos[ks]);
 #pragma unroll
-    for (int mi = 0; mi < MF; ++mi)
+        for (int mi = 0; mi < MF; ++mi)
 #pragma unroll
-      for (int ni = 0; ni < NF; ++ni) {
-        if constexpr (ES == 2) {
-          acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-              __builtin_bit_cast(half8_t, bf[ni]), __builtin_bit_cast(half8_t, af[mi]),
-              acc[mi][ni], 0, 0, 0);
-        } else {
-          const float4_t av = __builtin_bit_cast(float4_t, af[mi]);
-          const float4_t bv = __builtin_bit_cast(float4_t, bf[ni]);
+          for (int ni = 0; ni < NF; ++ni) {
+            const half8_t ah = __builtin_bit_cast(half8_t, af[mi]);
+            const half8_t bh = __builtin_bit_cast(half8_t, bf[ni]);
+            acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bh, ah, acc[mi][ni], 0, 0, 0);
+            acc2[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                __builtin_bit_cast(half8_t, bfl[ni]), ah, acc2[mi][ni], 0, 0, 0);
+            acc2[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                bh, __builtin_bit_cast(half8_t, afl[mi]), acc2[mi][ni], 0, 0, 0);
+          }
+      } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[e], av[e], acc[mi][ni], 0, 0, 0);
-        }
+        for (int mi = 0; mi < MF; ++mi)
+#pragma unroll
+          for (int ni = 0; ni < NF; ++ni) {
+            if constexpr (ES == 2) {
+              acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                  __builtin_bit_cast(half8_t, bf[ni]), __builtin_bit_cast(half8_t, af[mi]),
+                  acc[mi][ni], 0, 0, 0);
+            } else {
+              const float4_t av = __builtin_bit_cast(float4_t, af[mi]);
+              const float4_t bv = __builtin_bit_cast(float4_t, bf[ni]);
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                acc[mi][ni] =
+                    __builtin_amdgcn_mfma_f32_16x16x4f32(bv[e], av[e], acc[mi][ni], 0, 0, 0);
+            }
+          }
       }
+    }
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);  // no copy into LDS outlives the block (vmcnt 0)
   if constexpr (SPLIT) {
@@ -332,6 +293,32 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, OCC) void k_gemm_nt(
   float* const ybase = sg.y + (size_t)blockIdx.y * p.yslice;
   const bool vec = (sg.ldy & 3) == 0 && ((uintptr_t)ybase & 15) == 0 &&
                    ((uintptr_t)sg.res & 15) == 0;
+  // Rows whose stride or base rules out 16-byte stores (the router logits, E + 1 columns):
+  // the tile goes through LDS, then consecutive lanes store consecutive columns of a row,
+  // in place of 4-byte stores spread over 16 rows per instruction.
+  constexpr int LDT = BN + 4;  // row stride of the staged tile (floats)
+  if constexpr (BM * LDT * 4 <= NS * SLOT) {
+    if (!vec) {
+      __syncthreads();  // every wave is past its last read of the ring
+      float* so = (float*)lds;
+#pragma unroll
+      for (int mi = 0; mi < MF; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < NF; ++ni)
+          *(float4_t*)(so + (wm * WM + mi * 16 + j) * LDT + wn * WN + ni * 16 + 4 * q) =
+              acc[mi][ni];
+      __syncthreads();
+      for (int idx = threadIdx.x; idx < BM * BN; idx += NW * 64) {
+        const int row = idx / BN, col = idx - row * BN;
+        const int m = m0 + row, n = n0 + col;
+        if (m < M && n < N) {
+          const size_t o = (size_t)m * sg.ldy + n;
+          ybase[o] = sg.res ? sg.res[o] + so[row * LDT + col] : so[row * LDT + col];
+        }
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int mi = 0; mi < MF; ++mi) {
     const int m = m0 + wm * WM + mi * 16 + j;
@@ -425,8 +412,8 @@ int mx_gemm_f16(const void* a, int M, int K, const MxGemmSeg* segs, int nseg, hi
     long mid = 0;
     for (int i = 0; i < nseg; ++i) mid += (long)mx_ceil_div(M, 256) * mx_ceil_div(segs[i].n, 128);
     if (MX_GEMM_MID && mid >= 256 && mid % 256 == 0)
-      return launch<half_t, false, 256, 128, 64, 64, MX_GEMM_NS, 1>(args, segs, nseg, 1, s);
-    return launch<half_t, false, 128, 128, 64, 64, MX_GEMM_NS, 2>(args, segs, nseg, 1, s);
+      return launch<half_t, false, 256, 128, 64, 64, 3, 1>(args, segs, nseg, 1, s);
+    return launch<half_t, false, 128, 128, 64, 64, 2, 2>(args, segs, nseg, 1, s);
   }
   if (MX_GEMM_TAIL && big % 256) {
     // One 256 x 256 block per CU: the blocks past the last whole round would run as a
@@ -459,11 +446,11 @@ int mx_gemm_f16(const void* a, int M, int K, const MxGemmSeg* segs, int nseg, hi
       GemmArgs ah, at;
       MX_TRY(prepare(ah, a, M, K, 2, head, nh, K, 0));
       MX_TRY(prepare(at, a, M, K, 2, tail, nt, K, 0));
-      MX_TRY((launch<half_t, false, 256, 256, 128, 64, MX_GEMM_NS, 1>(ah, head, nh, 1, s)));
-      return launch<half_t, false, 128, 128, 64, 64, MX_GEMM_NS, 2>(at, tail, nt, 1, s);
+      MX_TRY((launch<half_t, false, 256, 256, 128, 64, 2, 1>(ah, head, nh, 1, s)));
+      return launch<half_t, false, 128, 128, 64, 64, 2, 2>(at, tail, nt, 1, s);
     }
   }
-  return launch<half_t, false, 256, 256, 128, 64, MX_GEMM_NS, 1>(args, segs, nseg, 1, s);
+  return launch<half_t, false, 256, 256, 128, 64, 2, 1>(args, segs, nseg, 1, s);
 }
 
 int mx_gemm_f32_slices(const float* a, int M, int K, const MxGemmSeg* segs, int nseg,
@@ -472,7 +459,7 @@ int mx_gemm_f32_slices(const float* a, int M, int K, const MxGemmSeg* segs, int 
   MX_TRY(prepare(args, a, M, K, 4, segs, nseg, kslice, yslice));
   const int splits = mx_ceil_div(K, kslice);
   if (splits > 1 && yslice <= 0) return MX_ERR_INVALID;
-  return launch<float, false, 128, 128, 64, 64, MX_GEMM_NS, 2>(args, segs, nseg, splits, s);
+  return launch<float, false, 128, 128, 64, 64, 2, 2>(args, segs, nseg, splits, s);
 }
 
 int mx_gemm_f16x2_slices(const void* a_hi, const void* a_lo, int M, int K, const MxGemmSeg* segs,
@@ -487,6 +474,7 @@ int mx_gemm_f16x2_slices(const void* a_hi, const void* a_lo, int M, int K, const
   args.a_lo = a_lo;
   const int splits = mx_ceil_div(K, kslice);
   if (splits > 1 && yslice <= 0) return MX_ERR_INVALID;
-  // 256 x 128 tiles of 8 waves, one block per CU (three 48 KiB stage slots).
-  return launch<half_t, true, MX_GEMM_SPLIT_BM, 128, 64, 64, 3, 1>(args, segs, nseg, splits, s);
+  // 128 x 128 tiles of 8 waves (64 x 32 each), one block per CU (two 64 KiB stage slots).
+  return launch<half_t, true, MX_GEMM_SPLIT_BM, MX_GEMM_SPLIT_BN, 64, 32, 2, 1>(args, segs, nseg,
+                                                                               splits, s);
 }

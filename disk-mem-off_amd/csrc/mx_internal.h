@@ -18,8 +18,9 @@ size_t mx_router_split_bytes(int hidden, int e1);
 int mx_router_logits_split(const void* h16, const void* h16lo, const void* router_w,
                            const void* shared_gate_w, int param_dtype, int tokens, int hidden,
                            int n_experts, int splits, void* wsplit, float* logits, hipStream_t s);
-// Rows per block of mx_gemm_f16x2_slices.
-#define MX_GEMM_SPLIT_BM 256
+// Rows and columns per block of mx_gemm_f16x2_slices.
+#define MX_GEMM_SPLIT_BM 128
+#define MX_GEMM_SPLIT_BN 128
 
 // Upper bound of the m-tile list for `tokens` tokens at m_blk rows per tile.
 int mx_max_mtiles(int tokens, int top_k, int n_experts, int has_shared, int m_blk);
@@ -125,8 +126,13 @@ int mx_dense_linear(int wdt, int tiled, const MxExpertPtrs* entry, const MxDense
                     int T, int N, int K, const void* a, float* y, hipStream_t s);
 
 // Dense GEMM on MFMA (mx_dense_gemm.hip): y_s[M, N_s] (fp32, row stride ldy_s) =
-// a[M, K] W_s[N_s, K]^T for up to MX_GEMM_MAX_SEG weight matrices sharing a.
+// a[M, K] W_s[N_s, K]^T for up to MX_GEMM_MAX_SEG weight matrices sharing a.  The reduction
+// runs in stages of MX_GEMM_STAGE_BYTES per row, so K (and a slice length) must be a
+// multiple of MX_GEMM_KMULT_F16 columns for fp16 operands, MX_GEMM_KMULT_F32 for fp32.
 #define MX_GEMM_MAX_SEG 3
+#define MX_GEMM_STAGE_BYTES 128
+#define MX_GEMM_KMULT_F16 (MX_GEMM_STAGE_BYTES / 2)
+#define MX_GEMM_KMULT_F32 (MX_GEMM_STAGE_BYTES / 4)
 struct MxGemmSeg {
   const void* w;  // [n, K] row-major (16-byte aligned), element type of a
   float* y;       // [M, ldy] fp32
@@ -138,12 +144,12 @@ struct MxGemmSeg {
 // fp16 a and W.
 int mx_gemm_f16(const void* a, int M, int K, const MxGemmSeg* segs, int nseg, hipStream_t s);
 // fp32 a and W, full fp32 products; the reduction is cut into slices of kslice columns
-// (a multiple of 16) and slice z writes its partial sums at y_s + z * yslice.
+// (a multiple of MX_GEMM_KMULT_F32) and slice z writes its partial sums at y_s + z * yslice.
 int mx_gemm_f32_slices(const float* a, int M, int K, const MxGemmSeg* segs, int nseg,
                        int kslice, long yslice, hipStream_t s);
 // fp32 operands as two fp16 planes each, x = hi + 2^-11 lo (hi = fp16(x), lo = fp16((x -
 // hi) 2^11)): y = a_hi w_hi + 2^-11 (a_hi w_lo + a_lo w_hi), fp32 sums; kslice a multiple
-// of 32, slices as mx_gemm_f32_slices.
+// of MX_GEMM_KMULT_F16, slices as mx_gemm_f32_slices.
 int mx_gemm_f16x2_slices(const void* a_hi, const void* a_lo, int M, int K, const MxGemmSeg* segs,
                          int nseg, int kslice, long yslice, hipStream_t s);
 
@@ -168,9 +174,9 @@ void mx_dense_work_carve(char* base, int T, int weight_dtype, int n_ent, MxDense
 // Writes the table entries and m-tile tables (one small launch per block call).
 int mx_dense_setup(const MxDenseWork& w, const MxDenseEntries& ents, int T, hipStream_t s);
 // Whether projections of T tokens with these weights and reduction length K run on
-// mx_gemm_f16 (fp16 weights, long inputs, K a multiple of its 32-column stage).
+// mx_gemm_f16 (fp16 weights, long inputs, K a multiple of its stage width).
 static inline bool mx_dense_on_gemm(int wdt, int T, int K) {
-  return wdt == MX_DT_F16 && T >= MX_DENSE_GEMM_MIN_TOKENS && K % 32 == 0;
+  return wdt == MX_DT_F16 && T >= MX_DENSE_GEMM_MIN_TOKENS && K % MX_GEMM_KMULT_F16 == 0;
 }
 // y[T, N] = a[T, K] W^T with W = projection `ent` (wmat, its weights, for mx_gemm_f16).
 int mx_project(const MxDenseWork& w, int ent, int wdt, const void* wmat, int T, int N, int K,

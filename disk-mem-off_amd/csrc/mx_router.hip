@@ -372,18 +372,19 @@ k_router_logits(const float* __restrict__ h32, const WT* __restrict__ wr,
 #define RT_SPLIT_ROUTED 1  // split-plane slice count from the routed rows' tiles
 #endif
 static bool router_on_gemm(int tokens, int hidden, int e1, int param_dtype) {
-  return param_dtype == MX_DT_F32 && tokens >= RT_GEMM_MIN_TOKENS && hidden % 16 == 0 &&
+  return param_dtype == MX_DT_F32 && tokens >= RT_GEMM_MIN_TOKENS && hidden % MX_GEMM_KMULT_F32 == 0 &&
          (long)tokens * hidden * 4 < (1l << 31) && (long)e1 * hidden * 4 < (1l << 31);
 }
 bool mx_router_on_split(int tokens, int hidden, int e1, int weight_dtype) {
   return RT_USE_SPLIT && weight_dtype != MX_DT_F32 && tokens >= RT_GEMM_MIN_TOKENS &&
-         hidden % 32 == 0 && (long)tokens * hidden * 2 < (1l << 31) &&
+         hidden % MX_GEMM_KMULT_F16 == 0 && (long)tokens * hidden * 2 < (1l << 31) &&
          (long)e1 * hidden * 2 < (1l << 31);
 }
 
 // Number of H-slices the router uses for T tokens (a pure function of the shape), at most
-// 16 and at most one per RT_KCH columns (k_router_logits), per 16 columns (RT_GEMM32) or
-// per 32 columns (RT_SPLIT; weight_dtype < 0: outside the MoE block, no split planes).
+// 16 and at most one per RT_KCH columns (k_router_logits) or per GEMM stage width
+// (MX_GEMM_KMULT_F32 columns on the fp32 GEMM, MX_GEMM_KMULT_F16 on the split-plane GEMM;
+// weight_dtype < 0: outside the MoE block, no split planes).
 int mx_router_splits_for(int tokens, int hidden, int n_experts, int has_shared_gate,
                          int param_dtype, int weight_dtype) {
   const int t = tokens > 0 ? tokens : 1;
@@ -393,18 +394,18 @@ int mx_router_splits_for(int tokens, int hidden, int n_experts, int has_shared_g
   if (weight_dtype >= 0 && mx_router_on_split(t, hidden, e1, weight_dtype)) {
     // Largest slice count whose blocks fit one round at one block per CU.  The GEMM covers
     // the routed rows only (the RMSNorm launch computes the shared-expert gate logit).
-    // Qwen3-Next, 4096 tokens: 16 x 4 tiles x 4 slices; GLM-4.7, 2048 tokens: 8 x 2 x 16.
+    // Qwen3-Next, 4096 tokens: 32 x 4 tiles x 2 slices; GLM-4.7, 2048 tokens: 16 x 2 x 8.
     const int cols = RT_SPLIT_ROUTED ? n_experts : e1;
-    tiles = (long)mx_ceil_div(t, MX_GEMM_SPLIT_BM) * mx_ceil_div(cols, 128);
+    tiles = (long)mx_ceil_div(t, MX_GEMM_SPLIT_BM) * mx_ceil_div(cols, MX_GEMM_SPLIT_BN);
     fill = RT_SPLIT_FILL;
-    kch = hidden / 32;
+    kch = hidden / MX_GEMM_KMULT_F16;
   } else if (router_on_gemm(t, hidden, e1, param_dtype)) {
     // Largest slice count whose blocks fit one round at two blocks per CU.  Qwen3-Next,
     // 4096 tokens: 32 x (4 + 1) tiles x 3 slices; GLM-4.7, 2048 tokens: 16 x 2 x 16.
     tiles = (long)mx_ceil_div(t, 128) *
             (mx_ceil_div(n_experts, 128) + (has_shared_gate ? 1 : 0));
     fill = 512;
-    kch = hidden / 16;
+    kch = hidden / MX_GEMM_KMULT_F32;
   } else {
     // Largest slice count whose blocks fit one round at 4 waves per SIMD (1024 blocks of 4
     // waves on 256 CUs).
@@ -453,7 +454,7 @@ int mx_router_logits_split(const void* h16, const void* h16lo, const void* route
     return MX_ERR_INVALID;
   const int e1 = n_experts + (shared_gate_w ? 1 : 0);
   if (!mx_router_on_split(tokens, hidden, e1, MX_DT_F16)) return MX_ERR_UNSUPPORTED;
-  const int kslice = mx_ceil_div(hidden / 32, splits) * 32;
+  const int kslice = mx_ceil_div(hidden / MX_GEMM_KMULT_F16, splits) * MX_GEMM_KMULT_F16;
   if (mx_ceil_div(hidden, kslice) != splits) return MX_ERR_INVALID;
   const MxRouterSplitW r = mx_router_split_planes(router_w, shared_gate_w, param_dtype,
                                                   n_experts, hidden, tokens, splits, wsplit,
@@ -481,7 +482,7 @@ extern "C" int mx_router_logits(const float* h32, const void* router_w, const vo
   const int e1 = n_experts + (shared_gate_w ? 1 : 0);
   hipStream_t s = (hipStream_t)stream;
   if (router_on_gemm(tokens, hidden, e1, param_dtype)) {
-    const int kslice = mx_ceil_div(hidden / 16, splits) * 16;
+    const int kslice = mx_ceil_div(hidden / MX_GEMM_KMULT_F32, splits) * MX_GEMM_KMULT_F32;
     if (mx_ceil_div(hidden, kslice) != splits) return MX_ERR_INVALID;
     const MxGemmSeg g[2] = {{router_w, logits, n_experts, e1},
                             {shared_gate_w, logits + n_experts, 1, e1}};
