@@ -113,7 +113,7 @@ typedef struct MxMoeWeights {
 typedef struct MxMoeViews {
   float* h32;          /* [T, H] rms-normalised activations; not written by a forward   */
                        /* whose router runs on fp16 planes (T >= 65, fp16 / int8        */
-                       /* experts, H a multiple of 32): h16 holds them there            */
+                       /* experts, H a multiple of 64): h16 holds them there            */
   void* h16;           /* [T, H] fp16 copy (NULL for MX_DT_F32 weights)                 */
   float* logits;       /* [S, T, E(+1)] router logit partials (S = router_splits)        */
   int32_t router_splits;
@@ -364,7 +364,7 @@ typedef struct MxLinearAttnViews {
 } MxLinearAttnViews;
 
 /* Stages: rmsnorm, qkvz, ba, conv+gates, scan, gated norm, out, residual.  With fp16
- * weights, T >= 65 and H (for qkvz / ba) or n dv (for out) a multiple of 32 the
+ * weights, T >= 65 and H (for qkvz / ba) or n dv (for out) a multiple of 64 the
  * projections run on the dense MFMA GEMM: ba is computed in the qkvz launch (stage 2 is
  * then empty, and the _profiled events report ba's time under qkvz), and out = x +
  * act W_out^T is formed in the out launch's epilogue (stage 7 is empty and the view y is
@@ -434,7 +434,7 @@ typedef struct MxFullAttnViews {
 } MxFullAttnViews;
 
 /* Stages: rmsnorm, q, k, v, qk-norm+rope, attention, o, residual.  With fp16 weights,
- * T >= 65 and H (for q / k / v) or n_heads head_dim (for o) a multiple of 32 the
+ * T >= 65 and H (for q / k / v) or n_heads head_dim (for o) a multiple of 64 the
  * projections run on the dense MFMA GEMM: k and v are computed in the q launch (stages 2
  * and 3 are then empty, and the _profiled events report their time under q), and out =
  * x + act W_o^T is formed in the o launch's epilogue (stage 7 is empty and the view y is
